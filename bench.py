@@ -1,0 +1,235 @@
+"""WKV7 benchmark on one MI355X (driver contract: one JSON line on stdout).
+
+Default workload: batched decode, B=256 sequences, H=40
+heads, D=64, T=1 per step, bf16 token io, fp32 state pool [256,40,64,64]
+updated in place, S0 ~ N(0, 0.1), retention w = exp(-exp(u)), u ~ U(-5,0)
+(raw-retention mode). One step = one launch over the whole batch.
+
+Cache-cold measurement: the 167.8 MB pool fits MI355X's 256 MB Infinity
+Cache, so consecutive in-place steps on one pool can read state from the
+cache. The timed loop therefore rotates over 4 pool replicas (671 MB) and 8
+token sets; step i uses replica i % 4, which keeps every step's state traffic
+on HBM. The in-place single-pool rate is reported beside it.
+
+Steps are replayed from HIP graphs (one captured graph per rotation
+position), so host launch overhead is not on the timed path. HIP events on
+the launch stream bracket the timed region; the average launch duration is
+elapsed / steps.
+
+Other workloads (--workload prefill | recurrent_long | varlen) time the
+chunked/long-sequence paths for the reports; the driver uses the default.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6
+METRIC = "WKV7 tokens/s + % roofline (HBM GB/s decode, MFMA TFLOP/s chunked), h32d64"
+
+
+def _parse():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=1000)
+    p.add_argument("--warmup", type=int, default=50)
+    p.add_argument("--workload", default="decode",
+                   choices=("decode",))
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="bound on the CPU-baseline sample (0 disables it)")
+    return p.parse_args()
+
+
+def decode_bytes_per_step(batch: int, heads: int, d: int = 64, io_bytes: int = 2) -> int:
+    """Algorithmic HBM bytes of one decode launch.
+
+    Per (sequence, head): state read + write 2*D*D*4 B, six token rows
+    (r, w, k, v, a, b) 6*D*io_bytes, one output row D*io_bytes.
+    """
+    per_unit = 2 * d * d * 4 + 7 * d * io_bytes
+    return batch * heads * per_unit
+
+
+def cpu_baseline_decode(batch, heads, seconds):
+    """Times the fp64 C oracle (the restated reference recurrence) on host cores."""
+    import numpy as np
+    import torch
+
+    from flashrwkv_amd import workloads
+    from oracle import oracle
+
+    cores = len(os.sched_getaffinity(0))
+    case = workloads.make_case(lengths=[1] * batch, heads=heads, head_size=64,
+                               dtype=torch.bfloat16, seed=99, state_std=0.1)
+    args = [case[n].double().numpy() for n in ("r", "w", "k", "v", "a", "b")]
+    pool = case["state_pool"].double().numpy()
+    cu = case["cu_seqlens"].numpy()
+    slots = case["state_indices"].numpy()
+    oracle.forward_varlen(*args, pool, cu, slots, num_threads=cores)  # warm-up
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        _, pool = oracle.forward_varlen(*args, pool, cu, slots, num_threads=cores)
+        steps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            break
+    return {
+        "value": steps * batch / elapsed,
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{steps} decode steps of B={batch}, H={heads}, D=64 through the fp64 C "
+                  f"oracle (oracle/wkv7_oracle.c), OpenMP over (sequence, head), "
+                  f"{elapsed:.1f} s",
+    }
+
+
+def bench_decode(args):
+    import torch
+
+    import flashrwkv_amd
+    from flashrwkv_amd import workloads
+    from flashrwkv_amd.tmix.wkv7 import DECAY_RAW_W, prepare_recurrent_metadata
+
+    if flashrwkv_amd._C is None:
+        raise SystemExit("flashrwkv_amd native library is not built")
+    ops = flashrwkv_amd._C.ops
+    dev = torch.device("cuda:0")
+    batch, heads, d = 256, 40, 64
+    n_pools, n_tokens = 4, 8
+
+    gen = torch.Generator(device=dev).manual_seed(20260805)
+    pools = [torch.randn((batch, heads, d, d), generator=gen, device=dev) * 0.1
+             for _ in range(n_pools)]
+    token_sets = [workloads.make_tokens(batch, heads, d, dtype=torch.bfloat16,
+                                       seed=20260805 + i, device=dev)
+                  for i in range(n_tokens)]
+    outputs = [torch.empty((batch, heads, d), device=dev, dtype=torch.bfloat16)
+               for _ in range(n_tokens)]
+    cu = torch.arange(batch + 1, device=dev, dtype=torch.int32)
+    slots = torch.arange(batch, device=dev, dtype=torch.int32)
+
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        ticket = prepare_recurrent_metadata(cu, slots, total_tokens=batch,
+                                            state_pool_size=batch, max_seqlen=1)
+
+        def step(i, pool=None):
+            t = token_sets[i % n_tokens]
+            ops.recurrent_fp32_forward_internal(
+                cu, slots, pools[i % n_pools] if pool is None else pool,
+                t["r"], t["w"], t["k"], t["v"], t["a"], t["b"],
+                outputs[i % n_tokens], 1.0, DECAY_RAW_W, None, ticket, 1)
+
+        for i in range(max(args.warmup, 8)):
+            step(i)
+        stream.synchronize()
+        cycle = 8  # lcm(n_pools, n_tokens)
+        graphs = []
+        for i in range(cycle):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                step(i)
+            graphs.append(g)
+        for i in range(args.warmup):
+            graphs[i % cycle].replay()
+        stream.synchronize()
+
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        wall0 = time.perf_counter()
+        start.record(stream)
+        for i in range(args.steps):
+            graphs[i % cycle].replay()
+        end.record(stream)
+        end.synchronize()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - wall0
+        cold_ms = start.elapsed_time(end) / args.steps
+
+        # In-place variant: one pool, the literal "consecutive steps" of the config.
+        inplace_graphs = []
+        for i in range(n_tokens):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                step(i, pool=pools[0])
+            inplace_graphs.append(g)
+        for i in range(args.warmup):
+            inplace_graphs[i % n_tokens].replay()
+        start.record(stream)
+        for i in range(args.steps):
+            inplace_graphs[i % n_tokens].replay()
+        end.record(stream)
+        end.synchronize()
+        inplace_ms = start.elapsed_time(end) / args.steps
+
+    nbytes = decode_bytes_per_step(batch, heads, d)
+    achieved = nbytes / (cold_ms * 1e-3) / 1e9
+    tok_s = batch / (cold_ms * 1e-3)
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(cold_ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded; BASELINE config 1 distributions)",
+        "config": {
+            "workload": "wkv7_decode_cfg1: B=256, H=40, D=64, T=1 per step, bf16 io, "
+                        "fp32 state pool in place, raw retention, 4 rotating pool "
+                        "replicas (cache-cold)",
+            "batch": batch, "heads": heads, "head_size": d, "io_dtype": "bf16",
+            "state_dtype": "fp32", "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "kernel": "recurrent_fp32_kernel<64,64,Bf16,kRawW>",
+            "algorithmic_bytes_per_launch": nbytes,
+        },
+        "inplace_single_pool": {
+            "ms_per_step": round(inplace_ms, 6),
+            "tokens_per_s": round(batch / (inplace_ms * 1e-3), 1),
+            "achieved_GBps": round(nbytes / (inplace_ms * 1e-3) / 1e9, 1),
+        },
+        "wall_s_timed_region": round(wall, 4),
+    }
+    if args.cpu_seconds > 0:
+        line["cpu_baseline"] = cpu_baseline_decode(batch, heads, args.cpu_seconds)
+    return line
+
+
+def main():
+    args = _parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; "
+                          f"--gpus {args.gpus} is not supported (see DESIGN.md, sharding)"}))
+        raise SystemExit(2)
+    if args.workload == "decode":
+        line = bench_decode(args)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,62 @@
+"""Native extension facade (the counterpart of the reference's ``flashrwkv2._C``).
+
+Loads ``_flashrwkv_amd_ops.so`` (the TORCH_LIBRARY binding over
+``libflashrwkv_amd.so``) and exposes the reference's native callable names
+with the reference's positional argument order, so code written against
+``flashrwkv2._C`` (e.g. reference tests calling
+``_C.recurrent_fp32_from_decay_logits`` directly) runs unchanged.
+
+Importing this module raises ImportError when the native libraries are not
+built; there is no Python or CPU fallback.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import torch
+
+_PKG = Path(__file__).resolve().parent
+OPS_LIBRARY = _PKG / "_flashrwkv_amd_ops.so"
+HIP_LIBRARY = _PKG / "libflashrwkv_amd.so"
+
+if not OPS_LIBRARY.exists() or not HIP_LIBRARY.exists():
+    raise ImportError(
+        "flashrwkv_amd native libraries are not built "
+        f"({OPS_LIBRARY.name}, {HIP_LIBRARY.name}); run "
+        "`python -m flashrwkv_amd._build`"
+    )
+
+torch.ops.load_library(str(OPS_LIBRARY))
+ops = torch.ops.flashrwkv_amd
+
+
+def prepare_recurrent_metadata(query_start_loc, state_indices, total_tokens,
+                               state_pool_size, max_seqlen=-1):
+    return ops.prepare_recurrent_metadata(
+        query_start_loc, state_indices, int(total_tokens), int(state_pool_size),
+        int(max_seqlen))
+
+
+def recurrent_fp32_from_decay_logits(query_start_loc, state_indices, state, r,
+                                     decay_logits, k, v, a, b, output, scale,
+                                     decay_bias=None, validated_metadata=None,
+                                     max_seqlen=-1):
+    ops.recurrent_fp32_from_decay_logits(
+        query_start_loc, state_indices, state, r, decay_logits, k, v, a, b,
+        output, float(scale), decay_bias, validated_metadata, int(max_seqlen))
+
+
+def recurrent_fp32_forward_internal(query_start_loc, state_indices, state, r,
+                                    decay, k, v, a, b, output, scale, decay_mode,
+                                    decay_bias=None, validated_metadata=None,
+                                    max_seqlen=-1):
+    ops.recurrent_fp32_forward_internal(
+        query_start_loc, state_indices, state, r, decay, k, v, a, b, output,
+        float(scale), int(decay_mode), decay_bias, validated_metadata,
+        int(max_seqlen))
+
+
+def loaded_libraries() -> list[str]:
+    """Absolute paths of the native libraries this facade loaded."""
+    return [str(HIP_LIBRARY), str(OPS_LIBRARY)]

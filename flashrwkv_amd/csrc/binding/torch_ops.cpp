@@ -1,0 +1,398 @@
+// Thin PyTorch-ROCm binding over the flashrwkv_amd C ABI.
+//
+// Replaces the reference's pybind11 registration layer for the WKV7 path
+// (csrc/registration.cpp:6-8, csrc/bindings.cpp:6-44 and the per-op register_*
+// functions, e.g. csrc/sm120/tmix/wkv7/infer_recurrent_fp32io16_forward_varlen.cpp:314-362)
+// with TORCH_LIBRARY(flashrwkv_amd) ops and a torch custom class for the
+// metadata ticket. This layer only validates tensors (same rules and error
+// vocabulary as csrc/validation.cpp:27-129 and the ticket checks of
+// infer_recurrent_fp32io16_forward_varlen.cpp:44-202), owns allocations the
+// reference binding owns (metadata snapshots, status word) and forwards raw
+// device pointers plus the current HIP stream to libflashrwkv_amd.so.
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/custom_class.h>
+#include <torch/library.h>
+
+#include <cmath>
+#include <cstdint>
+#include <limits>
+#include <optional>
+#include <unordered_set>
+#include <vector>
+
+#include "../../../include/flashrwkv_amd.h"
+
+namespace {
+
+using at::Tensor;
+
+void check_rc(int rc) {
+  TORCH_CHECK(rc == FRWKV_OK, "flashrwkv_amd: ", frwkv_status_string(rc), ": ",
+              frwkv_last_error());
+}
+
+void* current_stream(const Tensor& t) {
+  return c10::hip::getCurrentHIPStream(t.device().index()).stream();
+}
+
+void check_device_contiguous(const Tensor& t, const char* name) {
+  TORCH_CHECK(t.is_cuda(), name, " must be CUDA");
+  TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+}
+
+void check_same_device(const Tensor& ref, const Tensor& t, const char* name) {
+  TORCH_CHECK(t.device() == ref.device(), name,
+              " must be on the same device as state");
+}
+
+int io_code(at::ScalarType dtype) {
+  switch (dtype) {
+    case at::kFloat:
+      return FRWKV_DTYPE_F32;
+    case at::kHalf:
+      return FRWKV_DTYPE_F16;
+    case at::kBFloat16:
+      return FRWKV_DTYPE_BF16;
+    default:
+      TORCH_CHECK(false, "token tensors must be float16 or bfloat16");
+  }
+  return -1;
+}
+
+std::optional<uint32_t> tensor_version(const Tensor& t) {
+  if (t.unsafeGetTensorImpl()->is_inference()) return std::nullopt;
+  return t.unsafeGetTensorImpl()->version_counter().current_version();
+}
+
+// Host check of packed metadata values (one device-to-host copy). Returns the
+// longest sequence. Same rules and messages as the reference's
+// check_recurrent_metadata_values (infer_recurrent_fp32io16_forward_varlen.cpp:44-79).
+int64_t check_metadata_values(const Tensor& cu_seqlens,
+                              const Tensor& state_indices, int64_t total_tokens,
+                              int64_t state_pool_size) {
+  const Tensor cu = cu_seqlens.to(at::kCPU).contiguous();
+  const Tensor slots = state_indices.to(at::kCPU).contiguous();
+  const int32_t* offsets = cu.data_ptr<int32_t>();
+  const int32_t* slot_ptr = slots.data_ptr<int32_t>();
+  const int64_t count = slots.numel();
+  TORCH_CHECK(offsets[0] == 0, "query_start_loc must start at 0");
+  TORCH_CHECK(offsets[count] == total_tokens,
+              "the final query_start_loc offset must equal total_tokens");
+  std::unordered_set<int32_t> seen;
+  int64_t longest = 0;
+  for (int64_t i = 0; i < count; ++i) {
+    const int32_t start = offsets[i];
+    const int32_t end = offsets[i + 1];
+    TORCH_CHECK(start >= 0 && end > start && end <= total_tokens,
+                "query_start_loc must be strictly increasing with non-empty sequences");
+    TORCH_CHECK(slot_ptr[i] >= 0 && slot_ptr[i] < state_pool_size,
+                "state_indices entries must be within the state pool");
+    TORCH_CHECK(seen.insert(slot_ptr[i]).second,
+                "state_indices must be unique within one call");
+    longest = std::max<int64_t>(longest, end - start);
+  }
+  return longest;
+}
+
+struct Prepared {
+  Tensor cu_snapshot;
+  Tensor slot_snapshot;
+  Tensor status;
+};
+
+// Launches the device validation (status word + snapshots) on the current stream.
+Prepared device_prepare(const Tensor& cu_seqlens, const Tensor& state_indices,
+                        int64_t total_tokens, int64_t state_pool_size) {
+  c10::DeviceGuard guard(cu_seqlens.device());
+  Prepared p{at::empty_like(cu_seqlens), at::empty_like(state_indices),
+             at::empty({1}, cu_seqlens.options())};
+  check_rc(frwkv_metadata_validate(
+      cu_seqlens.data_ptr<int32_t>(), state_indices.data_ptr<int32_t>(),
+      static_cast<int32_t>(state_indices.numel()),
+      static_cast<int32_t>(total_tokens), static_cast<int32_t>(state_pool_size),
+      p.status.data_ptr<int32_t>(), p.cu_snapshot.data_ptr<int32_t>(),
+      p.slot_snapshot.data_ptr<int32_t>(), current_stream(cu_seqlens)));
+  return p;
+}
+
+// Reusable validated-metadata ticket (the reference's RecurrentMetadataTicket,
+// infer_recurrent_fp32io16_forward_varlen.cpp:88-202): it pins the caller's
+// metadata tensors by identity, data pointer, sizes, strides and version
+// counter, the launch sizes, the device and the preparing stream, and holds
+// the device snapshots and status word that launches read.
+class MetadataTicket : public torch::CustomClassHolder {
+ public:
+  MetadataTicket(Tensor cu, Tensor slots, Prepared prepared, int64_t total_tokens,
+                 int64_t state_pool_size, int64_t max_seqlen)
+      : cu_(std::move(cu)),
+        slots_(std::move(slots)),
+        prepared_(std::move(prepared)),
+        cu_version_(tensor_version(cu_)),
+        slots_version_(tensor_version(slots_)),
+        cu_data_(cu_.data_ptr()),
+        slots_data_(slots_.data_ptr()),
+        cu_sizes_(cu_.sizes().vec()),
+        slots_sizes_(slots_.sizes().vec()),
+        cu_strides_(cu_.strides().vec()),
+        slots_strides_(slots_.strides().vec()),
+        total_tokens_(total_tokens),
+        state_pool_size_(state_pool_size),
+        max_seqlen_(max_seqlen),
+        device_(cu_.device()),
+        stream_(current_stream(cu_)) {}
+
+  void check_compatible(const Tensor& cu, const Tensor& slots,
+                        int64_t total_tokens, int64_t state_pool_size,
+                        int64_t max_seqlen) const {
+    TORCH_CHECK(cu.is_same(cu_),
+                "validated_metadata query_start_loc identity mismatch");
+    TORCH_CHECK(slots.is_same(slots_),
+                "validated_metadata state_indices identity mismatch");
+    TORCH_CHECK(cu.data_ptr() == cu_data_ && slots.data_ptr() == slots_data_,
+                "validated_metadata metadata data_ptr mismatch");
+    TORCH_CHECK(cu.sizes().vec() == cu_sizes_ && slots.sizes().vec() == slots_sizes_ &&
+                    cu.strides().vec() == cu_strides_ &&
+                    slots.strides().vec() == slots_strides_,
+                "validated_metadata metadata shape or stride mismatch");
+    if (cu_version_.has_value()) {
+      TORCH_CHECK(tensor_version(cu) == cu_version_,
+                  "validated_metadata query_start_loc version mismatch");
+    }
+    if (slots_version_.has_value()) {
+      TORCH_CHECK(tensor_version(slots) == slots_version_,
+                  "validated_metadata state_indices version mismatch");
+    }
+    TORCH_CHECK(cu.device() == device_ && slots.device() == device_,
+                "validated_metadata device mismatch");
+    TORCH_CHECK(total_tokens == total_tokens_,
+                "validated_metadata total_tokens mismatch");
+    TORCH_CHECK(state_pool_size == state_pool_size_,
+                "validated_metadata state_pool_size mismatch");
+    if (max_seqlen > 0) {
+      TORCH_CHECK(max_seqlen == max_seqlen_, "validated_metadata max_seqlen mismatch");
+    }
+    TORCH_CHECK(current_stream(cu) == stream_,
+                "validated_metadata stream mismatch; prepare and consume the "
+                "ticket on the same stream");
+  }
+
+  const Prepared& prepared() const { return prepared_; }
+  int64_t max_seqlen() const { return max_seqlen_; }
+  int64_t total_tokens() const { return total_tokens_; }
+  int64_t state_pool_size() const { return state_pool_size_; }
+
+ private:
+  Tensor cu_, slots_;
+  Prepared prepared_;
+  std::optional<uint32_t> cu_version_, slots_version_;
+  void* cu_data_;
+  void* slots_data_;
+  std::vector<int64_t> cu_sizes_, slots_sizes_, cu_strides_, slots_strides_;
+  int64_t total_tokens_, state_pool_size_, max_seqlen_;
+  c10::Device device_;
+  void* stream_;
+};
+
+using TicketPtr = c10::intrusive_ptr<MetadataTicket>;
+
+TicketPtr prepare_recurrent_metadata(Tensor query_start_loc, Tensor state_indices,
+                                     int64_t total_tokens, int64_t state_pool_size,
+                                     int64_t max_seqlen) {
+  check_device_contiguous(query_start_loc, "query_start_loc");
+  check_device_contiguous(state_indices, "state_indices");
+  TORCH_CHECK(state_indices.device() == query_start_loc.device(),
+              "state_indices must be on the same device as state");
+  TORCH_CHECK(query_start_loc.scalar_type() == at::kInt &&
+                  state_indices.scalar_type() == at::kInt,
+              "recurrent metadata must be int32");
+  TORCH_CHECK(query_start_loc.dim() == 1 && state_indices.dim() == 1 &&
+                  state_indices.numel() > 0 &&
+                  query_start_loc.numel() == state_indices.numel() + 1,
+              "query_start_loc must have shape [B+1] and state_indices shape [B]");
+  TORCH_CHECK(state_indices.numel() <= 65535,
+              "state_indices must contain at most 65535 sequences");
+  TORCH_CHECK(total_tokens > 0 && total_tokens <= std::numeric_limits<int32_t>::max(),
+              "total_tokens must be positive and fit in int32");
+  TORCH_CHECK(state_pool_size > 0 &&
+                  state_pool_size <= std::numeric_limits<int32_t>::max(),
+              "state_pool_size must be positive and fit in int32");
+  const int64_t inferred =
+      check_metadata_values(query_start_loc, state_indices, total_tokens, state_pool_size);
+  if (max_seqlen <= 0) {
+    max_seqlen = inferred;
+  } else {
+    TORCH_CHECK(max_seqlen == inferred,
+                "max_seqlen must equal the largest packed sequence length");
+  }
+  Prepared prepared =
+      device_prepare(query_start_loc, state_indices, total_tokens, state_pool_size);
+  return c10::make_intrusive<MetadataTicket>(query_start_loc, state_indices,
+                                             std::move(prepared), total_tokens,
+                                             state_pool_size, max_seqlen);
+}
+
+// Layout checks of the fp32-state recurrent op (csrc/validation.cpp:27-129
+// rules; fp32 tokens only through the internal op).
+void check_recurrent_layout(const Tensor& cu, const Tensor& slots,
+                            const Tensor& state, const Tensor& r,
+                            const Tensor& decay, const Tensor& k, const Tensor& v,
+                            const Tensor& a, const Tensor& b, const Tensor& output,
+                            double scale, bool allow_fp32_tokens) {
+  const std::pair<const Tensor*, const char*> all[] = {
+      {&cu, "query_start_loc"}, {&slots, "state_indices"}, {&state, "state"},
+      {&r, "r"}, {&decay, "decay_logits"}, {&k, "k"}, {&v, "v"}, {&a, "a"},
+      {&b, "b"}, {&output, "output"}};
+  for (const auto& item : all) check_device_contiguous(*item.first, item.second);
+  TORCH_CHECK(cu.scalar_type() == at::kInt, "query_start_loc must be int32");
+  TORCH_CHECK(slots.scalar_type() == at::kInt, "state_indices must be int32");
+  TORCH_CHECK(std::isfinite(scale), "scale must be finite");
+  const int64_t count = slots.numel();
+  TORCH_CHECK(count > 0 && count <= 65535,
+              "state_indices must contain 1..65535 sequences");
+  TORCH_CHECK(slots.dim() == 1, "state_indices must have shape [N]");
+  TORCH_CHECK(cu.dim() == 1 && cu.size(0) == count + 1,
+              "query_start_loc must have shape [N+1]");
+  TORCH_CHECK(state.dim() == 4 && state.size(0) > 0 && state.size(1) > 0 &&
+                  state.size(2) == state.size(3),
+              "state must have square shape [slots,H,D,D]");
+  TORCH_CHECK(state.scalar_type() == at::kFloat, "state must be float32");
+  const int64_t d = state.size(2);
+  TORCH_CHECK(d == 64 || d == 128 || d == 256,
+              "recurrent head size must be 64, 128, or 256, got ", d);
+  TORCH_CHECK(state.size(0) <= std::numeric_limits<int32_t>::max(),
+              "state slot count must fit in int32");
+  const int64_t heads = state.size(1);
+  TORCH_CHECK(r.dim() == 3 && r.size(0) > 0 && r.size(1) == heads && r.size(2) == d,
+              "r must have shape [total_tokens,H,D] matching state");
+  TORCH_CHECK(r.size(0) <= std::numeric_limits<int32_t>::max(),
+              "token count must fit in int32");
+  TORCH_CHECK(r.sizes() == decay.sizes() && r.sizes() == k.sizes() &&
+                  r.sizes() == v.sizes() && r.sizes() == a.sizes() &&
+                  r.sizes() == b.sizes() && r.sizes() == output.sizes(),
+              "r,decay_logits,k,v,a,b,output shape mismatch");
+  const bool ok_dtype = r.scalar_type() == at::kHalf ||
+                        r.scalar_type() == at::kBFloat16 ||
+                        (allow_fp32_tokens && r.scalar_type() == at::kFloat);
+  TORCH_CHECK(ok_dtype, "token tensors must be float16 or bfloat16");
+  const auto dt = r.scalar_type();
+  TORCH_CHECK(decay.scalar_type() == dt && k.scalar_type() == dt &&
+                  v.scalar_type() == dt && a.scalar_type() == dt &&
+                  b.scalar_type() == dt && output.scalar_type() == dt,
+              "r,decay_logits,k,v,a,b,output dtype mismatch");
+  for (const auto& item : all) check_same_device(state, *item.first, item.second);
+}
+
+void check_decay_bias(const std::optional<Tensor>& bias, const Tensor& state,
+                      const Tensor& r) {
+  if (!bias.has_value()) return;
+  check_device_contiguous(*bias, "decay_bias");
+  check_same_device(state, *bias, "decay_bias");
+  TORCH_CHECK(bias->scalar_type() == r.scalar_type(),
+              "decay_bias must match the token tensor dtype");
+  const int64_t heads = state.size(1), d = state.size(2);
+  TORCH_CHECK((bias->dim() == 1 && bias->numel() == heads * d) ||
+                  (bias->dim() == 2 && bias->size(0) == heads && bias->size(1) == d),
+              "decay_bias must have shape [H*D] or [H,D]");
+}
+
+void recurrent_impl(const Tensor& cu, const Tensor& slots, Tensor& state,
+                    const Tensor& r, const Tensor& decay, const Tensor& k,
+                    const Tensor& v, const Tensor& a, const Tensor& b,
+                    Tensor& output, double scale,
+                    const std::optional<Tensor>& decay_bias,
+                    const std::optional<TicketPtr>& ticket, int64_t max_seqlen,
+                    int decay_mode, bool allow_fp32_tokens) {
+  check_recurrent_layout(cu, slots, state, r, decay, k, v, a, b, output, scale,
+                         allow_fp32_tokens);
+  check_decay_bias(decay_bias, state, r);
+  TORCH_CHECK(!(decay_bias.has_value() && decay_mode == FRWKV_DECAY_RAW_W),
+              "decay_bias is only defined for decay logits");
+  c10::DeviceGuard guard(state.device());
+  Prepared launch;
+  if (ticket.has_value() && ticket->defined()) {
+    (*ticket)->check_compatible(cu, slots, r.size(0), state.size(0), max_seqlen);
+    launch = (*ticket)->prepared();
+    max_seqlen = (*ticket)->max_seqlen();
+  } else {
+    // No ticket: device validation only (no host sync); a direct call with
+    // bad metadata fails closed inside the kernel.
+    launch = device_prepare(cu, slots, r.size(0), state.size(0));
+  }
+  check_rc(frwkv_recurrent_forward(
+      io_code(r.scalar_type()), decay_mode, static_cast<int32_t>(slots.numel()),
+      static_cast<int32_t>(state.size(1)), static_cast<int32_t>(state.size(2)),
+      static_cast<int32_t>(r.size(0)), static_cast<int32_t>(max_seqlen),
+      static_cast<int32_t>(state.size(0)), launch.cu_snapshot.data_ptr<int32_t>(),
+      launch.slot_snapshot.data_ptr<int32_t>(), launch.status.data_ptr<int32_t>(),
+      state.data_ptr<float>(), r.data_ptr(), decay.data_ptr(),
+      decay_bias.has_value() ? decay_bias->data_ptr() : nullptr, k.data_ptr(),
+      v.data_ptr(), a.data_ptr(), b.data_ptr(), output.data_ptr(),
+      static_cast<float>(scale), current_stream(state)));
+}
+
+// Public op: raw decay logits, fp16/bf16 tokens.
+void recurrent_fp32_from_decay_logits(
+    Tensor query_start_loc, Tensor state_indices, Tensor state, Tensor r,
+    Tensor decay_logits, Tensor k, Tensor v, Tensor a, Tensor b, Tensor output,
+    double scale, std::optional<Tensor> decay_bias,
+    std::optional<TicketPtr> validated_metadata, int64_t max_seqlen) {
+  recurrent_impl(query_start_loc, state_indices, state, r, decay_logits, k, v, a,
+                 b, output, scale, decay_bias, validated_metadata, max_seqlen,
+                 FRWKV_DECAY_LOGITS, /*allow_fp32_tokens=*/false);
+}
+
+// Internal op: explicit decay mode (0 logits, 1 raw retention) and fp32 tokens
+// allowed. Used by the measurement harness and parity tests.
+void recurrent_fp32_forward_internal(
+    Tensor query_start_loc, Tensor state_indices, Tensor state, Tensor r,
+    Tensor decay, Tensor k, Tensor v, Tensor a, Tensor b, Tensor output,
+    double scale, int64_t decay_mode, std::optional<Tensor> decay_bias,
+    std::optional<TicketPtr> validated_metadata, int64_t max_seqlen) {
+  TORCH_CHECK(decay_mode == FRWKV_DECAY_LOGITS || decay_mode == FRWKV_DECAY_RAW_W,
+              "decay_mode must be 0 (logits) or 1 (raw retention)");
+  recurrent_impl(query_start_loc, state_indices, state, r, decay, k, v, a, b,
+                 output, scale, decay_bias, validated_metadata, max_seqlen,
+                 static_cast<int>(decay_mode), /*allow_fp32_tokens=*/true);
+}
+
+}  // namespace
+
+TORCH_LIBRARY(flashrwkv_amd, m) {
+  m.class_<MetadataTicket>("MetadataTicket")
+      .def("max_seqlen", [](const TicketPtr& t) { return t->max_seqlen(); })
+      .def("total_tokens", [](const TicketPtr& t) { return t->total_tokens(); })
+      .def("state_pool_size", [](const TicketPtr& t) { return t->state_pool_size(); })
+      .def("status", [](const TicketPtr& t) { return t->prepared().status; })
+      .def("query_start_loc_snapshot",
+           [](const TicketPtr& t) { return t->prepared().cu_snapshot; })
+      .def("state_indices_snapshot",
+           [](const TicketPtr& t) { return t->prepared().slot_snapshot; })
+      .def("check_compatible",
+           [](const TicketPtr& t, Tensor cu, Tensor slots, int64_t total_tokens,
+              int64_t state_pool_size, int64_t max_seqlen) {
+             t->check_compatible(cu, slots, total_tokens, state_pool_size, max_seqlen);
+           });
+  m.def(
+      "prepare_recurrent_metadata(Tensor query_start_loc, Tensor state_indices, "
+      "int total_tokens, int state_pool_size, int max_seqlen=-1) -> "
+      "__torch__.torch.classes.flashrwkv_amd.MetadataTicket",
+      &prepare_recurrent_metadata);
+  m.def(
+      "recurrent_fp32_from_decay_logits(Tensor query_start_loc, Tensor "
+      "state_indices, Tensor(a!) state, Tensor r, Tensor decay_logits, Tensor k, "
+      "Tensor v, Tensor a, Tensor b, Tensor(b!) output, float scale, "
+      "Tensor? decay_bias=None, "
+      "__torch__.torch.classes.flashrwkv_amd.MetadataTicket? "
+      "validated_metadata=None, int max_seqlen=-1) -> ()",
+      &recurrent_fp32_from_decay_logits);
+  m.def(
+      "recurrent_fp32_forward_internal(Tensor query_start_loc, Tensor "
+      "state_indices, Tensor(a!) state, Tensor r, Tensor decay, Tensor k, "
+      "Tensor v, Tensor a, Tensor b, Tensor(b!) output, float scale, "
+      "int decay_mode, Tensor? decay_bias=None, "
+      "__torch__.torch.classes.flashrwkv_amd.MetadataTicket? "
+      "validated_metadata=None, int max_seqlen=-1) -> ()",
+      &recurrent_fp32_forward_internal);
+}

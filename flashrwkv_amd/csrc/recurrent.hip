@@ -1,0 +1,260 @@
+// fp32-state WKV7 recurrent forward (decode and short state-carry sequences).
+//
+// Replaces the reference's wkv_fp32_v2_kernel / wkv_fp32_v2_small_warp_kernel
+// and their dispatch (csrc/sm120/tmix/wkv7/infer_recurrent_fp32io16_forward_varlen.cu:90-275,
+// 369-508). Same contract: packed [N,H,D] tokens, [slots,H,D,D] fp32 pool laid
+// out [K,V] and updated in place at state_indices, fail-closed NaN output when
+// the metadata status word is non-zero.
+//
+// MI355X design. The value columns of a state are independent given the token
+// vectors (sa[v], y[v] and S[:,v] only touch column v), so the work unit is a
+// wave owning a slab of CW columns of one (sequence, head) state:
+//   * lane l holds a 4-column group (cg = l % (CW/4)) for RPL consecutive key
+//     rows (rg = l / (CW/4)), i.e. RPL float4 registers; the wave's loads and
+//     stores of a state slab are 16-byte per lane and fully coalesced;
+//   * token vectors of the lane's RPL rows are contiguous and read directly
+//     from global memory (lanes sharing rows share the cache line);
+//   * S^T a and S^T r reduce first in-lane over RPL rows, then across the
+//     NG = 64/(CW/4) row groups with xor shuffles;
+//   * waves never synchronise with each other, so the kernel has no barrier.
+// Decode (T=1) is HBM-bound: per (sequence, head) it moves the 16 KiB state in
+// and out plus 7 token rows; everything is issued up front.
+#include "capi_internal.h"
+#include "wkv7_device.h"
+
+namespace frwkv {
+namespace {
+
+constexpr int kThreads = 256;  // 4 independent waves per workgroup
+
+template <int NG>
+__device__ __forceinline__ float reduce_row_groups(float x) {
+  // Lanes with equal column group differ in the high bits of the lane id.
+  constexpr int kCg = 64 / NG;
+#pragma unroll
+  for (int offset = kCg; offset < 64; offset <<= 1) {
+    x += __shfl_xor(x, offset, 64);
+  }
+  return x;
+}
+
+template <int D, int CW, typename T, DecayMode M>
+__global__ __launch_bounds__(kThreads) void recurrent_fp32_kernel(
+    int32_t num_heads, int32_t num_units, int64_t output_elements,
+    int32_t total_tokens, int32_t state_pool_size,
+    const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ slots,
+    const int32_t* __restrict__ status, float* __restrict__ state,
+    const typename IoTraits<T>::storage* __restrict__ r_ptr,
+    const typename IoTraits<T>::storage* __restrict__ decay_ptr,
+    const typename IoTraits<T>::storage* __restrict__ bias_ptr,
+    const typename IoTraits<T>::storage* __restrict__ k_ptr,
+    const typename IoTraits<T>::storage* __restrict__ v_ptr,
+    const typename IoTraits<T>::storage* __restrict__ a_ptr,
+    const typename IoTraits<T>::storage* __restrict__ b_ptr,
+    typename IoTraits<T>::storage* __restrict__ out_ptr, float scale) {
+  constexpr int kWavesPerUnit = D / CW;
+  constexpr int kCg = CW / 4;       // lanes per row group (float4 columns)
+  constexpr int kNg = 64 / kCg;     // row groups per wave
+  constexpr int kRpl = D / kNg;     // key rows per lane
+  static_assert(kRpl % 4 == 0, "lane rows load in 4-element pieces");
+
+  if (status[0] != 0) {
+    fill_nan<T>(out_ptr, output_elements);
+    return;
+  }
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  const int unit = wave / kWavesPerUnit;
+  if (unit >= num_units) return;
+  const int slab = wave % kWavesPerUnit;
+  const int seq = unit / num_heads;
+  const int head = unit % num_heads;
+  const int cg = lane % kCg;
+  const int rg = lane / kCg;
+  const int row0 = rg * kRpl;
+  const int col = slab * CW + 4 * cg;
+
+  const int32_t t_begin = cu_seqlens[seq];
+  const int32_t t_end = cu_seqlens[seq + 1];
+  const int32_t slot = slots[seq];
+  // Validated metadata never fails these; they keep a bad direct launch from
+  // touching memory outside the tensors.
+  if (t_begin < 0 || t_end > total_tokens || t_begin >= t_end || slot < 0 ||
+      slot >= state_pool_size) {
+    return;
+  }
+
+  float* sbase = state + ((static_cast<int64_t>(slot) * num_heads + head) * D) * D;
+  float4 s[kRpl];
+#pragma unroll
+  for (int j = 0; j < kRpl; ++j) {
+    s[j] = *reinterpret_cast<const float4*>(sbase + static_cast<int64_t>(row0 + j) * D + col);
+  }
+
+  float bias[kRpl];
+  if (bias_ptr != nullptr) {
+    load_vec<T, kRpl>(bias_ptr + head * D + row0, bias);
+  } else {
+#pragma unroll
+    for (int j = 0; j < kRpl; ++j) bias[j] = 0.0f;
+  }
+
+  for (int32_t t = t_begin; t < t_end; ++t) {
+    const int64_t base = (static_cast<int64_t>(t) * num_heads + head) * D;
+    float rr[kRpl], ww[kRpl], kk[kRpl], aa[kRpl], bb[kRpl], vv[4];
+    load_vec<T, kRpl>(a_ptr + base + row0, aa);
+    load_vec<T, kRpl>(decay_ptr + base + row0, ww);
+    load_vec<T, kRpl>(b_ptr + base + row0, bb);
+    load_vec<T, kRpl>(k_ptr + base + row0, kk);
+    load_vec<T, kRpl>(r_ptr + base + row0, rr);
+    load_vec<T, 4>(v_ptr + base + col, vv);
+
+    float4 sa = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < kRpl; ++j) {
+      sa.x = fmaf(aa[j], s[j].x, sa.x);
+      sa.y = fmaf(aa[j], s[j].y, sa.y);
+      sa.z = fmaf(aa[j], s[j].z, sa.z);
+      sa.w = fmaf(aa[j], s[j].w, sa.w);
+    }
+    sa.x = reduce_row_groups<kNg>(sa.x);
+    sa.y = reduce_row_groups<kNg>(sa.y);
+    sa.z = reduce_row_groups<kNg>(sa.z);
+    sa.w = reduce_row_groups<kNg>(sa.w);
+
+    float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < kRpl; ++j) {
+      const float w = decay_retention<M>(ww[j] + bias[j]);
+      s[j].x = fmaf(w, s[j].x, fmaf(bb[j], sa.x, kk[j] * vv[0]));
+      s[j].y = fmaf(w, s[j].y, fmaf(bb[j], sa.y, kk[j] * vv[1]));
+      s[j].z = fmaf(w, s[j].z, fmaf(bb[j], sa.z, kk[j] * vv[2]));
+      s[j].w = fmaf(w, s[j].w, fmaf(bb[j], sa.w, kk[j] * vv[3]));
+      y.x = fmaf(rr[j], s[j].x, y.x);
+      y.y = fmaf(rr[j], s[j].y, y.y);
+      y.z = fmaf(rr[j], s[j].z, y.z);
+      y.w = fmaf(rr[j], s[j].w, y.w);
+    }
+    y.x = reduce_row_groups<kNg>(y.x);
+    y.y = reduce_row_groups<kNg>(y.y);
+    y.z = reduce_row_groups<kNg>(y.z);
+    y.w = reduce_row_groups<kNg>(y.w);
+    if (rg == 0) {
+      store4<T>(out_ptr + base + col, scale * y.x, scale * y.y, scale * y.z,
+                scale * y.w);
+    }
+  }
+
+#pragma unroll
+  for (int j = 0; j < kRpl; ++j) {
+    *reinterpret_cast<float4*>(sbase + static_cast<int64_t>(row0 + j) * D + col) = s[j];
+  }
+}
+
+struct RecurrentArgs {
+  int32_t num_sequences, num_heads, head_size, total_tokens, max_seqlen,
+      state_pool_size;
+  const int32_t* cu;
+  const int32_t* slots;
+  const int32_t* status;
+  float* state;
+  const void *r, *decay, *bias, *k, *v, *a, *b;
+  void* out;
+  float scale;
+  hipStream_t stream;
+};
+
+template <int D, int CW, typename T, DecayMode M>
+int launch_recurrent(const RecurrentArgs& p) {
+  using S = typename IoTraits<T>::storage;
+  const int units = p.num_sequences * p.num_heads;
+  const int64_t waves = static_cast<int64_t>(units) * (D / CW);
+  const int blocks = static_cast<int>((waves + 3) / 4);
+  const int64_t out_elems = static_cast<int64_t>(p.total_tokens) * p.num_heads * D;
+  hipLaunchKernelGGL((recurrent_fp32_kernel<D, CW, T, M>), dim3(blocks),
+                     dim3(kThreads), 0, p.stream, p.num_heads, units, out_elems,
+                     p.total_tokens, p.state_pool_size, p.cu, p.slots, p.status,
+                     p.state, static_cast<const S*>(p.r),
+                     static_cast<const S*>(p.decay), static_cast<const S*>(p.bias),
+                     static_cast<const S*>(p.k), static_cast<const S*>(p.v),
+                     static_cast<const S*>(p.a), static_cast<const S*>(p.b),
+                     static_cast<S*>(p.out), p.scale);
+  return check_launch("recurrent_fp32_kernel");
+}
+
+template <typename T, DecayMode M>
+int dispatch_head_size(const RecurrentArgs& p) {
+  switch (p.head_size) {
+    case 64:
+      // Decode keeps one wave per state (fewest redundant decay evaluations);
+      // longer sequences split the state over 4 waves for more parallelism.
+      if (p.max_seqlen > 0 && p.max_seqlen <= 2) {
+        return launch_recurrent<64, 64, T, M>(p);
+      }
+      return launch_recurrent<64, 16, T, M>(p);
+    case 128:
+      return launch_recurrent<128, 16, T, M>(p);
+    case 256:
+      return launch_recurrent<256, 16, T, M>(p);
+    default:
+      return set_error(FRWKV_ERR_UNSUPPORTED,
+                       "recurrent head size must be 64, 128, or 256, got %d",
+                       p.head_size);
+  }
+}
+
+template <typename T>
+int dispatch_decay(const RecurrentArgs& p, int decay_mode) {
+  if (decay_mode == FRWKV_DECAY_LOGITS) return dispatch_head_size<T, DecayMode::kLogits>(p);
+  if (decay_mode == FRWKV_DECAY_RAW_W) {
+    if (p.bias != nullptr) {
+      return set_error(FRWKV_ERR_INVALID_ARGUMENT,
+                       "decay_bias is only defined for the logits decay mode");
+    }
+    return dispatch_head_size<T, DecayMode::kRawW>(p);
+  }
+  return set_error(FRWKV_ERR_INVALID_ARGUMENT, "unknown decay mode %d", decay_mode);
+}
+
+}  // namespace
+}  // namespace frwkv
+
+extern "C" int frwkv_recurrent_forward(
+    int io_dtype, int decay_mode, int32_t num_sequences, int32_t num_heads,
+    int32_t head_size, int32_t total_tokens, int32_t max_seqlen,
+    int32_t state_pool_size, const int32_t* cu_seqlens,
+    const int32_t* state_indices, const int32_t* metadata_status,
+    float* state_pool, const void* r, const void* decay, const void* decay_bias,
+    const void* k, const void* v, const void* a, const void* b, void* output,
+    float scale, void* stream) {
+  using namespace frwkv;
+  if (!cu_seqlens || !state_indices || !metadata_status || !state_pool || !r ||
+      !decay || !k || !v || !a || !b || !output) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT,
+                     "frwkv_recurrent_forward: null pointer argument");
+  }
+  if (num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 ||
+      total_tokens <= 0 || state_pool_size <= 0) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT,
+                     "frwkv_recurrent_forward: sizes must be positive "
+                     "(B=%d, H=%d, N=%d, slots=%d)",
+                     num_sequences, num_heads, total_tokens, state_pool_size);
+  }
+  if (!__builtin_isfinite(scale)) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT, "scale must be finite");
+  }
+  RecurrentArgs p{num_sequences, num_heads, head_size, total_tokens, max_seqlen,
+                  state_pool_size, cu_seqlens, state_indices, metadata_status,
+                  state_pool, r, decay, decay_bias, k, v, a, b, output, scale,
+                  static_cast<hipStream_t>(stream)};
+  switch (io_dtype) {
+    case FRWKV_DTYPE_BF16:
+      return dispatch_decay<Bf16>(p, decay_mode);
+    case FRWKV_DTYPE_F16:
+      return dispatch_decay<F16>(p, decay_mode);
+    case FRWKV_DTYPE_F32:
+      return dispatch_decay<float>(p, decay_mode);
+    default:
+      return set_error(FRWKV_ERR_INVALID_ARGUMENT, "unknown io dtype %d", io_dtype);
+  }
+}

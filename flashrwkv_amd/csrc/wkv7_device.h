@@ -1,0 +1,176 @@
+// Device-side helpers shared by the WKV7 HIP kernels (gfx950, wave64).
+//
+// Decay transform: the reference's public boundary is raw decay logits x,
+// turned into the retention w = exp(-e^{-1/2} * sigmoid(x + bias))
+// (reference csrc/sm120/tmix/wkv7/recurrent_decay.cuh:10-22). This build also
+// accepts the retention w itself (DecayMode::kRawW), which is what the
+// measurement harness feeds (w = exp(-exp(u)) covers values below the
+// logits mode's floor of exp(-e^{-1/2}) = 0.5453).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace frwkv {
+
+enum class DecayMode : int { kLogits = 0, kRawW = 1 };
+
+// e^{-1/2}: the clampw scale of the retention transform.
+constexpr float kExpNegHalf = 0.60653065971263342f;
+constexpr float kLog2E = 1.4426950408889634f;
+
+// Retention and its natural log from a pre-transform decay input.
+// Logits: log w = -e^{-1/2} * sigmoid(x); computing log w directly keeps full
+// precision for w close to 1, which the chunked kernels need.
+template <DecayMode M>
+__device__ __forceinline__ float decay_log(float x) {
+  if constexpr (M == DecayMode::kLogits) {
+    const float sig = 1.0f / (1.0f + exp2f(-kLog2E * x));
+    return -kExpNegHalf * sig;
+  } else {
+    return __logf(x);
+  }
+}
+
+template <DecayMode M>
+__device__ __forceinline__ float decay_retention(float x) {
+  if constexpr (M == DecayMode::kLogits) {
+    return exp2f(kLog2E * decay_log<M>(x));
+  } else {
+    return x;
+  }
+}
+
+// ------------------------------------------------------------ io types ----
+
+typedef uint16_t bf16_bits;
+typedef uint16_t f16_bits;
+
+struct Bf16 {};
+struct F16 {};
+
+template <typename T> struct IoTraits;
+template <> struct IoTraits<float> {
+  using storage = float;
+  static constexpr int kBytes = 4;
+};
+template <> struct IoTraits<Bf16> {
+  using storage = uint16_t;
+  static constexpr int kBytes = 2;
+};
+template <> struct IoTraits<F16> {
+  using storage = uint16_t;
+  static constexpr int kBytes = 2;
+};
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t bits16) {
+  _Float16 h;
+  __builtin_memcpy(&h, &bits16, 2);
+  return static_cast<float>(h);
+}
+
+template <typename T>
+__device__ __forceinline__ float to_f32(typename IoTraits<T>::storage x) {
+  if constexpr (__is_same(T, float)) {
+    return x;
+  } else if constexpr (__is_same(T, Bf16)) {
+    return bf16_to_f32(x);
+  } else {
+    return f16_to_f32(x);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ typename IoTraits<T>::storage from_f32(float x) {
+  if constexpr (__is_same(T, float)) {
+    return x;
+  } else if constexpr (__is_same(T, Bf16)) {
+    __bf16 h = static_cast<__bf16>(x);  // v_cvt_pk_bf16_f32: round to nearest even
+    uint16_t bits;
+    __builtin_memcpy(&bits, &h, 2);
+    return bits;
+  } else {
+    _Float16 h = static_cast<_Float16>(x);
+    uint16_t bits;
+    __builtin_memcpy(&bits, &h, 2);
+    return bits;
+  }
+}
+
+// Loads N contiguous elements (16-byte aligned when N*bytes >= 16) as floats.
+template <typename T, int N>
+__device__ __forceinline__ void load_vec(const typename IoTraits<T>::storage* p,
+                                         float (&out)[N]) {
+  if constexpr (__is_same(T, float)) {
+    static_assert(N % 4 == 0, "fp32 rows load in float4 pieces");
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      const float4 q = reinterpret_cast<const float4*>(p)[i];
+      out[4 * i + 0] = q.x;
+      out[4 * i + 1] = q.y;
+      out[4 * i + 2] = q.z;
+      out[4 * i + 3] = q.w;
+    }
+  } else if constexpr (N % 8 == 0) {
+#pragma unroll
+    for (int i = 0; i < N / 8; ++i) {
+      const uint4 q = reinterpret_cast<const uint4*>(p)[i];
+      const uint32_t words[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        out[8 * i + 2 * j + 0] = to_f32<T>(static_cast<uint16_t>(words[j] & 0xffffu));
+        out[8 * i + 2 * j + 1] = to_f32<T>(static_cast<uint16_t>(words[j] >> 16));
+      }
+    }
+  } else {
+    static_assert(N % 4 == 0, "16-bit rows load in 8-byte pieces");
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      const uint2 q = reinterpret_cast<const uint2*>(p)[i];
+      out[4 * i + 0] = to_f32<T>(static_cast<uint16_t>(q.x & 0xffffu));
+      out[4 * i + 1] = to_f32<T>(static_cast<uint16_t>(q.x >> 16));
+      out[4 * i + 2] = to_f32<T>(static_cast<uint16_t>(q.y & 0xffffu));
+      out[4 * i + 3] = to_f32<T>(static_cast<uint16_t>(q.y >> 16));
+    }
+  }
+}
+
+// Stores 4 contiguous values.
+template <typename T>
+__device__ __forceinline__ void store4(typename IoTraits<T>::storage* p, float x0,
+                                       float x1, float x2, float x3) {
+  if constexpr (__is_same(T, float)) {
+    *reinterpret_cast<float4*>(p) = make_float4(x0, x1, x2, x3);
+  } else {
+    uint2 q;
+    q.x = static_cast<uint32_t>(from_f32<T>(x0)) |
+          (static_cast<uint32_t>(from_f32<T>(x1)) << 16);
+    q.y = static_cast<uint32_t>(from_f32<T>(x2)) |
+          (static_cast<uint32_t>(from_f32<T>(x3)) << 16);
+    *reinterpret_cast<uint2*>(p) = q;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ typename IoTraits<T>::storage nan_value() {
+  return from_f32<T>(__int_as_float(0x7fc00000));
+}
+
+// Grid-stride NaN fill used when the metadata status word reports an error:
+// outputs become NaN and no state is written (fail closed).
+template <typename T>
+__device__ __forceinline__ void fill_nan(typename IoTraits<T>::storage* out,
+                                         int64_t elements) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const auto nan = nan_value<T>();
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+       i < elements; i += stride) {
+    out[i] = nan;
+  }
+}
+
+}  // namespace frwkv

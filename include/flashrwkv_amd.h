@@ -1,0 +1,115 @@
+/*
+ * flashrwkv_amd -- C ABI of the MI355X-native WKV7 operator family.
+ *
+ * libflashrwkv_amd.so exports these entry points. They take plain device
+ * pointers, sizes and a HIP stream (passed as void*, a hipStream_t; NULL is
+ * the null stream), launch hand-written gfx950 HIP kernels on that stream and
+ * return immediately (no host synchronisation, no allocation). Every call
+ * returns FRWKV_OK or an error code; frwkv_last_error() gives the message of
+ * the last failing call on the calling thread.
+ *
+ * Tensor conventions (all row-major, contiguous, device memory):
+ *   tokens   r, decay, k, v, a, b, output: [total_tokens, H, D] of io_dtype
+ *   state    pool [slots, H, D, D] laid out [K,V] (state[slot][h][key][value])
+ *   metadata cu_seqlens int32 [B+1], state_indices int32 [B]
+ *   decay    FRWKV_DECAY_LOGITS: raw decay logits x, retention
+ *            w = exp(-e^{-1/2} sigmoid(x + bias)) (the reference boundary);
+ *            FRWKV_DECAY_RAW_W: the retention w itself (bias must be NULL).
+ *   recurrence per token: sa = S^T a; S = diag(w) S + b sa^T + k v^T;
+ *            y = scale S^T r.
+ *
+ * Each entry point cites the reference native interface it replaces
+ * (paths relative to the rwkv-rs/FlashRWKV2 source tree).
+ */
+#ifndef FLASHRWKV_AMD_H_
+#define FLASHRWKV_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FRWKV_ABI_VERSION 1
+
+enum frwkv_status {
+  FRWKV_OK = 0,
+  FRWKV_ERR_INVALID_ARGUMENT = 1,
+  FRWKV_ERR_UNSUPPORTED = 2,
+  FRWKV_ERR_HIP = 3
+};
+
+enum frwkv_dtype {
+  FRWKV_DTYPE_F32 = 0,
+  FRWKV_DTYPE_F16 = 1,
+  FRWKV_DTYPE_BF16 = 2
+};
+
+enum frwkv_decay_mode {
+  FRWKV_DECAY_LOGITS = 0,
+  FRWKV_DECAY_RAW_W = 1
+};
+
+/* Metadata status bits written by frwkv_metadata_validate (same bit meanings
+ * as csrc/validation/recurrent_metadata.cu:15-20). */
+enum frwkv_metadata_error {
+  FRWKV_META_BAD_ENDPOINT = 1,
+  FRWKV_META_BAD_RANGE = 2,
+  FRWKV_META_BAD_SLOT = 4,
+  FRWKV_META_DUPLICATE_SLOT = 8
+};
+
+/* ABI version of the loaded library (FRWKV_ABI_VERSION at build time). */
+int frwkv_abi_version(void);
+
+/* Static description of a status code. */
+const char* frwkv_status_string(int status);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* frwkv_last_error(void);
+
+/*
+ * Validates packed metadata on the device and snapshots it.
+ * Replaces prepare_recurrent_metadata_cuda / validate_recurrent_metadata_kernel
+ * (csrc/validation/recurrent_metadata.cu:22-97, 99-140).
+ * Writes status[0] = OR of frwkv_metadata_error bits (0 when valid) and copies
+ * cu_seqlens / state_indices into the snapshots, which later launches read so
+ * that a caller mutating its metadata afterwards cannot change a launch.
+ * Requires 1 <= num_sequences <= 65535, total_tokens > 0, state_pool_size > 0.
+ */
+int frwkv_metadata_validate(const int32_t* cu_seqlens,
+                            const int32_t* state_indices,
+                            int32_t num_sequences, int32_t total_tokens,
+                            int32_t state_pool_size, int32_t* status,
+                            int32_t* cu_seqlens_snapshot,
+                            int32_t* state_indices_snapshot, void* stream);
+
+/*
+ * fp32-state recurrent forward over packed varlen sequences, state pool
+ * updated in place at state_indices.
+ * Replaces recurrent_fp32_from_decay_logits_cuda
+ * (csrc/sm120/tmix/wkv7/infer_recurrent_fp32io16_forward_varlen.cu:448-508).
+ * head_size in {64, 128, 256}; io_dtype F16/BF16/F32; decay_bias NULL or
+ * [H*D] of io_dtype (logits mode only). metadata_status is the status word of
+ * frwkv_metadata_validate: when it is non-zero at run time the kernels fill
+ * output with NaN and leave the pool untouched. max_seqlen is the longest
+ * sequence (<= 0: unknown); it selects between the per-token recurrent
+ * kernel and the chunked kernel, never the result beyond rounding.
+ */
+int frwkv_recurrent_forward(int io_dtype, int decay_mode, int32_t num_sequences,
+                            int32_t num_heads, int32_t head_size,
+                            int32_t total_tokens, int32_t max_seqlen,
+                            int32_t state_pool_size, const int32_t* cu_seqlens,
+                            const int32_t* state_indices,
+                            const int32_t* metadata_status, float* state_pool,
+                            const void* r, const void* decay,
+                            const void* decay_bias, const void* k,
+                            const void* v, const void* a, const void* b,
+                            void* output, float scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHRWKV_AMD_H_ */

@@ -1,0 +1,274 @@
+"""WKV7 fp64 oracle -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this module, and only as the checker. The product
+path (``flashrwkv_amd``) never imports it and has no CPU fallback.
+
+Two independent restatements of the reference's naive recurrence
+(``/root/reference/tests/tmix/wkv7/test.py:157-213``) live here:
+
+* :func:`forward` / :func:`backward` call ``libwkv7_oracle.so`` (plain fp64
+  loops in ``wkv7_oracle.c``), fast enough for full-length sampled heads.
+* :func:`forward_einsum` is a numpy einsum restatement (per token, vectorised
+  over heads), used to cross-check the C loops.
+
+Decay transform: :func:`retention_from_logits` restates
+``csrc/sm120/tmix/wkv7/recurrent_decay.cuh:18-22`` (``exp(-e^{-1/2} sigmoid(x))``);
+its log-derivative restates ``:27-32``.
+
+How each function is pinned (see ``tests/test_oracle.py``):
+
+* ``retention_from_logits``: the reference's exp2 constants reproduce the
+  closed form; finite differences pin the log-derivative.
+* ``forward`` / ``forward_einsum``: one-step closed form, the a=b=0 gated
+  linear attention closed form, the w=1, a=b=0 matmul form
+  ``Y = scale * tril(R K^T) V``, the k=0 explicit transition product, joint
+  linearity in (v, S0), permutation invariance of packed sequences, and
+  agreement of the two independent restatements.
+* ``backward``: torch fp64 autograd through an independent per-token torch
+  forward (itself checked against ``forward``), and central finite
+  differences at D=4.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "libwkv7_oracle.so"
+_LIB = None
+
+EXP_NEG_HALF = math.exp(-0.5)
+
+
+def build() -> Path:
+    """Compile ``libwkv7_oracle.so`` with the committed Makefile."""
+    subprocess.run(["make", "-s", "-C", str(_HERE)], check=True)
+    return _LIB_PATH
+
+
+def _lib():
+    global _LIB
+    if _LIB is None:
+        if not _LIB_PATH.exists():
+            build()
+        lib = ctypes.CDLL(str(_LIB_PATH))
+        i32p = ctypes.POINTER(ctypes.c_int32)
+        f64p = ctypes.POINTER(ctypes.c_double)
+        lib.wkv7o_forward.argtypes = [
+            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+            i32p, i32p, i32p, i32p,
+            f64p, f64p, f64p, f64p, f64p, f64p, f64p,
+            ctypes.c_double, f64p, f64p, f64p, ctypes.c_int,
+        ]
+        lib.wkv7o_forward.restype = None
+        lib.wkv7o_backward.argtypes = [
+            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+            i32p, i32p, i32p, i32p,
+            f64p, f64p, f64p, f64p, f64p, f64p, f64p,
+            ctypes.c_double, f64p, f64p,
+            f64p, f64p, f64p, f64p, f64p, f64p, f64p, ctypes.c_int,
+        ]
+        lib.wkv7o_backward.restype = None
+        lib.wkv7o_max_threads.argtypes = []
+        lib.wkv7o_max_threads.restype = ctypes.c_int
+        lib.wkv7o_retention_from_logits.argtypes = [ctypes.c_double]
+        lib.wkv7o_retention_from_logits.restype = ctypes.c_double
+        lib.wkv7o_retention_log_derivative.argtypes = [ctypes.c_double]
+        lib.wkv7o_retention_log_derivative.restype = ctypes.c_double
+        _LIB = lib
+    return _LIB
+
+
+def max_threads() -> int:
+    return int(_lib().wkv7o_max_threads())
+
+
+def _f64(x) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(x, dtype=np.float64))
+
+
+def _i32(x) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(x, dtype=np.int32))
+
+
+def _p(arr: np.ndarray | None, ctype):
+    if arr is None:
+        return ctypes.POINTER(ctype)()
+    return arr.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+# ---------------------------------------------------------------- decay ----
+
+
+def retention_from_logits(x, bias=None) -> np.ndarray:
+    """``exp(-e^{-1/2} * sigmoid(x + bias))`` in fp64 (recurrent_decay.cuh:18-22)."""
+    x = _f64(x)
+    if bias is not None:
+        x = x + _f64(bias).reshape((1,) * (x.ndim - 2) + tuple(x.shape[-2:]))
+    return np.exp(-EXP_NEG_HALF / (1.0 + np.exp(-x)))
+
+
+def retention_log_derivative(x, bias=None) -> np.ndarray:
+    """``d log(retention) / dx = -e^{-1/2} sigma (1 - sigma)`` (recurrent_decay.cuh:27-32)."""
+    x = _f64(x)
+    if bias is not None:
+        x = x + _f64(bias).reshape((1,) * (x.ndim - 2) + tuple(x.shape[-2:]))
+    sig = 1.0 / (1.0 + np.exp(-x))
+    return -EXP_NEG_HALF * sig * (1.0 - sig)
+
+
+# ------------------------------------------------------------- metadata ----
+
+
+def segments_from_cu_seqlens(cu_seqlens):
+    """One segment per packed sequence: (seg_offsets, seg_starts, seg_ends)."""
+    cu = _i32(cu_seqlens)
+    count = cu.shape[0] - 1
+    return (
+        np.arange(count + 1, dtype=np.int32),
+        np.ascontiguousarray(cu[:-1]),
+        np.ascontiguousarray(cu[1:]),
+    )
+
+
+def chunk_metadata(lengths, chunk_size):
+    """StateTune chunk metadata for packed sequences of ``lengths``.
+
+    Mirrors the construction used by the reference's tests
+    (``tests/rl_infctx/wkv7/test.py:56-80``): returns
+    (sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, cu_seqlens).
+    """
+    offsets, starts, ends, cu = [0], [], [], [0]
+    start = 0
+    for length in lengths:
+        end = start + int(length)
+        for s in range(start, end, chunk_size):
+            starts.append(s)
+            ends.append(min(s + chunk_size, end))
+        offsets.append(len(starts))
+        cu.append(end)
+        start = end
+    return _i32(offsets), _i32(starts), _i32(ends), _i32(cu)
+
+
+# -------------------------------------------------------------- forward ----
+
+
+def forward(r, w, k, v, a, b, state, *, seg_offsets, seg_starts, seg_ends,
+            state_slots, scale=1.0, want_boundary=False, want_state_dot_a=False,
+            num_threads=0):
+    """fp64 forward over segments (C loops). ``w`` is the retention.
+
+    ``state`` is a slot pool ``[slots,H,D,D]`` ([K,V]); a copy is updated and
+    returned. Returns ``(y, state_out, boundary or None, state_dot_a or None)``.
+    """
+    r, w, k, v, a, b = (_f64(t) for t in (r, w, k, v, a, b))
+    n, heads, d = r.shape
+    state_out = _f64(state).copy()
+    seg_offsets, seg_starts, seg_ends, state_slots = (
+        _i32(t) for t in (seg_offsets, seg_starts, seg_ends, state_slots)
+    )
+    y = np.zeros((n, heads, d), dtype=np.float64)
+    boundary = (
+        np.zeros((seg_starts.shape[0], heads, d, d), dtype=np.float64)
+        if want_boundary else None
+    )
+    sda = np.zeros((n, heads, d), dtype=np.float64) if want_state_dot_a else None
+    f64, i32 = ctypes.c_double, ctypes.c_int32
+    _lib().wkv7o_forward(
+        int(seg_offsets.shape[0] - 1), heads, d,
+        _p(seg_offsets, i32), _p(seg_starts, i32), _p(seg_ends, i32),
+        _p(state_slots, i32), _p(state_out, f64),
+        _p(r, f64), _p(w, f64), _p(k, f64), _p(v, f64), _p(a, f64), _p(b, f64),
+        float(scale), _p(y, f64), _p(boundary, f64), _p(sda, f64),
+        int(num_threads),
+    )
+    return y, state_out, boundary, sda
+
+
+def forward_varlen(r, w, k, v, a, b, state_pool, cu_seqlens, state_indices,
+                   scale=1.0, num_threads=0):
+    """Inference varlen forward: one segment per packed sequence."""
+    so, ss, se = segments_from_cu_seqlens(cu_seqlens)
+    y, st, _, _ = forward(r, w, k, v, a, b, state_pool, seg_offsets=so,
+                          seg_starts=ss, seg_ends=se, state_slots=state_indices,
+                          scale=scale, num_threads=num_threads)
+    return y, st
+
+
+def backward(r, w, k, v, a, b, initial_state, *, seg_offsets, seg_starts,
+             seg_ends, state_slots, scale=1.0, dy=None, dstate_final=None,
+             num_threads=0):
+    """fp64 adjoint of :func:`forward` (C loops, forward states recomputed).
+
+    Returns ``dict(dr, dw, dk, dv, da, db, dstate0)`` where ``dw`` is dL/d(retention).
+    """
+    r, w, k, v, a, b = (_f64(t) for t in (r, w, k, v, a, b))
+    n, heads, d = r.shape
+    s0 = _f64(initial_state)
+    seg_offsets, seg_starts, seg_ends, state_slots = (
+        _i32(t) for t in (seg_offsets, seg_starts, seg_ends, state_slots)
+    )
+    dy = None if dy is None else _f64(dy)
+    dsf = None if dstate_final is None else _f64(dstate_final)
+    out = {name: np.zeros((n, heads, d)) for name in ("dr", "dw", "dk", "dv", "da", "db")}
+    out["dstate0"] = np.zeros_like(s0)
+    f64, i32 = ctypes.c_double, ctypes.c_int32
+    _lib().wkv7o_backward(
+        int(seg_offsets.shape[0] - 1), heads, d,
+        _p(seg_offsets, i32), _p(seg_starts, i32), _p(seg_ends, i32),
+        _p(state_slots, i32), _p(s0, f64),
+        _p(r, f64), _p(w, f64), _p(k, f64), _p(v, f64), _p(a, f64), _p(b, f64),
+        float(scale), _p(dy, f64), _p(dsf, f64),
+        _p(out["dr"], f64), _p(out["dw"], f64), _p(out["dk"], f64),
+        _p(out["dv"], f64), _p(out["da"], f64), _p(out["db"], f64),
+        _p(out["dstate0"], f64), int(num_threads),
+    )
+    return out
+
+
+def forward_einsum(r, w, k, v, a, b, state_pool, cu_seqlens, state_indices,
+                   scale=1.0):
+    """Independent numpy restatement of test.py:157-213 (per token, all heads)."""
+    r, w, k, v, a, b = (_f64(t) for t in (r, w, k, v, a, b))
+    pool = _f64(state_pool).copy()
+    y = np.zeros_like(r)
+    cu = [int(x) for x in np.asarray(cu_seqlens)]
+    slots = [int(x) for x in np.asarray(state_indices)]
+    for seq, (start, end) in enumerate(zip(cu[:-1], cu[1:])):
+        s = pool[slots[seq]].copy()
+        for t in range(start, end):
+            sa = np.einsum("hk,hkv->hv", a[t], s)
+            s = w[t][:, :, None] * s + b[t][:, :, None] * sa[:, None, :] \
+                + k[t][:, :, None] * v[t][:, None, :]
+            y[t] = scale * np.einsum("hk,hkv->hv", r[t], s)
+        pool[slots[seq]] = s
+    return y, pool
+
+
+# ------------------------------------------------------------- metrics -----
+
+
+def max_rel_error(actual, expected) -> float:
+    """Normwise max relative error ``max|x - x_ref| / max|x_ref|``."""
+    actual = np.asarray(actual, dtype=np.float64)
+    expected = np.asarray(expected, dtype=np.float64)
+    denom = float(np.max(np.abs(expected))) if expected.size else 0.0
+    if denom == 0.0:
+        denom = 1.0
+    return float(np.max(np.abs(actual - expected)) / denom) if expected.size else 0.0
+
+
+def relative_rmse(actual, expected) -> float:
+    """The reference's relative-RMSE metric (tests/tmix/wkv7/test.py:304-307)."""
+    actual = np.asarray(actual, dtype=np.float64)
+    expected = np.asarray(expected, dtype=np.float64)
+    base = max(float(np.sqrt(np.mean(expected ** 2))), 1.0e-6)
+    return float(np.sqrt(np.mean((actual - expected) ** 2)) / base)

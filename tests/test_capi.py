@@ -1,0 +1,68 @@
+"""CPU checks of the C ABI: the library loads and exports every declared entry
+point, and argument errors are reported without touching a GPU."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch  # noqa: F401  (loads the HIP runtime the library binds to)
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+LIB_PATH = ROOT / "flashrwkv_amd" / "libflashrwkv_amd.so"
+
+DECL = re.compile(r"^[A-Za-z_][\w\s\*]*?\b(frwkv_\w+)\s*\(", re.MULTILINE)
+
+
+def declared_symbols() -> list[str]:
+    names = []
+    for header in HEADERS:
+        text = header.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.DOTALL)
+        names.extend(DECL.findall(text))
+    return sorted(set(names))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not LIB_PATH.exists():
+        pytest.fail(f"{LIB_PATH} is not built; run python -m flashrwkv_amd._build")
+    return ctypes.CDLL(str(LIB_PATH))
+
+
+def test_header_declares_entry_points():
+    names = declared_symbols()
+    for required in ("frwkv_abi_version", "frwkv_status_string", "frwkv_last_error",
+                     "frwkv_metadata_validate", "frwkv_recurrent_forward"):
+        assert required in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    missing = [name for name in declared_symbols() if not hasattr(lib, name)]
+    assert not missing, missing
+
+
+def test_version_and_status_strings(lib):
+    lib.frwkv_abi_version.restype = ctypes.c_int
+    header = (ROOT / "include" / "flashrwkv_amd.h").read_text()
+    version = int(re.search(r"#define FRWKV_ABI_VERSION (\d+)", header).group(1))
+    assert lib.frwkv_abi_version() == version
+    lib.frwkv_status_string.restype = ctypes.c_char_p
+    assert lib.frwkv_status_string(0) == b"ok"
+    assert lib.frwkv_status_string(1) == b"invalid argument"
+    assert lib.frwkv_status_string(99) == b"unknown status"
+
+
+def test_null_pointers_are_rejected_before_any_launch(lib):
+    lib.frwkv_last_error.restype = ctypes.c_char_p
+    null = ctypes.c_void_p()
+    rc = lib.frwkv_metadata_validate(null, null, 1, 1, 1, null, null, null, null)
+    assert rc == 1
+    assert b"null pointer" in lib.frwkv_last_error()
+    args = [ctypes.c_int(2), ctypes.c_int(0)] + [ctypes.c_int32(1)] * 6 + [null] * 13 \
+        + [ctypes.c_float(1.0), null]
+    assert lib.frwkv_recurrent_forward(*args) == 1
+    assert b"null pointer" in lib.frwkv_last_error()

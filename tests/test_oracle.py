@@ -1,0 +1,284 @@
+"""Pins the fp64 oracle (oracle/) before any GPU result is compared with it.
+
+Each check is chosen so that a plausible slip in the oracle (dropped term,
+wrong sign, transposed state, off-by-one in the token loop, wrong decay
+constant) fails at least one of them. None of them restates the oracle's own
+loop: closed forms, independent restatements, autograd and finite
+differences supply the expected values.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+
+RNG = np.random.default_rng(1234)
+
+
+def _tokens(n, h, d, *, rng=RNG, w_range=(0.3, 0.999)):
+    r = rng.standard_normal((n, h, d))
+    k = rng.standard_normal((n, h, d))
+    v = rng.standard_normal((n, h, d))
+    w = rng.uniform(*w_range, size=(n, h, d))
+    kk = rng.standard_normal((n, h, d))
+    kk /= np.linalg.norm(kk, axis=-1, keepdims=True)
+    g = 1.0 / (1.0 + np.exp(-rng.standard_normal((n, h, d))))
+    return r, w, k, v, -kk, kk * g
+
+
+def _single(lengths, h=2, d=8, *, rng=RNG, state_std=0.3, slots=None, pool=None):
+    n = sum(lengths)
+    toks = _tokens(n, h, d, rng=rng)
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    if slots is None:
+        slots = np.arange(len(lengths), dtype=np.int32)
+    slots = np.asarray(slots, dtype=np.int32)
+    if pool is None:
+        pool = rng.standard_normal((max(slots) + 1, h, d, d)) * state_std
+    return toks, cu, slots, pool
+
+
+# ------------------------------------------------------------------ decay --
+
+
+def test_reference_exp2_constants_restate_closed_form():
+    # recurrent_decay.cuh:10-12 constants.
+    assert math.isclose(-0.8750387749145276, -math.exp(-0.5) * math.log2(math.e), rel_tol=1e-15)
+    assert math.isclose(-1.4426950408889634, -math.log2(math.e), rel_tol=1e-15)
+    assert math.isclose(0.6065306597126334, math.exp(-0.5), rel_tol=1e-15)
+    x = np.linspace(-12, 12, 97)
+    exp2_form = np.exp2(-0.8750387749145276 / (1.0 + np.exp2(-1.4426950408889634 * x)))
+    np.testing.assert_allclose(oracle.retention_from_logits(x.reshape(1, -1, 1)).ravel(),
+                               exp2_form, rtol=1e-14)
+    # Range of the logits transform: (exp(-e^{-1/2}), 1).
+    assert oracle.retention_from_logits(np.array([[[-40.0]]])).item() > 0.9999999
+    assert math.isclose(oracle.retention_from_logits(np.array([[[40.0]]])).item(),
+                        math.exp(-math.exp(-0.5)), rel_tol=1e-12)
+
+
+def test_retention_log_derivative_matches_finite_difference():
+    x = np.linspace(-6, 6, 41).reshape(1, -1, 1)
+    h = 1e-6
+    fd = (np.log(oracle.retention_from_logits(x + h)) -
+          np.log(oracle.retention_from_logits(x - h))) / (2 * h)
+    np.testing.assert_allclose(oracle.retention_log_derivative(x), fd, rtol=1e-7, atol=1e-10)
+
+
+def test_bias_broadcasts_per_head_feature():
+    x = RNG.standard_normal((3, 2, 4))
+    bias = RNG.standard_normal((2, 4))
+    np.testing.assert_allclose(oracle.retention_from_logits(x, bias),
+                               oracle.retention_from_logits(x + bias[None]), rtol=1e-15)
+
+
+# -------------------------------------------------------- forward closed forms --
+
+
+def test_one_step_closed_form_general_state():
+    (r, w, k, v, a, b), cu, slots, pool = _single([1], h=3, d=6)
+    scale = 0.7
+    y, pool_out = oracle.forward_varlen(r, w, k, v, a, b, pool, cu, slots, scale)
+    for h in range(3):
+        s0 = pool[0, h]
+        s1 = np.diag(w[0, h]) @ s0 + np.outer(b[0, h], a[0, h] @ s0) + np.outer(k[0, h], v[0, h])
+        np.testing.assert_allclose(pool_out[0, h], s1, rtol=1e-13, atol=1e-13)
+        np.testing.assert_allclose(y[0, h], scale * s1.T @ r[0, h], rtol=1e-13, atol=1e-13)
+
+
+def test_zero_state_one_step_is_scaled_dot_product():
+    (r, w, k, v, a, b), cu, slots, _ = _single([1], h=2, d=5)
+    pool = np.zeros((1, 2, 5, 5))
+    y, _ = oracle.forward_varlen(r, w, k, v, a, b, pool, cu, slots, 1.5)
+    expected = 1.5 * np.einsum("hd,hd->h", r[0], k[0])[:, None] * v[0]
+    np.testing.assert_allclose(y[0], expected, rtol=1e-13, atol=1e-13)
+
+
+def test_unit_decay_no_delta_is_causal_linear_attention():
+    t, d = 23, 7
+    (r, _, k, v, _, _), cu, slots, _ = _single([t], h=1, d=d)
+    w = np.ones_like(r)
+    zeros = np.zeros_like(r)
+    pool = np.zeros((1, 1, d, d))
+    y, _ = oracle.forward_varlen(r, w, k, v, zeros, zeros, pool, cu, slots, 0.5)
+    R, K, V = r[:, 0], k[:, 0], v[:, 0]
+    expected = 0.5 * np.tril(R @ K.T) @ V
+    np.testing.assert_allclose(y[:, 0], expected, rtol=1e-12, atol=1e-12)
+
+
+def test_no_delta_is_gated_linear_attention_with_initial_state():
+    t, d = 19, 6
+    (r, w, k, v, _, _), cu, slots, pool = _single([t], h=1, d=d)
+    zeros = np.zeros_like(r)
+    y, pool_out = oracle.forward_varlen(r, w, k, v, zeros, zeros, pool, cu, slots, 1.0)
+    W = w[:, 0]
+    logc = np.cumsum(np.log(W), axis=0)  # log prod_{j<=t} w_j
+    for tt in range(t):
+        acc = (r[tt, 0] * np.exp(logc[tt])) @ pool[0, 0]
+        for i in range(tt + 1):
+            decay = np.exp(logc[tt] - logc[i])  # prod_{i<j<=t} w_j
+            acc = acc + ((r[tt, 0] * decay) @ k[i, 0]) * v[i, 0]
+        np.testing.assert_allclose(y[tt, 0], acc, rtol=1e-11, atol=1e-11)
+
+
+def test_zero_key_is_product_of_transitions():
+    t, d = 9, 5
+    (r, w, k, v, a, b), cu, slots, pool = _single([t], h=1, d=d)
+    k = np.zeros_like(k)
+    _, pool_out = oracle.forward_varlen(r, w, k, v, a, b, pool, cu, slots, 1.0)
+    s = pool[0, 0]
+    for tt in range(t):
+        m = np.diag(w[tt, 0]) + np.outer(b[tt, 0], a[tt, 0])
+        s = m @ s
+    np.testing.assert_allclose(pool_out[0, 0], s, rtol=1e-12, atol=1e-12)
+
+
+def test_joint_linearity_in_values_and_initial_state():
+    (r, w, k, v1, a, b), cu, slots, pool1 = _single([5, 11], h=2, d=6)
+    v2 = RNG.standard_normal(v1.shape)
+    pool2 = RNG.standard_normal(pool1.shape)
+    al, be = 0.8, -1.7
+    y1, s1 = oracle.forward_varlen(r, w, k, v1, a, b, pool1, cu, slots)
+    y2, s2 = oracle.forward_varlen(r, w, k, v2, a, b, pool2, cu, slots)
+    y3, s3 = oracle.forward_varlen(r, w, k, al * v1 + be * v2, a, b,
+                                   al * pool1 + be * pool2, cu, slots)
+    np.testing.assert_allclose(y3, al * y1 + be * y2, rtol=1e-10, atol=1e-10)
+    np.testing.assert_allclose(s3, al * s1 + be * s2, rtol=1e-10, atol=1e-10)
+
+
+def test_packing_permutation_and_slot_mapping_invariance():
+    lengths = [3, 1, 7]
+    (r, w, k, v, a, b), cu, _, _ = _single(lengths, h=2, d=4)
+    pool = RNG.standard_normal((6, 2, 4, 4))
+    slots = np.array([4, 0, 2], dtype=np.int32)
+    y, out = oracle.forward_varlen(r, w, k, v, a, b, pool, cu, slots)
+    order = [2, 0, 1]
+    pieces = [np.arange(cu[i], cu[i + 1]) for i in order]
+    idx = np.concatenate(pieces)
+    cu2 = np.concatenate([[0], np.cumsum([lengths[i] for i in order])]).astype(np.int32)
+    y2, out2 = oracle.forward_varlen(*(t[idx] for t in (r, w, k, v, a, b)), pool, cu2,
+                                     slots[order])
+    np.testing.assert_allclose(y2, y[idx], rtol=1e-13, atol=1e-13)
+    np.testing.assert_allclose(out2, out, rtol=1e-13, atol=1e-13)
+    untouched = [1, 3, 5]
+    np.testing.assert_array_equal(out[untouched], pool[untouched])
+
+
+def test_c_loops_match_independent_einsum_restatement():
+    lengths = [1, 15, 16, 17, 65]
+    (r, w, k, v, a, b), cu, _, _ = _single(lengths, h=2, d=16)
+    pool = RNG.standard_normal((9, 2, 16, 16)) * 0.03
+    slots = np.array([5, 0, 7, 2, 4], dtype=np.int32)
+    y1, s1 = oracle.forward_varlen(r, w, k, v, a, b, pool, cu, slots, 0.9)
+    y2, s2 = oracle.forward_einsum(r, w, k, v, a, b, pool, cu, slots, 0.9)
+    np.testing.assert_allclose(y1, y2, rtol=1e-11, atol=1e-12)
+    np.testing.assert_allclose(s1, s2, rtol=1e-11, atol=1e-12)
+
+
+def test_segmentation_invariance_and_boundaries():
+    lengths = [37, 9]
+    (r, w, k, v, a, b), _, _, _ = _single(lengths, h=2, d=8)
+    s0 = RNG.standard_normal((2, 2, 8, 8)) * 0.1
+    so, ss, se, cu = oracle.chunk_metadata(lengths, 8)
+    y_c, st_c, boundary, sda = oracle.forward(
+        r, w, k, v, a, b, s0, seg_offsets=so, seg_starts=ss, seg_ends=se,
+        state_slots=np.arange(2), want_boundary=True, want_state_dot_a=True)
+    y_1, st_1 = oracle.forward_varlen(r, w, k, v, a, b, s0, cu, np.arange(2))
+    np.testing.assert_allclose(y_c, y_1, rtol=1e-13, atol=1e-13)
+    np.testing.assert_allclose(st_c, st_1, rtol=1e-13, atol=1e-13)
+    # boundary of a sequence's first chunk is S0; later ones are the state
+    # after running the sequence prefix through the single-segment path.
+    for seq in range(2):
+        for c in range(so[seq], so[seq + 1]):
+            start = ss[c]
+            prefix = start - cu[seq]
+            if prefix == 0:
+                np.testing.assert_array_equal(boundary[c], s0[seq])
+            else:
+                sl = slice(cu[seq], start)
+                _, st_prefix = oracle.forward_varlen(
+                    *(t[sl] for t in (r, w, k, v, a, b)), s0[seq:seq + 1],
+                    np.array([0, prefix], dtype=np.int32), np.zeros(1, dtype=np.int32))
+                np.testing.assert_allclose(boundary[c], st_prefix[0], rtol=1e-12, atol=1e-12)
+    # state_dot_a[t] = a_t^T S_{t-1}: at a sequence's first token, S_{t-1} = S0.
+    for seq in range(2):
+        t0 = cu[seq]
+        np.testing.assert_allclose(sda[t0], np.einsum("hk,hkv->hv", a[t0], s0[seq]),
+                                   rtol=1e-13, atol=1e-13)
+
+
+# ---------------------------------------------------------------- backward --
+
+
+def _torch_forward(r, w, k, v, a, b, s0, scale):
+    """Independent per-token torch restatement for autograd (one sequence)."""
+    s = s0
+    ys = []
+    for t in range(r.shape[0]):
+        sa = torch.einsum("hk,hkv->hv", a[t], s)
+        s = w[t].unsqueeze(-1) * s + b[t].unsqueeze(-1) * sa.unsqueeze(-2) \
+            + k[t].unsqueeze(-1) * v[t].unsqueeze(-2)
+        ys.append(scale * torch.einsum("hk,hkv->hv", r[t], s))
+    return torch.stack(ys), s
+
+
+def test_backward_matches_fp64_autograd():
+    lengths = [13]
+    (r, w, k, v, a, b), cu, slots, pool = _single(lengths, h=2, d=6)
+    scale = 0.75
+    dy = RNG.standard_normal(r.shape)
+    dsf = RNG.standard_normal(pool.shape) * 0.1
+    so, ss, se = oracle.segments_from_cu_seqlens(cu)
+    grads = oracle.backward(r, w, k, v, a, b, pool, seg_offsets=so, seg_starts=ss,
+                            seg_ends=se, state_slots=slots, scale=scale, dy=dy,
+                            dstate_final=dsf)
+    tens = [torch.tensor(x, requires_grad=True) for x in (r, w, k, v, a, b)]
+    s0 = torch.tensor(pool[0], requires_grad=True)
+    y_t, s_t = _torch_forward(*tens, s0, scale)
+    y_o, s_o = oracle.forward_varlen(r, w, k, v, a, b, pool, cu, slots, scale)
+    np.testing.assert_allclose(y_t.detach().numpy(), y_o, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(s_t.detach().numpy(), s_o[0], rtol=1e-12, atol=1e-12)
+    loss = (y_t * torch.tensor(dy)).sum() + (s_t * torch.tensor(dsf[0])).sum()
+    loss.backward()
+    for name, t in zip(("dr", "dw", "dk", "dv", "da", "db"), tens):
+        np.testing.assert_allclose(grads[name], t.grad.numpy(), rtol=1e-10, atol=1e-11,
+                                   err_msg=name)
+    np.testing.assert_allclose(grads["dstate0"][0], s0.grad.numpy(), rtol=1e-10, atol=1e-11)
+
+
+def test_backward_central_finite_differences_tiny():
+    (r, w, k, v, a, b), cu, slots, pool = _single([4, 3], h=1, d=4)
+    dy = RNG.standard_normal(r.shape)
+    dsf = RNG.standard_normal(pool.shape)
+    so, ss, se = oracle.segments_from_cu_seqlens(cu)
+
+    def loss(rr, ww, kk_, vv, aa, bb, p):
+        y, s = oracle.forward_varlen(rr, ww, kk_, vv, aa, bb, p, cu, slots, 1.1)
+        return float(np.sum(y * dy) + np.sum(s * dsf))
+
+    grads = oracle.backward(r, w, k, v, a, b, pool, seg_offsets=so, seg_starts=ss,
+                            seg_ends=se, state_slots=slots, scale=1.1, dy=dy,
+                            dstate_final=dsf)
+    base = [r, w, k, v, a, b, pool]
+    names = ["dr", "dw", "dk", "dv", "da", "db", "dstate0"]
+    eps = 1e-6
+    for which, name in enumerate(names):
+        arr = base[which]
+        for flat in RNG.choice(arr.size, size=6, replace=False):
+            idx = np.unravel_index(flat, arr.shape)
+            plus = [x.copy() for x in base]
+            minus = [x.copy() for x in base]
+            plus[which][idx] += eps
+            minus[which][idx] -= eps
+            fd = (loss(*plus) - loss(*minus)) / (2 * eps)
+            assert abs(fd - grads[name][idx]) <= 1e-6 * max(1.0, abs(fd)), (name, idx)
+
+
+def test_metrics_are_normwise():
+    ref = np.array([1.0, -4.0, 2.0])
+    assert oracle.max_rel_error(ref + np.array([0.0, 0.4, 0.0]), ref) == pytest.approx(0.1)
+    assert oracle.relative_rmse(ref, ref) == 0.0

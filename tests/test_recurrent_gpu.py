@@ -1,0 +1,368 @@
+"""GPU parity and contract tests of the fp32-state recurrent operator.
+
+Case construction follows the reference's tests (tests/tmix/wkv7/test.py:417-477:
+lengths (1,15,16,17,65), permuted slots [5,0,7,2,4], input scales r 0.12,
+logits 3.5, k/v/a/b 0.06, pool 0.03), but expected values come from the fp64
+oracle fed the same cast inputs. Tolerances (normwise max relative error):
+fp32 tokens 1e-5; fp16/bf16 outputs 2e-2; fp32 state 1e-4 with 16-bit
+tokens. The reference's relative-RMSE gate (0.002, tests/fixtures/
+tolerances-v1.json:9-12) is checked as well.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import flashrwkv_amd
+from flashrwkv_amd import workloads
+from flashrwkv_amd.tmix.wkv7 import (
+    DECAY_LOGITS,
+    DECAY_RAW_W,
+    infer_recurrent_fp32io16_forward_varlen,
+    prepare_recurrent_metadata,
+    recurrent_forward_internal,
+)
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL_Y = {torch.float32: 1e-5, torch.float16: 2e-2, torch.bfloat16: 2e-2}
+TOL_STATE_16 = 1e-4
+REF_RMSE = 0.002
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _require_native():
+    if flashrwkv_amd._C is None:
+        pytest.fail("flashrwkv_amd native library is not built (no fallback exists)")
+    if not torch.cuda.is_available():
+        pytest.fail("a GPU is required for tests marked gpu")
+
+
+DEV = torch.device("cuda")
+
+
+def _np(t):
+    return t.detach().double().cpu().numpy()
+
+
+def _reference_case(*, dtype, head_size, lengths=(1, 15, 16, 17, 65), bias=False,
+                    heads=2, seed=0):
+    g = torch.Generator().manual_seed(20260804 + head_size + int(bias) + seed)
+    total = sum(lengths)
+    shape = (total, heads, head_size)
+
+    def rnd(scale):
+        return (torch.randn(shape, generator=g) * scale).to(dtype)
+
+    offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    slots = [5, 0, 7, 2, 4][: len(lengths)] if len(lengths) <= 5 else list(range(len(lengths)))
+    pool = torch.randn((max(9, len(lengths)), heads, head_size, head_size), generator=g) * 0.03
+    case = {
+        "r": rnd(0.12), "decay_logits": rnd(3.5), "k": rnd(0.06), "v": rnd(0.06),
+        "a": rnd(0.06), "b": rnd(0.06),
+        "cu_seqlens": torch.tensor(offsets, dtype=torch.int32),
+        "state_indices": torch.tensor(slots, dtype=torch.int32),
+        "state_pool": pool,
+        "decay_bias": (torch.randn((heads, head_size), generator=g) * 0.2).to(dtype)
+        if bias else None,
+    }
+    return case
+
+
+def _to_dev(case):
+    return {k: (v.to(DEV) if isinstance(v, torch.Tensor) else v) for k, v in case.items()}
+
+
+def _oracle_logits(case, scale=1.0):
+    names = ("r", "decay_logits", "k", "v", "a", "b")
+    r, x, k, v, a, b = (_np(case[n]) for n in names)
+    bias = None if case["decay_bias"] is None else _np(case["decay_bias"])
+    w = oracle.retention_from_logits(x, bias)
+    return oracle.forward_varlen(r, w, k, v, a, b, _np(case["state_pool"]),
+                                 case["cu_seqlens"].numpy(), case["state_indices"].numpy(),
+                                 scale)
+
+
+ARGS = ("r", "decay_logits", "k", "v", "a", "b")
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("head_size", (64, 128, 256))
+@pytest.mark.parametrize("with_bias", (False, True))
+def test_public_precision_untouched_slots_and_determinism(dtype, head_size, with_bias):
+    print(f"case dtype={dtype} D={head_size} bias={with_bias}", flush=True)
+    case = _reference_case(dtype=dtype, head_size=head_size, bias=with_bias)
+    dev = _to_dev(case)
+    before = dev["state_pool"].clone()
+    y = infer_recurrent_fp32io16_forward_varlen(
+        *(dev[n] for n in ARGS), state_pool=dev["state_pool"],
+        cu_seqlens=dev["cu_seqlens"], state_indices=dev["state_indices"],
+        decay_bias=dev["decay_bias"])
+    torch.cuda.synchronize()
+    y_ref, pool_ref = _oracle_logits(case)
+    assert y.dtype == dtype and y.shape == dev["v"].shape
+    active = case["state_indices"].long().numpy()
+    pool = _np(dev["state_pool"])
+    assert oracle.max_rel_error(_np(y), y_ref) <= TOL_Y[dtype]
+    assert oracle.relative_rmse(_np(y), y_ref) <= REF_RMSE
+    assert oracle.max_rel_error(pool[active], pool_ref[active]) <= TOL_STATE_16
+    untouched = [i for i in range(pool.shape[0]) if i not in set(active.tolist())]
+    assert torch.equal(dev["state_pool"][untouched], before[untouched])
+    # Bitwise determinism on re-run from the same state.
+    second = before.clone()
+    y2 = infer_recurrent_fp32io16_forward_varlen(
+        *(dev[n] for n in ARGS), state_pool=second, cu_seqlens=dev["cu_seqlens"],
+        state_indices=dev["state_indices"], decay_bias=dev["decay_bias"])
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    assert torch.equal(dev["state_pool"], second)
+
+
+def _baseline_case(lengths, heads, dtype, seed, state_std, u_low=-5.0):
+    return workloads.make_case(lengths=lengths, heads=heads, head_size=64, dtype=dtype,
+                               seed=seed, state_std=state_std, u_low=u_low)
+
+
+def _run_raw(case, max_seqlen=None, scale=1.0):
+    dev = _to_dev(case)
+    y = recurrent_forward_internal(
+        dev["r"], dev["w"], dev["k"], dev["v"], dev["a"], dev["b"],
+        state_pool=dev["state_pool"], cu_seqlens=dev["cu_seqlens"],
+        state_indices=dev["state_indices"], decay_mode=DECAY_RAW_W, scale=scale,
+        max_seqlen=max_seqlen)
+    torch.cuda.synchronize()
+    return y, dev["state_pool"]
+
+
+def _oracle_raw(case, scale=1.0):
+    return oracle.forward_varlen(*(_np(case[n]) for n in ("r", "w", "k", "v", "a", "b")),
+                                 _np(case["state_pool"]), case["cu_seqlens"].numpy(),
+                                 case["state_indices"].numpy(), scale)
+
+
+def test_config0_fp32_matches_fp64_oracle_to_1e5():
+    print("case config0 fp32 B=1 T=64 H=32", flush=True)
+    case = _baseline_case([64], 32, torch.float32, seed=20260804, state_std=0.0)
+    y, pool = _run_raw(case)
+    y_ref, pool_ref = _oracle_raw(case)
+    assert oracle.max_rel_error(_np(y), y_ref) <= 1e-5
+    assert oracle.max_rel_error(_np(pool), pool_ref) <= 1e-5
+
+
+def test_config1_decode_full_shape_three_steps():
+    print("case config1 decode B=256 H=40, 3 steps", flush=True)
+    b, h = 256, 40
+    first = _baseline_case([1] * b, h, torch.bfloat16, seed=20260805, state_std=0.1)
+    pool_dev = first["state_pool"].to(DEV)
+    pool_ref = _np(first["state_pool"])
+    for step in range(3):
+        case = _baseline_case([1] * b, h, torch.bfloat16, seed=20260805 + step, state_std=0.1)
+        dev = _to_dev(case)
+        y = recurrent_forward_internal(
+            dev["r"], dev["w"], dev["k"], dev["v"], dev["a"], dev["b"], state_pool=pool_dev,
+            cu_seqlens=dev["cu_seqlens"], state_indices=dev["state_indices"],
+            decay_mode=DECAY_RAW_W, max_seqlen=1)
+        torch.cuda.synchronize()
+        y_ref, pool_ref = oracle.forward_varlen(
+            *(_np(case[n]) for n in ("r", "w", "k", "v", "a", "b")), pool_ref,
+            case["cu_seqlens"].numpy(), case["state_indices"].numpy())
+        assert oracle.max_rel_error(_np(y), y_ref) <= TOL_Y[torch.bfloat16]
+        assert oracle.max_rel_error(_np(pool_dev), pool_ref) <= TOL_STATE_16
+
+
+def test_config2_long_sequences_subset_of_batch():
+    # Sequences and heads are independent, so two of config 2's eight
+    # sequences at full length (T=4096, H=32) check the same per-unit work.
+    print("case config2 B=2(of 8) T=4096 H=32", flush=True)
+    case = _baseline_case([4096, 4096], 32, torch.bfloat16, seed=20260806, state_std=0.0)
+    y, pool = _run_raw(case)
+    y_ref, pool_ref = _oracle_raw(case)
+    assert oracle.max_rel_error(_np(y), y_ref) <= TOL_Y[torch.bfloat16]
+    assert oracle.max_rel_error(_np(pool), pool_ref) <= 1e-3
+
+
+@pytest.mark.parametrize("lengths", [(1,), (2, 3), (1, 1, 1, 1, 1), (9, 1, 33, 4)])
+@pytest.mark.parametrize("head_size", (64, 128, 256))
+def test_raw_retention_fp32_tokens_ragged(lengths, head_size):
+    print(f"case raw fp32 lengths={lengths} D={head_size}", flush=True)
+    case = workloads.make_case(lengths=lengths, heads=3, head_size=head_size,
+                               dtype=torch.float32, seed=11 + head_size, state_std=0.1,
+                               pool_slots=len(lengths) + 2,
+                               slots=list(range(len(lengths) + 1, 0, -1))[: len(lengths)])
+    y, pool = _run_raw(case, scale=0.5)
+    y_ref, pool_ref = _oracle_raw(case, scale=0.5)
+    assert oracle.max_rel_error(_np(y), y_ref) <= 1e-5
+    assert oracle.max_rel_error(_np(pool), pool_ref) <= 1e-5
+
+
+@pytest.mark.parametrize(
+    "kind",
+    ["wrong_rank", "wrong_length", "wrong_dtype", "wrong_start", "wrong_end",
+     "non_increasing", "empty_sequence", "wrong_slot_length", "duplicate_slot",
+     "negative_slot", "out_of_range_slot"],
+)
+def test_public_rejects_invalid_metadata_and_preserves_state(kind):
+    dev = _to_dev(_reference_case(dtype=torch.bfloat16, head_size=64))
+    cu, slots, pool = dev["cu_seqlens"], dev["state_indices"], dev["state_pool"]
+    bad_cu, bad_slots = cu, slots
+    if kind == "wrong_rank":
+        bad_cu = cu.reshape(1, -1)
+    elif kind == "wrong_length":
+        bad_cu = cu[:-1]
+    elif kind == "wrong_dtype":
+        bad_cu = cu.to(torch.int64)
+    elif kind == "wrong_start":
+        bad_cu = cu + 1
+    elif kind == "wrong_end":
+        bad_cu = cu.clone()
+        bad_cu[-1] -= 1
+    elif kind in ("non_increasing", "empty_sequence"):
+        bad_cu = cu.clone()
+        bad_cu[2] = bad_cu[1]
+    elif kind == "wrong_slot_length":
+        bad_slots = slots[:-1]
+    elif kind == "duplicate_slot":
+        bad_slots = slots.clone()
+        bad_slots[1] = bad_slots[0]
+    elif kind == "negative_slot":
+        bad_slots = slots.clone()
+        bad_slots[0] = -1
+    else:
+        bad_slots = slots.clone()
+        bad_slots[0] = pool.shape[0]
+    before = pool.clone()
+    with pytest.raises((TypeError, ValueError, RuntimeError)):
+        infer_recurrent_fp32io16_forward_varlen(
+            *(dev[n] for n in ARGS), state_pool=pool, cu_seqlens=bad_cu,
+            state_indices=bad_slots)
+    torch.cuda.synchronize()
+    assert torch.equal(pool, before)
+
+
+def test_low_level_invalid_metadata_fails_closed_without_state_write():
+    case = _to_dev(_reference_case(dtype=torch.float16, head_size=64, lengths=(4,)))
+    pool = case["state_pool"]
+    bad_cu = torch.tensor([1, 4], device=DEV, dtype=torch.int32)
+    slots = torch.tensor([0], device=DEV, dtype=torch.int32)
+    out = torch.zeros_like(case["v"])
+    before = pool.clone()
+    flashrwkv_amd._C.recurrent_fp32_from_decay_logits(
+        bad_cu, slots, pool, *(case[n] for n in ARGS), out, 1.0, None, None)
+    torch.cuda.synchronize()
+    assert torch.isnan(out).all()
+    assert torch.equal(pool, before)
+
+
+def test_ticket_rejects_identity_size_version_and_stream_mismatch():
+    dev = _to_dev(_reference_case(dtype=torch.bfloat16, head_size=64, lengths=(4, 5)))
+    args = tuple(dev[n] for n in ARGS)
+    cu, slots, pool = dev["cu_seqlens"], dev["state_indices"], dev["state_pool"]
+    ticket = prepare_recurrent_metadata(cu, slots, total_tokens=9, state_pool_size=pool.shape[0])
+    with pytest.raises(RuntimeError, match="identity"):
+        infer_recurrent_fp32io16_forward_varlen(*args, state_pool=pool.clone(),
+                                                cu_seqlens=cu.clone(), state_indices=slots,
+                                                validated_metadata=ticket)
+    short = tuple(t[:-1].contiguous() for t in args)
+    with pytest.raises(RuntimeError, match="total_tokens"):
+        infer_recurrent_fp32io16_forward_varlen(*short, state_pool=pool.clone(),
+                                                cu_seqlens=cu, state_indices=slots,
+                                                validated_metadata=ticket)
+    with pytest.raises(RuntimeError, match="state_pool_size"):
+        infer_recurrent_fp32io16_forward_varlen(
+            *args, state_pool=torch.cat((pool, pool[:1])), cu_seqlens=cu,
+            state_indices=slots, validated_metadata=ticket)
+    cu[1] += 1
+    with pytest.raises(RuntimeError, match="version"):
+        infer_recurrent_fp32io16_forward_varlen(*args, state_pool=pool.clone(),
+                                                cu_seqlens=cu, state_indices=slots,
+                                                validated_metadata=ticket)
+    cu[1] -= 1
+    ticket2 = prepare_recurrent_metadata(cu, slots, total_tokens=9, state_pool_size=pool.shape[0])
+    other = torch.cuda.Stream(device=DEV)
+    with torch.cuda.stream(other):
+        with pytest.raises(RuntimeError, match="stream"):
+            infer_recurrent_fp32io16_forward_varlen(*args, state_pool=pool.clone(),
+                                                    cu_seqlens=cu, state_indices=slots,
+                                                    validated_metadata=ticket2)
+    other.synchronize()
+
+
+def test_structural_rejections():
+    dev = _to_dev(_reference_case(dtype=torch.float16, head_size=64))
+    args = tuple(dev[n] for n in ARGS)
+    pool, cu, slots = dev["state_pool"], dev["cu_seqlens"], dev["state_indices"]
+
+    def call(*a, **kw):
+        kw.setdefault("state_pool", pool)
+        kw.setdefault("cu_seqlens", cu)
+        kw.setdefault("state_indices", slots)
+        return infer_recurrent_fp32io16_forward_varlen(*a, **kw)
+
+    bad = torch.zeros((args[0].shape[0], args[0].shape[1], 63), device=DEV,
+                      dtype=args[0].dtype)
+    with pytest.raises(ValueError, match="contiguous"):
+        call(args[0].transpose(0, 1), *args[1:])
+    with pytest.raises(RuntimeError, match="shape"):
+        call(bad, *args[1:])
+    with pytest.raises(RuntimeError, match="float16 or bfloat16"):
+        call(args[0].float(), *args[1:])
+    with pytest.raises(RuntimeError, match="dtype mismatch"):
+        call(args[0], args[1].to(torch.bfloat16), *args[2:])
+    with pytest.raises(TypeError, match="float32"):
+        call(*args, state_pool=pool.half())
+    with pytest.raises(RuntimeError, match="square"):
+        call(*args, state_pool=pool[:, :, :, :-1].contiguous())
+    with pytest.raises(RuntimeError, match="decay_bias"):
+        call(*args, decay_bias=torch.zeros(2, 63, device=DEV, dtype=args[0].dtype))
+    with pytest.raises(RuntimeError, match="decay_bias"):
+        call(*args, decay_bias=torch.zeros(2, 64, device=DEV, dtype=torch.float32))
+    with pytest.raises(RuntimeError, match="contiguous"):
+        call(*args, decay_bias=torch.zeros(64, 2, device=DEV, dtype=args[0].dtype).t())
+    for s in (float("nan"), float("inf")):
+        with pytest.raises(RuntimeError, match="finite"):
+            call(*args, scale=s)
+    small = _to_dev(_reference_case(dtype=torch.float16, head_size=32, lengths=(4,)))
+    with pytest.raises(RuntimeError, match="64, 128, or 256"):
+        infer_recurrent_fp32io16_forward_varlen(
+            *(small[n] for n in ARGS), state_pool=small["state_pool"],
+            cu_seqlens=small["cu_seqlens"], state_indices=small["state_indices"])
+    with pytest.raises((ValueError, RuntimeError), match="CUDA"):
+        infer_recurrent_fp32io16_forward_varlen(
+            *(t.cpu() for t in args), state_pool=pool.cpu(), cu_seqlens=cu.cpu(),
+            state_indices=slots.cpu())
+
+
+def test_graph_capture_with_ticket_replays_match_eager():
+    case = workloads.make_case(lengths=[1] * 8, heads=4, head_size=64, dtype=torch.bfloat16,
+                               seed=5, state_std=0.1)
+    dev = _to_dev(case)
+    stream = torch.cuda.Stream()
+    pool0 = dev["state_pool"].clone()
+    with torch.cuda.stream(stream):
+        ticket = prepare_recurrent_metadata(dev["cu_seqlens"], dev["state_indices"],
+                                            total_tokens=8, state_pool_size=8, max_seqlen=1)
+        pool = pool0.clone()
+        out = recurrent_forward_internal(
+            dev["r"], dev["w"], dev["k"], dev["v"], dev["a"], dev["b"], state_pool=pool,
+            cu_seqlens=dev["cu_seqlens"], state_indices=dev["state_indices"],
+            decay_mode=DECAY_RAW_W, max_seqlen=1, validated_metadata=ticket)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    eager_out, eager_pool = out.clone(), pool.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        pool.copy_(pool0)
+        gout = recurrent_forward_internal(
+            dev["r"], dev["w"], dev["k"], dev["v"], dev["a"], dev["b"], state_pool=pool,
+            cu_seqlens=dev["cu_seqlens"], state_indices=dev["state_indices"],
+            decay_mode=DECAY_RAW_W, max_seqlen=1, validated_metadata=ticket)
+    for _ in range(3):
+        pool.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gout, eager_out)
+        assert torch.equal(pool, eager_pool)
