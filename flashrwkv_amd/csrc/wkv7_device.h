@@ -155,6 +155,20 @@ __device__ __forceinline__ void store4(typename IoTraits<T>::storage* p, float x
   }
 }
 
+// Streaming (nontemporal) 16-byte state traffic: each state slab is read and
+// written once per launch, so it should not displace reusable lines.
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4 load_f4_stream(const float* p) {
+  const f32x4_t x = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(p));
+  return make_float4(x.x, x.y, x.z, x.w);
+}
+
+__device__ __forceinline__ void store_f4_stream(float* p, float4 v) {
+  const f32x4_t x = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(x, reinterpret_cast<f32x4_t*>(p));
+}
+
 template <typename T>
 __device__ __forceinline__ typename IoTraits<T>::storage nan_value() {
   return from_f32<T>(__int_as_float(0x7fc00000));
