@@ -17,8 +17,9 @@ on the timed path. HIP events on
 the launch stream bracket the timed region; the average launch duration is
 elapsed / steps.
 
-Other workloads (--workload prefill | recurrent_long | varlen) time the
-chunked/long-sequence paths for the reports; the driver uses the default.
+The default run (--workload all) adds a "chunked_prefill" object measuring
+BASELINE config 3 (chunked prefill, B=16, T=4096, H=32) against the bf16 MFMA
+roofline; --workload prefill makes that the headline line instead.
 """
 
 from __future__ import annotations
@@ -44,8 +45,10 @@ def _parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=1000)
     p.add_argument("--warmup", type=int, default=50)
-    p.add_argument("--workload", default="decode",
-                   choices=("decode",))
+    p.add_argument("--workload", default="all",
+                   choices=("all", "decode", "prefill"),
+                   help="all: decode headline line plus the chunked-prefill leg")
+    p.add_argument("--prefill-steps", type=int, default=20)
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="bound on the CPU-baseline sample (0 disables it)")
     return p.parse_args()
@@ -216,14 +219,143 @@ def bench_decode(args):
     return line
 
 
+def chunk_flops(chunk: int = 64, d: int = 64) -> int:
+    """Algorithmic FLOPs of one (64-token chunk, head) of the chunked forward.
+
+    18 C^2 D (four C x C x D triangle products and four C x C x D
+    applications) + 8 C D^2 (two C x D x D state products, two D x C x D state
+    updates) + C^3 / 3 (triangular inverse).
+    """
+    return 18 * chunk * chunk * d + 8 * chunk * d * d + chunk ** 3 // 3
+
+
+def cpu_baseline_prefill(t_len, heads_total, seconds):
+    """fp64 C oracle on a bounded sample: whole (sequence, head) recurrences."""
+    import numpy as np
+    import torch
+
+    from flashrwkv_amd import workloads
+    from oracle import oracle
+
+    cores = len(os.sched_getaffinity(0))
+    sample_heads = max(1, cores)
+    case = workloads.make_case(lengths=[t_len], heads=sample_heads, head_size=64,
+                               dtype=torch.bfloat16, seed=98, state_std=0.0, u_low=-8.0)
+    args = [case[n].double().numpy() for n in ("r", "w", "k", "v", "a", "b")]
+    pool = np.zeros((1, sample_heads, 64, 64))
+    cu = case["cu_seqlens"].numpy()
+    slots = case["state_indices"].numpy()
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        oracle.forward_varlen(*args, pool, cu, slots, num_threads=cores)
+        reps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            break
+    token_heads_per_s = reps * t_len * sample_heads / elapsed
+    return {
+        "value": token_heads_per_s / heads_total,
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{reps} x (1 sequence x {sample_heads} heads x T={t_len}) through the fp64 "
+                  f"C oracle, OpenMP over heads, {elapsed:.1f} s; token-heads/s divided by "
+                  f"H={heads_total} (heads are independent)",
+    }
+
+
+def bench_prefill(args):
+    """chunked prefill, B=16, T=4096, H=32, D=64, bf16 io,
+    raw retention u ~ U(-8, 0), fp32 state pool updated in place."""
+    import torch
+
+    import flashrwkv_amd
+    from flashrwkv_amd import workloads
+    from flashrwkv_amd.tmix.wkv7 import DECAY_RAW_W
+
+    if flashrwkv_amd._C is None:
+        raise SystemExit("flashrwkv_amd native library is not built")
+    ops = flashrwkv_amd._C.ops
+    dev = torch.device("cuda:0")
+    batch, t_len, heads, d = 16, 4096, 32, 64
+    n_tok = batch * t_len
+    tok = workloads.make_tokens(n_tok, heads, d, dtype=torch.bfloat16, seed=20260807,
+                                device=dev, u_low=-8.0)
+    pool = torch.zeros((batch, heads, d, d), device=dev)
+    cu = torch.arange(0, n_tok + 1, t_len, device=dev, dtype=torch.int32)
+    slots = torch.arange(batch, device=dev, dtype=torch.int32)
+    stream = torch.cuda.Stream(device=dev)
+
+    def step():
+        ops.chunk_forward_internal(tok["r"], tok["w"], tok["k"], tok["v"], tok["a"],
+                                   tok["b"], pool, cu, slots, 1.0, DECAY_RAW_W, None)
+
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            step()
+        stream.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(args.prefill_steps):
+            step()
+        end.record(stream)
+        end.synchronize()
+    ms = start.elapsed_time(end) / args.prefill_steps
+    chunk_heads = batch * heads * (t_len // 64)
+    flops = chunk_heads * chunk_flops()
+    nbytes = n_tok * heads * 7 * d * 2 + 2 * batch * heads * d * d * 4
+    tflops = flops / (ms * 1e-3) / 1e12
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    attainable = min(BF16_PEAK_TFLOPS, flops / nbytes * HBM_PEAK_GBPS / 1e3)
+    out = {
+        "workload": "wkv7_chunked_prefill_cfg3: B=16, T=4096, H=32, D=64, bf16 io, chunk 64, "
+                    "raw retention u~U(-8,0), fp32 state pool",
+        "ms_per_step": round(ms, 4),
+        "tokens_per_s": round(n_tok / (ms * 1e-3), 1),
+        "steps": args.prefill_steps,
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
+                     "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                     "frac_of_attainable": round(tflops / attainable, 4),
+                     "attainable": round(attainable, 1),
+                     "traffic": None, "kernel": "chunk_fwd_kernel<Bf16,kRawW,float>",
+                     "algorithmic_flops_per_launch": flops},
+        "hbm": {"achieved_GBps": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                "algorithmic_bytes_per_launch": nbytes},
+    }
+    if args.cpu_seconds > 0:
+        out["cpu_baseline"] = cpu_baseline_prefill(t_len, heads, args.cpu_seconds)
+    return out
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; "
-                          f"--gpus {args.gpus} is not supported (see DESIGN.md, sharding)"}))
+        print(json.dumps({"error": f"--gpus {args.gpus}: this build measures one GPU only. "
+                          "Every (sequence, head) recurrence is independent, so N GPUs "
+                          "would each run the one-GPU kernels on their share of sequences "
+                          "or heads with no communication; no multi-GPU run is made."}))
         raise SystemExit(2)
-    if args.workload == "decode":
+    if args.workload == "prefill":
+        pre = bench_prefill(args)
+        line = {
+            "metric": METRIC, "value": pre["tokens_per_s"], "unit": "tokens/s",
+            "n_gpus": 1, "steps": args.prefill_steps, "warmup": 3,
+            "ms_per_step": pre["ms_per_step"], "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded; BASELINE config 3 distributions)",
+            "config": {"workload": pre["workload"], "parallelism": "single GPU"},
+            "roofline": pre["roofline"], "hbm": pre["hbm"],
+        }
+        if "cpu_baseline" in pre:
+            line["cpu_baseline"] = pre["cpu_baseline"]
+    else:
         line = bench_decode(args)
+        if args.workload == "all":
+            line["chunked_prefill"] = bench_prefill(args)
     print(json.dumps(line), flush=True)
 
 

@@ -60,3 +60,34 @@ def recurrent_fp32_forward_internal(query_start_loc, state_indices, state, r,
 def loaded_libraries() -> list[str]:
     """Absolute paths of the native libraries this facade loaded."""
     return [str(HIP_LIBRARY), str(OPS_LIBRARY)]
+
+
+def infer_chunk_bf16_forward_varlen(r, decay_logits, k, v, a, b, state_pool, cu_seqlens,
+                                    state_indices, chunk_size=16, max_seqlen=-1,
+                                    scale=1.0, decay_bias=None):
+    return ops.infer_chunk_bf16_forward_varlen(
+        r, decay_logits, k, v, a, b, state_pool, cu_seqlens, state_indices,
+        int(chunk_size), int(max_seqlen), float(scale), decay_bias)
+
+
+def chunk_forward_internal(r, decay, k, v, a, b, state_pool, cu_seqlens, state_indices,
+                           scale, decay_mode, decay_bias=None):
+    return ops.chunk_forward_internal(r, decay, k, v, a, b, state_pool, cu_seqlens,
+                                      state_indices, float(scale), int(decay_mode),
+                                      decay_bias)
+
+
+def statetune_recurrent_fp32io16_forward(sequence_chunk_offsets, chunk_token_starts,
+                                         chunk_token_ends, state, r, decay_logits, k, v,
+                                         a, b, output, boundary, state_dot_a, scale=1.0):
+    ops.statetune_recurrent_fp32io16_forward(
+        sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, state, r,
+        decay_logits, k, v, a, b, output, boundary, state_dot_a, float(scale))
+
+
+def statetune_forward_internal(sequence_chunk_offsets, chunk_token_starts,
+                               chunk_token_ends, state, r, decay, k, v, a, b, output,
+                               boundary, state_dot_a, scale, decay_mode):
+    ops.statetune_forward_internal(
+        sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, state, r, decay,
+        k, v, a, b, output, boundary, state_dot_a, float(scale), int(decay_mode))

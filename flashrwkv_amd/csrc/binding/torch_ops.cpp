@@ -357,6 +357,190 @@ void recurrent_fp32_forward_internal(
                  static_cast<int>(decay_mode), /*allow_fp32_tokens=*/true);
 }
 
+// ---------------------------------------------------------------- chunk ---
+
+void check_chunk_tokens(const Tensor& r, const Tensor& decay, const Tensor& k,
+                        const Tensor& v, const Tensor& a, const Tensor& b,
+                        bool bf16_only) {
+  const std::pair<const Tensor*, const char*> all[] = {
+      {&r, "r"}, {&decay, "decay_logits"}, {&k, "k"}, {&v, "v"}, {&a, "a"}, {&b, "b"}};
+  for (const auto& item : all) {
+    check_device_contiguous(*item.first, item.second);
+    TORCH_CHECK(item.first->device() == r.device(), item.second,
+                " must be on the same device as r");
+    if (bf16_only) {
+      TORCH_CHECK(item.first->scalar_type() == at::kBFloat16, item.second,
+                  " must be bfloat16");
+    } else {
+      TORCH_CHECK(item.first->scalar_type() == r.scalar_type(),
+                  "r,decay_logits,k,v,a,b dtype mismatch");
+    }
+    TORCH_CHECK(item.first->sizes() == r.sizes(), item.second,
+                " must have the same shape as r");
+  }
+  TORCH_CHECK(r.scalar_type() == at::kBFloat16 || r.scalar_type() == at::kHalf,
+              "token tensors must be float16 or bfloat16");
+  TORCH_CHECK(r.dim() == 3 && r.size(0) > 0 && r.size(1) > 0 && r.size(2) == 64,
+              "chunk token tensors must have shape [total_tokens,H,64]");
+  TORCH_CHECK(r.size(0) <= std::numeric_limits<int32_t>::max(),
+              "token count must fit in int32");
+}
+
+void check_chunk_metadata(const Tensor& cu, const Tensor& slots, const Tensor& r) {
+  check_device_contiguous(cu, "cu_seqlens");
+  check_device_contiguous(slots, "state_indices");
+  TORCH_CHECK(cu.device() == r.device() && slots.device() == r.device(),
+              "cu_seqlens and state_indices must be on the same device as r");
+  TORCH_CHECK(cu.scalar_type() == at::kInt && slots.scalar_type() == at::kInt,
+              "chunk metadata must be int32");
+  TORCH_CHECK(cu.dim() == 1 && slots.dim() == 1 && slots.numel() > 0 &&
+                  cu.numel() == slots.numel() + 1,
+              "cu_seqlens must have shape [B+1] and state_indices [B]");
+  TORCH_CHECK(slots.numel() <= 65535, "state_indices must contain at most 65535 sequences");
+}
+
+void chunk_impl(const Tensor& r, const Tensor& decay, const Tensor& k, const Tensor& v,
+                const Tensor& a, const Tensor& b, Tensor& pool, const Tensor& cu,
+                const Tensor& slots, double scale, const std::optional<Tensor>& decay_bias,
+                int decay_mode, const Tensor& output) {
+  TORCH_CHECK(std::isfinite(scale), "scale must be finite");
+  check_device_contiguous(pool, "state_pool");
+  TORCH_CHECK(pool.device() == r.device(), "state_pool must be on the same device as r");
+  TORCH_CHECK(pool.dim() == 4 && pool.size(0) > 0 && pool.size(1) == r.size(1) &&
+                  pool.size(2) == 64 && pool.size(3) == 64,
+              "state_pool must have shape [slots,H,64,64]");
+  TORCH_CHECK(pool.size(0) <= std::numeric_limits<int32_t>::max(),
+              "state slot count must fit in int32");
+  check_chunk_metadata(cu, slots, r);
+  check_decay_bias(decay_bias, pool, r);
+  TORCH_CHECK(!(decay_bias.has_value() && decay_mode == FRWKV_DECAY_RAW_W),
+              "decay_bias is only defined for decay logits");
+  const int pool_code = pool.scalar_type() == at::kFloat      ? FRWKV_DTYPE_F32
+                        : pool.scalar_type() == at::kBFloat16 ? FRWKV_DTYPE_BF16
+                                                              : -1;
+  TORCH_CHECK(pool_code >= 0, "state_pool must be float32 or bfloat16");
+  c10::DeviceGuard guard(r.device());
+  Prepared launch = device_prepare(cu, slots, r.size(0), pool.size(0));
+  check_rc(frwkv_chunk_forward(
+      io_code(r.scalar_type()), decay_mode, pool_code, static_cast<int32_t>(slots.numel()),
+      static_cast<int32_t>(r.size(1)), 64, static_cast<int32_t>(r.size(0)),
+      static_cast<int32_t>(pool.size(0)), launch.cu_snapshot.data_ptr<int32_t>(),
+      launch.slot_snapshot.data_ptr<int32_t>(), launch.status.data_ptr<int32_t>(),
+      pool.data_ptr(), r.data_ptr(), decay.data_ptr(),
+      decay_bias.has_value() ? decay_bias->data_ptr() : nullptr, k.data_ptr(), v.data_ptr(),
+      a.data_ptr(), b.data_ptr(), output.data_ptr(), static_cast<float>(scale),
+      current_stream(r)));
+}
+
+// Public op (reference infer_chunk_bf16_forward_varlen.cpp:77-171): bf16
+// tokens, bf16 pool updated in place, returns (output, state_pool).
+std::tuple<Tensor, Tensor> infer_chunk_bf16_forward_varlen(
+    Tensor r, Tensor decay_logits, Tensor k, Tensor v, Tensor a, Tensor b,
+    Tensor state_pool, Tensor cu_seqlens, Tensor state_indices, int64_t chunk_size,
+    int64_t max_seqlen, double scale, std::optional<Tensor> decay_bias) {
+  check_chunk_tokens(r, decay_logits, k, v, a, b, /*bf16_only=*/true);
+  TORCH_CHECK(state_pool.scalar_type() == at::kBFloat16, "state_pool must be bfloat16");
+  TORCH_CHECK(chunk_size > 0, "chunk_size must be positive");
+  TORCH_CHECK(max_seqlen > 0, "max_seqlen must be positive");
+  Tensor output = at::empty_like(v);
+  chunk_impl(r, decay_logits, k, v, a, b, state_pool, cu_seqlens, state_indices, scale,
+             decay_bias, FRWKV_DECAY_LOGITS, output);
+  return {output, state_pool};
+}
+
+// Internal op: explicit decay mode, fp16/bf16 tokens, fp32 or bf16 pool.
+Tensor chunk_forward_internal(Tensor r, Tensor decay, Tensor k, Tensor v, Tensor a,
+                              Tensor b, Tensor state_pool, Tensor cu_seqlens,
+                              Tensor state_indices, double scale, int64_t decay_mode,
+                              std::optional<Tensor> decay_bias) {
+  TORCH_CHECK(decay_mode == FRWKV_DECAY_LOGITS || decay_mode == FRWKV_DECAY_RAW_W,
+              "decay_mode must be 0 (logits) or 1 (raw retention)");
+  check_chunk_tokens(r, decay, k, v, a, b, /*bf16_only=*/false);
+  Tensor output = at::empty_like(v);
+  chunk_impl(r, decay, k, v, a, b, state_pool, cu_seqlens, state_indices, scale, decay_bias,
+             static_cast<int>(decay_mode), output);
+  return output;
+}
+
+// ------------------------------------------------------------ statetune ---
+
+void check_statetune_metadata(const Tensor& offsets, const Tensor& starts,
+                              const Tensor& ends, const Tensor& state) {
+  const std::pair<const Tensor*, const char*> all[] = {
+      {&offsets, "sequence_chunk_offsets"},
+      {&starts, "chunk_token_starts"},
+      {&ends, "chunk_token_ends"}};
+  for (const auto& item : all) {
+    check_device_contiguous(*item.first, item.second);
+    TORCH_CHECK(item.first->scalar_type() == at::kInt, item.second, " must be int32");
+    TORCH_CHECK(item.first->device() == state.device(), item.second,
+                " must share the state device");
+    TORCH_CHECK(item.first->dim() == 1, item.second, " must be one-dimensional");
+  }
+  TORCH_CHECK(offsets.numel() == state.size(0) + 1,
+              "sequence_chunk_offsets must have shape [B+1]");
+  TORCH_CHECK(starts.numel() > 0 && ends.numel() == starts.numel(),
+              "chunk token metadata must have matching shape [C]");
+}
+
+void statetune_forward_impl(const Tensor& offsets, const Tensor& starts, const Tensor& ends,
+                            Tensor& state, const Tensor& r, const Tensor& decay,
+                            const Tensor& k, const Tensor& v, const Tensor& a,
+                            const Tensor& b, Tensor& output, Tensor& boundary,
+                            Tensor& state_dot_a, double scale, int decay_mode) {
+  TORCH_CHECK(std::isfinite(scale), "scale must be finite");
+  check_device_contiguous(state, "state");
+  TORCH_CHECK(state.scalar_type() == at::kFloat, "state must be float32");
+  TORCH_CHECK(state.dim() == 4 && state.size(0) > 0 && state.size(1) > 0 &&
+                  state.size(2) == state.size(3),
+              "state must have shape [B,H,D,D]");
+  TORCH_CHECK(state.size(2) == 64, "state head size must be 64 for the MI355X chunked kernels");
+  check_chunk_tokens(r, decay, k, v, a, b, /*bf16_only=*/false);
+  TORCH_CHECK(r.size(1) == state.size(1), "token tensors must have shape [total_tokens,H,D]");
+  for (const auto* t : {&r, &decay, &k, &v, &a, &b}) check_same_device(state, *t, "token");
+  check_statetune_metadata(offsets, starts, ends, state);
+  check_device_contiguous(output, "output");
+  check_device_contiguous(boundary, "boundary");
+  check_device_contiguous(state_dot_a, "state_dot_a");
+  TORCH_CHECK(output.sizes() == r.sizes() && output.scalar_type() == r.scalar_type(),
+              "output must match r");
+  TORCH_CHECK(boundary.scalar_type() == at::kFloat && boundary.dim() == 4 &&
+                  boundary.size(0) == starts.numel() && boundary.size(1) == state.size(1) &&
+                  boundary.size(2) == 64 && boundary.size(3) == 64,
+              "boundary must have shape [chunks,H,D,D] float32");
+  TORCH_CHECK(state_dot_a.scalar_type() == at::kFloat && state_dot_a.sizes() == r.sizes(),
+              "state_dot_a must have shape [total_tokens,H,D] float32");
+  c10::DeviceGuard guard(state.device());
+  check_rc(frwkv_statetune_forward(
+      io_code(r.scalar_type()), decay_mode, static_cast<int32_t>(state.size(0)),
+      static_cast<int32_t>(state.size(1)), 64, static_cast<int32_t>(r.size(0)),
+      static_cast<int32_t>(starts.numel()), offsets.data_ptr<int32_t>(),
+      starts.data_ptr<int32_t>(), ends.data_ptr<int32_t>(), state.data_ptr<float>(),
+      r.data_ptr(), decay.data_ptr(), nullptr, k.data_ptr(), v.data_ptr(), a.data_ptr(),
+      b.data_ptr(), output.data_ptr(), boundary.data_ptr<float>(),
+      state_dot_a.data_ptr<float>(), static_cast<float>(scale), current_stream(state)));
+}
+
+// Reference statetune_recurrent_fp32io16_forward.cpp:26-44 (decay logits).
+void statetune_recurrent_fp32io16_forward(Tensor offsets, Tensor starts, Tensor ends,
+                                          Tensor state, Tensor r, Tensor decay_logits,
+                                          Tensor k, Tensor v, Tensor a, Tensor b,
+                                          Tensor output, Tensor boundary,
+                                          Tensor state_dot_a, double scale) {
+  statetune_forward_impl(offsets, starts, ends, state, r, decay_logits, k, v, a, b, output,
+                         boundary, state_dot_a, scale, FRWKV_DECAY_LOGITS);
+}
+
+void statetune_forward_internal(Tensor offsets, Tensor starts, Tensor ends, Tensor state,
+                                Tensor r, Tensor decay, Tensor k, Tensor v, Tensor a,
+                                Tensor b, Tensor output, Tensor boundary,
+                                Tensor state_dot_a, double scale, int64_t decay_mode) {
+  TORCH_CHECK(decay_mode == FRWKV_DECAY_LOGITS || decay_mode == FRWKV_DECAY_RAW_W,
+              "decay_mode must be 0 (logits) or 1 (raw retention)");
+  statetune_forward_impl(offsets, starts, ends, state, r, decay, k, v, a, b, output,
+                         boundary, state_dot_a, scale, static_cast<int>(decay_mode));
+}
+
 }  // namespace
 
 TORCH_LIBRARY(flashrwkv_amd, m) {
@@ -395,4 +579,27 @@ TORCH_LIBRARY(flashrwkv_amd, m) {
       "__torch__.torch.classes.flashrwkv_amd.MetadataTicket? "
       "validated_metadata=None, int max_seqlen=-1) -> ()",
       &recurrent_fp32_forward_internal);
+  m.def(
+      "infer_chunk_bf16_forward_varlen(Tensor r, Tensor decay_logits, Tensor k, "
+      "Tensor v, Tensor a, Tensor b, Tensor(a!) state_pool, Tensor cu_seqlens, "
+      "Tensor state_indices, int chunk_size=16, int max_seqlen=-1, float scale=1.0, "
+      "Tensor? decay_bias=None) -> (Tensor, Tensor(a!))",
+      &infer_chunk_bf16_forward_varlen);
+  m.def(
+      "chunk_forward_internal(Tensor r, Tensor decay, Tensor k, Tensor v, Tensor a, "
+      "Tensor b, Tensor(a!) state_pool, Tensor cu_seqlens, Tensor state_indices, "
+      "float scale, int decay_mode, Tensor? decay_bias=None) -> Tensor",
+      &chunk_forward_internal);
+  m.def(
+      "statetune_recurrent_fp32io16_forward(Tensor sequence_chunk_offsets, "
+      "Tensor chunk_token_starts, Tensor chunk_token_ends, Tensor(a!) state, Tensor r, "
+      "Tensor decay_logits, Tensor k, Tensor v, Tensor a, Tensor b, Tensor(b!) output, "
+      "Tensor(c!) boundary, Tensor(d!) state_dot_a, float scale=1.0) -> ()",
+      &statetune_recurrent_fp32io16_forward);
+  m.def(
+      "statetune_forward_internal(Tensor sequence_chunk_offsets, "
+      "Tensor chunk_token_starts, Tensor chunk_token_ends, Tensor(a!) state, Tensor r, "
+      "Tensor decay, Tensor k, Tensor v, Tensor a, Tensor b, Tensor(b!) output, "
+      "Tensor(c!) boundary, Tensor(d!) state_dot_a, float scale, int decay_mode) -> ()",
+      &statetune_forward_internal);
 }

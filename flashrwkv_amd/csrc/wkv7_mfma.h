@@ -1,0 +1,83 @@
+// MFMA and LDS-tile helpers for the chunked WKV7 kernels (gfx950, wave64).
+//
+// Every matrix product in the chunked kernels is a sum of 16x16x16 bf16 MFMA
+// tiles (v_mfma_f32_16x16x16_bf16, fp32 accumulate). With lane l, g = l / 16
+// and n = l % 16 the register layouts are:
+//   A operand (4 bf16): A[m = n][k = 4g + e],  e = 0..3
+//   B operand (4 bf16): B[k = 4g + e][n]
+//   C / D     (4 fp32): C[m = 4g + j][n],      j = 0..3
+// so an accumulator tile in C layout is, after conversion to bf16, directly
+// the B operand of a product contracting over its rows, and the A operand of
+// a product contracting over its columns with its transpose. Kernels chain
+// products through registers this way and only stage operands that several
+// waves share through LDS.
+//
+// LDS tiles are 64 x 64 bf16 with a padded row stride of 72 elements
+// (144 bytes = 36 banks): the 16 rows an operand read touches start in 16
+// distinct bank groups, so 8-byte operand reads are conflict-free within each
+// 16-lane group.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace frwkv {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTileStride = 72;                  // bf16 elements per LDS row
+constexpr int kTileElems = 64 * kTileStride;     // one 64 x 64 tile
+
+__device__ __forceinline__ f32x4 mfma16(i16x4 a, i16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// Round-to-nearest-even fp32 -> bf16 bits.
+__device__ __forceinline__ uint16_t to_bf16_bits(float x) {
+  __bf16 h = static_cast<__bf16>(x);
+  uint16_t bits;
+  __builtin_memcpy(&bits, &h, 2);
+  return bits;
+}
+
+__device__ __forceinline__ float bf16_float(uint16_t bits) {
+  return __uint_as_float(static_cast<uint32_t>(bits) << 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(to_bf16_bits(lo)) |
+         (static_cast<uint32_t>(to_bf16_bits(hi)) << 16);
+}
+
+// C-layout accumulator -> bf16 operand registers.
+__device__ __forceinline__ i16x4 to_operand(f32x4 c) {
+  i16x4 r;
+  r[0] = static_cast<short>(to_bf16_bits(c[0]));
+  r[1] = static_cast<short>(to_bf16_bits(c[1]));
+  r[2] = static_cast<short>(to_bf16_bits(c[2]));
+  r[3] = static_cast<short>(to_bf16_bits(c[3]));
+  return r;
+}
+
+// Operand read from an LDS tile: 4 consecutive bf16 of row `row` starting at
+// column `col` (8-byte aligned). Serves as A operand (row = m, col = k0) or
+// as B operand of a tile stored [n][k] (row = n, col = k0).
+template <int Stride = kTileStride>
+__device__ __forceinline__ i16x4 lds_operand(const uint16_t* tile, int row, int col) {
+  return *reinterpret_cast<const i16x4*>(tile + row * Stride + col);
+}
+
+// Stores a C-layout tile transposed: lane (g, n) writes its 4 values to
+// dst[n][4g .. 4g+3] of a tile with the given row stride (one 8-byte write).
+__device__ __forceinline__ void lds_store_transposed(uint16_t* dst, int stride,
+                                                     int g, int n, f32x4 c) {
+  uint2 q;
+  q.x = pack_bf16x2(c[0], c[1]);
+  q.y = pack_bf16x2(c[2], c[3]);
+  *reinterpret_cast<uint2*>(dst + n * stride + 4 * g) = q;
+}
+
+}  // namespace frwkv

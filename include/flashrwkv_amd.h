@@ -108,6 +108,55 @@ int frwkv_recurrent_forward(int io_dtype, int decay_mode, int32_t num_sequences,
                             const void* v, const void* a, const void* b,
                             void* output, float scale, void* stream);
 
+/*
+ * Chunked forward over packed varlen sequences (prefill), state pool updated
+ * in place at state_indices. Exact chunk form of the recurrence on bf16 MFMA
+ * with fp32 accumulation and an fp32 state carried between 64-token chunks;
+ * results equal frwkv_recurrent_forward up to bf16 rounding.
+ * Replaces infer_chunk_bf16_forward_varlen_cuda and its K1/K2 kernels
+ * (csrc/sm120/tmix/wkv7/infer_chunk_bf16_forward_varlen.cu:42-334; binding
+ * infer_chunk_bf16_forward_varlen.cpp:77-171), whose chunk_size argument has
+ * no counterpart here: the result does not depend on the chunking.
+ * head_size must be 64; io_dtype F16/BF16; pool_dtype F32 (fp32 pool) or
+ * BF16 (the reference contract's bf16 pool, read and written as bf16);
+ * metadata_status as in frwkv_recurrent_forward (non-zero: NaN output, pool
+ * untouched). In FRWKV_DECAY_RAW_W mode the retention is clamped to
+ * [2^-20, 1].
+ */
+int frwkv_chunk_forward(int io_dtype, int decay_mode, int pool_dtype,
+                        int32_t num_sequences, int32_t num_heads,
+                        int32_t head_size, int32_t total_tokens,
+                        int32_t state_pool_size, const int32_t* cu_seqlens,
+                        const int32_t* state_indices,
+                        const int32_t* metadata_status, void* state_pool,
+                        const void* r, const void* decay,
+                        const void* decay_bias, const void* k, const void* v,
+                        const void* a, const void* b, void* output, float scale,
+                        void* stream);
+
+/*
+ * Training (StateTune) forward with caller chunk metadata: sequence s owns
+ * chunks sequence_chunk_offsets[s] .. sequence_chunk_offsets[s+1]-1, chunk c
+ * covers tokens chunk_token_starts[c] .. chunk_token_ends[c]-1. state
+ * [B,H,D,D] fp32 holds S0 on entry and the final state on return (the caller
+ * passes a copy). boundary [num_chunks,H,D,D] fp32 receives the state at each
+ * chunk start; state_dot_a [total_tokens,H,D] fp32 receives a_t^T S_{t-1}.
+ * Replaces statetune_recurrent_fp32io16_forward_cuda
+ * (csrc/sm90/tmix/wkv7/statetune_recurrent_fp32io16_forward.cu:32-224;
+ * binding statetune_recurrent_fp32io16_forward.cpp:26-56). head_size 64.
+ */
+int frwkv_statetune_forward(int io_dtype, int decay_mode, int32_t num_sequences,
+                            int32_t num_heads, int32_t head_size,
+                            int32_t total_tokens, int32_t num_chunks,
+                            const int32_t* sequence_chunk_offsets,
+                            const int32_t* chunk_token_starts,
+                            const int32_t* chunk_token_ends, float* state,
+                            const void* r, const void* decay,
+                            const void* decay_bias, const void* k,
+                            const void* v, const void* a, const void* b,
+                            void* output, float* boundary, float* state_dot_a,
+                            float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

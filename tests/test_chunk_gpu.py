@@ -1,0 +1,247 @@
+"""GPU parity tests of the chunked WKV7 forward (prefill and StateTune forward).
+
+Expected values come from the fp64 oracle (oracle/wkv7_oracle.c, a
+restatement of the reference naive recurrence tests/tmix/wkv7/test.py:157-213
+and tests/tmix/wkv7/statetune/test.py:39-88) fed the same cast inputs.
+Tolerance (normwise max relative error, max|x - ref| / max|ref|): 2e-2 for
+bf16/fp16 outputs and for the fp32 state carried through bf16 MFMA chunks.
+The chunked result must not depend on the chunking, so the recurrent
+kernel's output on the same inputs is a second, independent reference.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import flashrwkv_amd
+from flashrwkv_amd import workloads
+from flashrwkv_amd.tmix.wkv7 import (
+    DECAY_LOGITS,
+    DECAY_RAW_W,
+    recurrent_forward_internal,
+)
+from flashrwkv_amd.tmix.wkv7.chunk import (
+    chunk_forward_internal,
+    infer_chunk_bf16_forward_varlen,
+)
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+DEV = torch.device("cuda")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _require_native():
+    if flashrwkv_amd._C is None:
+        pytest.fail("flashrwkv_amd native library is not built (no fallback exists)")
+    if not torch.cuda.is_available():
+        pytest.fail("a GPU is required for tests marked gpu")
+
+
+def _np(t):
+    if isinstance(t, np.ndarray):
+        return t.astype(np.float64)
+    return t.detach().double().cpu().numpy()
+
+
+def _dev(case):
+    return {k: (v.to(DEV) if isinstance(v, torch.Tensor) else v) for k, v in case.items()}
+
+
+def _oracle(case, *, w=None, pool=None, scale=1.0):
+    w = case["w"] if w is None else w
+    pool = case["state_pool"] if pool is None else pool
+    return oracle.forward_varlen(
+        _np(case["r"]), _np(w), _np(case["k"]), _np(case["v"]), _np(case["a"]),
+        _np(case["b"]), _np(pool), case["cu_seqlens"].numpy(),
+        case["state_indices"].numpy(), scale=scale)
+
+
+def _check(name, actual, expected, tol=TOL):
+    err = oracle.max_rel_error(_np(actual), expected)
+    print(f"{name}: max-rel {err:.3e}")
+    assert np.isfinite(err) and err <= tol, f"{name}: {err:.3e} > {tol}"
+    return err
+
+
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+@pytest.mark.parametrize("lengths", [(1,), (64,), (65,), (1, 17, 64, 65, 130, 200),
+                                     (300, 7, 128)])
+def test_raw_retention_fp32_pool_matches_oracle(dtype, lengths):
+    slots = list(range(len(lengths)))[::-1]
+    case = workloads.make_case(lengths=lengths, heads=3, head_size=64, dtype=dtype,
+                               seed=11 + len(lengths), state_std=0.1,
+                               pool_slots=len(lengths) + 2, slots=slots)
+    d = _dev(case)
+    pool = d["state_pool"].clone()
+    y = chunk_forward_internal(d["r"], d["w"], d["k"], d["v"], d["a"], d["b"],
+                               state_pool=pool, cu_seqlens=d["cu_seqlens"],
+                               state_indices=d["state_indices"], decay_mode=DECAY_RAW_W,
+                               scale=0.75)
+    torch.cuda.synchronize()
+    y_ref, pool_ref = _oracle(case, scale=0.75)
+    _check("y", y, y_ref)
+    _check("state", pool, pool_ref)
+    # Untouched slots stay bitwise equal.
+    untouched = sorted(set(range(pool.shape[0])) - set(slots))
+    for s in untouched:
+        assert torch.equal(pool[s], d["state_pool"][s])
+
+
+def test_logits_bias_bf16_pool_public_op():
+    lengths = (5, 64, 129, 77)
+    g = torch.Generator().manual_seed(20260810)
+    case = workloads.make_case(lengths=lengths, heads=4, head_size=64,
+                               dtype=torch.bfloat16, seed=21, state_std=0.05,
+                               pool_slots=6, slots=[4, 0, 5, 2])
+    logits = (torch.randn(case["r"].shape, generator=g) * 2.0).to(torch.bfloat16)
+    bias = (torch.randn((4, 64), generator=g) * 0.5).to(torch.bfloat16)
+    pool16 = case["state_pool"].to(torch.bfloat16)
+    d = _dev(case)
+    pool = pool16.to(DEV).clone()
+    y = infer_chunk_bf16_forward_varlen(
+        d["r"], logits.to(DEV), d["k"], d["v"], d["a"], d["b"], state_pool=pool,
+        cu_seqlens=d["cu_seqlens"], state_indices=d["state_indices"], chunk_size=16,
+        decay_bias=bias.to(DEV))
+    torch.cuda.synchronize()
+    w = oracle.retention_from_logits(_np(logits), _np(bias))
+    y_ref, pool_ref = _oracle(case, w=w, pool=pool16)
+    _check("y", y, y_ref)
+    _check("state (bf16 pool)", pool, pool_ref)
+    for s in (1, 3):
+        assert torch.equal(pool[s], pool16[s].to(DEV))
+
+
+def test_strong_decay_takes_subchunk_path():
+    """Retention far below the logits range forces the 16- and 4-token passes."""
+    lengths = (64, 100, 33)
+    case = workloads.make_case(lengths=lengths, heads=2, head_size=64,
+                               dtype=torch.bfloat16, seed=31, state_std=0.1)
+    g = torch.Generator().manual_seed(5)
+    u = torch.rand(case["w"].shape, generator=g)
+    w = torch.where(u < 0.3, torch.full_like(u, 1e-3), torch.exp(-torch.exp(-8 * u)))
+    w[:, 0, :8] = 1e-9  # some features below the 2^-20 clamp
+    case["w"] = w.to(torch.bfloat16)
+    d = _dev(case)
+    pool = d["state_pool"].clone()
+    y = chunk_forward_internal(d["r"], d["w"], d["k"], d["v"], d["a"], d["b"],
+                               state_pool=pool, cu_seqlens=d["cu_seqlens"],
+                               state_indices=d["state_indices"], decay_mode=DECAY_RAW_W)
+    torch.cuda.synchronize()
+    y_ref, pool_ref = _oracle(case)
+    _check("y", y, y_ref)
+    _check("state", pool, pool_ref)
+
+
+def test_chunk_matches_recurrent_kernel_and_is_deterministic():
+    lengths = (1000, 64, 333)
+    case = workloads.make_case(lengths=lengths, heads=4, head_size=64,
+                               dtype=torch.bfloat16, seed=41, state_std=0.1)
+    d = _dev(case)
+    pool_c = d["state_pool"].clone()
+    pool_r = d["state_pool"].clone()
+    kw = dict(cu_seqlens=d["cu_seqlens"], state_indices=d["state_indices"],
+              decay_mode=DECAY_RAW_W)
+    args = (d["r"], d["w"], d["k"], d["v"], d["a"], d["b"])
+    y_c = chunk_forward_internal(*args, state_pool=pool_c, **kw)
+    y_r = recurrent_forward_internal(*args, state_pool=pool_r, **kw)
+    pool_c2 = d["state_pool"].clone()
+    y_c2 = chunk_forward_internal(*args, state_pool=pool_c2, **kw)
+    torch.cuda.synchronize()
+    _check("y chunk vs recurrent", y_c, _np(y_r))
+    _check("state chunk vs recurrent", pool_c, _np(pool_r))
+    assert torch.equal(y_c, y_c2) and torch.equal(pool_c, pool_c2)
+
+
+def test_config3_full_shape_sampled_heads():
+    """BASELINE config 3 at full shape; heads are independent, so the oracle
+    runs on a sample of (sequence, head) pairs at the full T=4096."""
+    batch, t_len, heads = 16, 4096, 32
+    case = workloads.make_case(lengths=[t_len] * batch, heads=heads, head_size=64,
+                               dtype=torch.bfloat16, seed=20260807, state_std=0.0,
+                               u_low=-8.0)
+    d = _dev(case)
+    pool = d["state_pool"].clone()
+    y = chunk_forward_internal(d["r"], d["w"], d["k"], d["v"], d["a"], d["b"],
+                               state_pool=pool, cu_seqlens=d["cu_seqlens"],
+                               state_indices=d["state_indices"], decay_mode=DECAY_RAW_W)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all()
+    y = y.view(batch, t_len, heads, 64)
+    for seq, head in ((0, 0), (7, 13), (15, 31)):
+        sl = slice(seq * t_len, (seq + 1) * t_len)
+        sub = {n: case[n][sl, head:head + 1] for n in ("r", "w", "k", "v", "a", "b")}
+        y_ref, s_ref = oracle.forward_varlen(
+            *(_np(sub[n]) for n in ("r", "w", "k", "v", "a", "b")),
+            np.zeros((1, 1, 64, 64)), np.array([0, t_len], dtype=np.int32),
+            np.array([0], dtype=np.int32))
+        _check(f"y seq{seq} head{head}", y[seq, :, head:head + 1], y_ref.reshape(t_len, 1, 64))
+        _check(f"state seq{seq} head{head}", pool[seq, head], s_ref[0, 0])
+
+
+def test_invalid_metadata_fails_closed_with_nan_and_untouched_pool():
+    lengths = (10, 20)
+    case = workloads.make_case(lengths=lengths, heads=2, head_size=64,
+                               dtype=torch.bfloat16, seed=51)
+    d = _dev(case)
+    pool = d["state_pool"].clone()
+    bad_slots = torch.tensor([0, 0], dtype=torch.int32, device=DEV)  # duplicate slot
+    y = chunk_forward_internal(d["r"], d["w"], d["k"], d["v"], d["a"], d["b"],
+                               state_pool=pool, cu_seqlens=d["cu_seqlens"],
+                               state_indices=bad_slots, decay_mode=DECAY_RAW_W)
+    torch.cuda.synchronize()
+    assert torch.isnan(y.float()).all()
+    assert torch.equal(pool, d["state_pool"])
+
+
+def test_statetune_forward_matches_oracle_boundaries_and_state_dot_a():
+    lengths = (70, 5, 130)
+    chunk = 32
+    offsets, starts, ends, cu = oracle.chunk_metadata(lengths, chunk)
+    case = workloads.make_case(lengths=lengths, heads=2, head_size=64,
+                               dtype=torch.bfloat16, seed=61, state_std=0.1)
+    d = _dev(case)
+    s0 = d["state_pool"].clone()
+    state = s0.clone()
+    n_tok = int(cu[-1])
+    y = torch.empty_like(d["v"])
+    boundary = torch.empty((len(starts), 2, 64, 64), device=DEV)
+    sda = torch.empty((n_tok, 2, 64), device=DEV)
+    meta = [torch.from_numpy(x).to(DEV) for x in (offsets, starts, ends)]
+    flashrwkv_amd._C.statetune_forward_internal(
+        *meta, state, d["r"], d["w"], d["k"], d["v"], d["a"], d["b"], y, boundary, sda,
+        0.5, DECAY_RAW_W)
+    torch.cuda.synchronize()
+    y_ref, s_ref, b_ref, sda_ref = oracle.forward(
+        *(_np(case[n]) for n in ("r", "w", "k", "v", "a", "b")), _np(case["state_pool"]),
+        seg_offsets=offsets, seg_starts=starts, seg_ends=ends,
+        state_slots=np.arange(len(lengths), dtype=np.int32), scale=0.5,
+        want_boundary=True, want_state_dot_a=True)
+    _check("y", y, y_ref)
+    _check("final state", state, s_ref)
+    _check("boundary", boundary, b_ref)
+    _check("state_dot_a", sda, sda_ref)
+    assert torch.equal(s0, d["state_pool"])
+
+
+def test_public_chunk_wrapper_rejects_bad_arguments_before_launch():
+    case = _dev(workloads.make_case(lengths=(4,), heads=1, head_size=64,
+                                    dtype=torch.bfloat16, seed=3))
+    pool = case["state_pool"].to(torch.bfloat16)
+    args = [case[n] for n in ("r", "w", "k", "v", "a", "b")]
+    kw = dict(state_pool=pool, cu_seqlens=case["cu_seqlens"],
+              state_indices=case["state_indices"])
+    with pytest.raises(TypeError, match="chunk_size"):
+        infer_chunk_bf16_forward_varlen(*args, chunk_size=2.0, **kw)
+    with pytest.raises(ValueError, match="chunk_size"):
+        infer_chunk_bf16_forward_varlen(*args, chunk_size=0, **kw)
+    with pytest.raises(ValueError, match="bfloat16"):
+        infer_chunk_bf16_forward_varlen(*[x.half() for x in args], **kw)
+    with pytest.raises(ValueError, match="state_pool"):
+        infer_chunk_bf16_forward_varlen(*args, **{**kw, "state_pool": pool.float()})
+    with pytest.raises(ValueError, match="finite"):
+        infer_chunk_bf16_forward_varlen(*args, scale=float("inf"), **kw)
