@@ -27,20 +27,23 @@
 // 4-token spans never exceed 80; below 2^-20 the clamp changes S_t by less
 // than 1e-6 |S_{t-1}|, far under bf16 resolution.
 //
-// Work decomposition (one 256-thread workgroup per (sequence, head)):
+// Work decomposition (one 256-thread workgroup per (sequence, head), two
+// workgroups per CU: 80 KB of LDS and at most 256 registers per lane):
 //   * prepare: the chunk's 64 tokens x 64 features are decoded once (two
 //     tokens x 8 features per thread), the cumulative decay is a wave
 //     shuffle scan plus a cross-wave carry, and the scaled operands go to LDS
 //     as bf16 ([token][feature] tiles and, for products contracting over
 //     tokens, [feature][token] tiles);
-//   * intra-chunk products: the 40 lower-triangular 16x16 tiles of Lab,
-//     Lak, Arb, Ark are spread over the four waves; wave p also inverts the
-//     diagonal block I - Lab_pp in fp32 (forward substitution);
+//   * intra-chunk products: the 40 lower-triangular 16x16 blocks of Lab,
+//     Lak, Arb, Ark (stored packed) are spread over the four waves; wave p
+//     also inverts the diagonal block I - Lab_pp (forward substitution);
 //   * state-dependent part: wave w owns value columns 16w..16w+15. Its slice
-//     of the fp32 state lives in MFMA accumulators for the whole sequence;
+//     of the fp32 state lives in MFMA accumulators for the whole sequence
+//     and its slice of V is loaded from HBM straight into operand registers;
 //     the block forward substitution SA_p = T_pp (rhs_p + sum_q Lab_pq SA_q),
 //     the output tiles and the state update chain through registers, so this
 //     part has no barrier.
+// The token rows of chunk c+1 are loaded while chunk c computes.
 #include "capi_internal.h"
 #include "wkv7_device.h"
 #include "wkv7_mfma.h"
@@ -54,23 +57,39 @@ constexpr int kChunkThreads = 256;
 constexpr float kSpanLimit = 80.0f;   // log2 units
 constexpr float kLog2Min = -20.0f;    // per-token clamp of log2 retention
 
+// Operand tiles: 64 rows x 64 bf16, row stride 68 elements (136 B = 34
+// dwords): the 16 rows of an 8-byte operand read hit 16 distinct dword pairs.
+constexpr int kOpStride = 68;
+constexpr int kOpTile = 64 * kOpStride;
+// Lower-triangular C x C matrices: the 10 blocks (p, q <= p) of 16 x 16,
+// packed, row stride 20 (40 B = 10 dwords, conflict-free the same way).
+constexpr int kTriStride = 20;
+constexpr int kTriBlock = 16 * kTriStride;
+constexpr int kTriBlocks = 10;
+
+enum TriMatrix { kLab = 0, kLak = 1, kArb = 2, kArk = 3 };
+
+__device__ __forceinline__ int tri_index(int p, int q) { return (p * (p + 1)) / 2 + q; }
+
 struct ChunkSmem {
-  uint16_t at[kTileElems];   // [t][k]
-  uint16_t rt[kTileElems];   // [t][k]
-  uint16_t bh[kTileElems];   // [t][k]
-  uint16_t kh[kTileElems];   // [t][k]
-  uint16_t btT[kTileElems];  // [k][t]
-  uint16_t ktT[kTileElems];  // [k][t]
-  uint16_t vT[kTileElems];   // [v][t]
-  uint16_t lab[kTileElems];  // [t][i]
-  uint16_t lak[kTileElems];
-  uint16_t arb[kTileElems];
-  uint16_t ark[kTileElems];
-  uint16_t tinv[4][16 * 24];  // (I - Lab_pp)^{-1}, [t][i], row stride 24
-  float lpp[4][16 * 16];      // fp32 Lab_pp, [t][i]
-  float gc[kHead];            // 2^GC per key feature
-  float wave_tot[4][kHead];   // per-wave sums of log2 retention
+  uint16_t at[kOpTile];   // [t][k]
+  uint16_t rt[kOpTile];   // [t][k]
+  uint16_t bh[kOpTile];   // [t][k]
+  uint16_t kh[kOpTile];   // [t][k]
+  uint16_t btT[kOpTile];  // [k][t]
+  uint16_t ktT[kOpTile];  // [k][t]
+  union {
+    uint16_t tri[4][kTriBlocks * kTriBlock];  // Lab, Lak, Arb, Ark: [t][i]
+    float wave_tot[4][kHead];                 // decay scan carry (prepare only)
+  };
+  uint16_t tinv[4][kTriBlock];  // (I - Lab_pp)^{-1}, [t][i]
+  float gc[kHead];              // 2^GC per key feature
 };
+static_assert(sizeof(ChunkSmem) <= 80 * 1024, "two workgroups per CU need <= 80 KB of LDS");
+
+__device__ __forceinline__ const uint16_t* tri_block(const ChunkSmem& sm, int m, int p, int q) {
+  return sm.tri[m] + tri_index(p, q) * kTriBlock;
+}
 
 struct ChunkFwdParams {
   int32_t num_heads;
@@ -98,9 +117,12 @@ struct ChunkFwdParams {
   int64_t out_elems;
 };
 
-// Raw token rows held by one thread: 2 tokens x 8 features of each input.
-struct RawRows {
-  uint4 r[2], w[2], k[2], v[2], a[2], b[2];
+// Token rows of one chunk held by a thread: r, w, k, a, b for 2 tokens x 8
+// features (prepare layout), and V in MFMA operand layout for the wave's 16
+// value columns: lane (g, n) holds V[16q + 4g + e][16w + n] in vs[q][e].
+struct ChunkRows {
+  uint4 r[2], w[2], k[2], a[2], b[2];
+  i16x4 vs[4];
 };
 
 template <typename T>
@@ -117,16 +139,6 @@ __device__ __forceinline__ uint4 load_row8(const void* base, int64_t offset) {
       static_cast<const typename IoTraits<T>::storage*>(base) + offset);
 }
 
-template <typename PoolT>
-__device__ __forceinline__ float pool_load(const void* base, int64_t i) {
-  return to_f32<PoolT>(static_cast<const typename IoTraits<PoolT>::storage*>(base)[i]);
-}
-
-template <typename PoolT>
-__device__ __forceinline__ void pool_store(void* base, int64_t i, float x) {
-  static_cast<typename IoTraits<PoolT>::storage*>(base)[i] = from_f32<PoolT>(x);
-}
-
 // log2 of the retention, clamped to [kLog2Min, 0].
 template <DecayMode M>
 __device__ __forceinline__ float log2_retention(float x) {
@@ -134,15 +146,31 @@ __device__ __forceinline__ float log2_retention(float x) {
   return fminf(fmaxf(lg, kLog2Min), 0.0f);
 }
 
+// 8 floats -> 8 bf16 at an 8-byte aligned LDS address (two 8-byte writes).
+__device__ __forceinline__ void store8_bf16(uint16_t* dst, const float (&x)[8]) {
+  uint2 lo, hi;
+  lo.x = pack_bf16x2(x[0], x[1]);
+  lo.y = pack_bf16x2(x[2], x[3]);
+  hi.x = pack_bf16x2(x[4], x[5]);
+  hi.y = pack_bf16x2(x[6], x[7]);
+  reinterpret_cast<uint2*>(dst)[0] = lo;
+  reinterpret_cast<uint2*>(dst)[1] = hi;
+}
+
 struct Spans {
   float all;       // -GC over the prepared range
   float block[4];  // per 16-token block
+
+  // block[q] for a runtime q without indexing a private array.
+  __device__ __forceinline__ float block_at(int q) const {
+    return q == 0 ? block[0] : q == 1 ? block[1] : q == 2 ? block[2] : block[3];
+  }
 };
 
-// Decodes the thread's raw rows restricted to tokens [lo, hi) of the chunk,
+// Decodes the thread's rows restricted to tokens [lo, hi) of the chunk,
 // scans the decay and writes every scaled operand tile. Ends with a barrier.
 template <typename T, DecayMode M>
-__device__ Spans prepare(ChunkSmem& sm, const RawRows& raw, const float (&bias)[8],
+__device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bias)[8],
                          int lo, int hi) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -150,40 +178,27 @@ __device__ Spans prepare(ChunkSmem& sm, const RawRows& raw, const float (&bias)[
   const int tp = lane >> 3;
   const int kg = lane & 7;
   const int t0 = 16 * wave + 2 * tp;
+  const float on0 = (t0 >= lo && t0 < hi) ? 1.0f : 0.0f;
+  const float on1 = (t0 + 1 >= lo && t0 + 1 < hi) ? 1.0f : 0.0f;
 
   __syncthreads();  // earlier readers of the tiles are done
 
-  float lg[2][8], rr[2][8], kk[2][8], vv[2][8], aa[2][8], bb[2][8];
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const bool active = (t0 + s >= lo) && (t0 + s < hi);
-    float wraw[8];
-    unpack8<T>(raw.w[s], wraw);
-    unpack8<T>(raw.r[s], rr[s]);
-    unpack8<T>(raw.k[s], kk[s]);
-    unpack8<T>(raw.v[s], vv[s]);
-    unpack8<T>(raw.a[s], aa[s]);
-    unpack8<T>(raw.b[s], bb[s]);
+  float lg0[8], lg1[8];
+  {
+    float w0[8], w1[8];
+    unpack8<T>(rows.w[0], w0);
+    unpack8<T>(rows.w[1], w1);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      lg[s][e] = active ? log2_retention<M>(wraw[e] + bias[e]) : 0.0f;
-      if (!active) {
-        rr[s][e] = 0.0f;
-        kk[s][e] = 0.0f;
-        vv[s][e] = 0.0f;
-        aa[s][e] = 0.0f;
-        bb[s][e] = 0.0f;
-      }
+      lg0[e] = on0 * log2_retention<M>(w0[e] + bias[e]);
+      lg1[e] = on1 * log2_retention<M>(w1[e] + bias[e]);
     }
   }
 
   // Inclusive scan over the wave's 8 token pairs (lanes 8 apart share kg).
-  float incl[8], pair[8];
+  float incl[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    pair[e] = lg[0][e] + lg[1][e];
-    incl[e] = pair[e];
-  }
+  for (int e = 0; e < 8; ++e) incl[e] = lg0[e] + lg1[e];
 #pragma unroll
   for (int off = 8; off < 64; off <<= 1) {
 #pragma unroll
@@ -198,25 +213,27 @@ __device__ Spans prepare(ChunkSmem& sm, const RawRows& raw, const float (&bias)[
   }
   __syncthreads();
 
-  float base[8], total[8];
+  float g0[8], g1[8], gp0[8], total[8];
   Spans spans;
 #pragma unroll
   for (int q = 0; q < 4; ++q) spans.block[q] = 0.0f;
+  float span_all = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    base[e] = 0.0f;
-    total[e] = 0.0f;
+    float base = 0.0f, tot = 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const float x = sm.wave_tot[q][8 * kg + e];
-      if (q < wave) base[e] += x;
-      total[e] += x;
+      base += (q < wave) ? x : 0.0f;
+      tot += x;
       spans.block[q] = fmaxf(spans.block[q], -x);
     }
+    total[e] = tot;
+    span_all = fmaxf(span_all, -tot);
+    gp0[e] = base + incl[e] - lg0[e] - lg1[e];
+    g0[e] = gp0[e] + lg0[e];
+    g1[e] = g0[e] + lg1[e];
   }
-  float span_all = 0.0f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) span_all = fmaxf(span_all, -total[e]);
   // Max over the 8 feature groups (lane bits 0..2): every lane of every wave
   // ends with the same values, so branches on them are uniform.
 #pragma unroll
@@ -229,55 +246,65 @@ __device__ Spans prepare(ChunkSmem& sm, const RawRows& raw, const float (&bias)[
   }
   spans.all = span_all;
 
-  float gtok[2][8], gprev[2][8];
+  // Token t0: gp = gp0, g = g0; token t0 + 1: gp = g0, g = g1.
+  float up0[8], up1[8], dn0[8], dn1[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float excl = base[e] + incl[e] - pair[e];
-    gprev[0][e] = excl;
-    gtok[0][e] = excl + lg[0][e];
-    gprev[1][e] = gtok[0][e];
-    gtok[1][e] = gtok[0][e] + lg[1][e];
+    up0[e] = exp2f(g0[e]);   // 2^G(t0)  (= 2^Gp(t0+1))
+    up1[e] = exp2f(g1[e]);   // 2^G(t0+1)
+    dn0[e] = exp2f(-g0[e]);
+    dn1[e] = exp2f(-g1[e]);
   }
-
-  float btv[2][8], ktv[2][8];
+  {
+    float x0[8], x1[8], t[8];
+    unpack8<T>(rows.a[0], x0);
+    unpack8<T>(rows.a[1], x1);
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const int t = t0 + s;
-    float atv[8], rtv[8], bhv[8], khv[8];
+    for (int e = 0; e < 8; ++e) t[e] = on0 * x0[e] * exp2f(gp0[e]);
+    store8_bf16(sm.at + t0 * kOpStride + 8 * kg, t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = on1 * x1[e] * up0[e];
+    store8_bf16(sm.at + (t0 + 1) * kOpStride + 8 * kg, t);
+
+    unpack8<T>(rows.r[0], x0);
+    unpack8<T>(rows.r[1], x1);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = on0 * x0[e] * up0[e];
+    store8_bf16(sm.rt + t0 * kOpStride + 8 * kg, t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = on1 * x1[e] * up1[e];
+    store8_bf16(sm.rt + (t0 + 1) * kOpStride + 8 * kg, t);
+
+    unpack8<T>(rows.b[0], x0);
+    unpack8<T>(rows.b[1], x1);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = on0 * x0[e] * dn0[e];
+    store8_bf16(sm.bh + t0 * kOpStride + 8 * kg, t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = on1 * x1[e] * dn1[e];
+    store8_bf16(sm.bh + (t0 + 1) * kOpStride + 8 * kg, t);
+    // Token-contiguous tile: the thread's two tokens form one 32-bit pair.
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float up = exp2f(gprev[s][e]);
-      const float ug = exp2f(gtok[s][e]);
-      const float dn = exp2f(-gtok[s][e]);
-      const float tail = exp2f(total[e] - gtok[s][e]);
-      atv[e] = aa[s][e] * up;
-      rtv[e] = rr[s][e] * ug;
-      bhv[e] = bb[s][e] * dn;
-      khv[e] = kk[s][e] * dn;
-      btv[s][e] = bb[s][e] * tail;
-      ktv[s][e] = kk[s][e] * tail;
+      const float gcv = exp2f(total[e]);
+      *reinterpret_cast<uint32_t*>(sm.btT + (8 * kg + e) * kOpStride + t0) =
+          pack_bf16x2(on0 * x0[e] * (gcv * dn0[e]), on1 * x1[e] * (gcv * dn1[e]));
     }
-    uint4 q;
-    q = make_uint4(pack_bf16x2(atv[0], atv[1]), pack_bf16x2(atv[2], atv[3]),
-                   pack_bf16x2(atv[4], atv[5]), pack_bf16x2(atv[6], atv[7]));
-    *reinterpret_cast<uint4*>(sm.at + t * kTileStride + 8 * kg) = q;
-    q = make_uint4(pack_bf16x2(rtv[0], rtv[1]), pack_bf16x2(rtv[2], rtv[3]),
-                   pack_bf16x2(rtv[4], rtv[5]), pack_bf16x2(rtv[6], rtv[7]));
-    *reinterpret_cast<uint4*>(sm.rt + t * kTileStride + 8 * kg) = q;
-    q = make_uint4(pack_bf16x2(bhv[0], bhv[1]), pack_bf16x2(bhv[2], bhv[3]),
-                   pack_bf16x2(bhv[4], bhv[5]), pack_bf16x2(bhv[6], bhv[7]));
-    *reinterpret_cast<uint4*>(sm.bh + t * kTileStride + 8 * kg) = q;
-    q = make_uint4(pack_bf16x2(khv[0], khv[1]), pack_bf16x2(khv[2], khv[3]),
-                   pack_bf16x2(khv[4], khv[5]), pack_bf16x2(khv[6], khv[7]));
-    *reinterpret_cast<uint4*>(sm.kh + t * kTileStride + 8 * kg) = q;
-  }
-  // Token-contiguous tiles: the thread's two tokens form one 32-bit pair.
+
+    unpack8<T>(rows.k[0], x0);
+    unpack8<T>(rows.k[1], x1);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int row = (8 * kg + e) * kTileStride + t0;
-    *reinterpret_cast<uint32_t*>(sm.btT + row) = pack_bf16x2(btv[0][e], btv[1][e]);
-    *reinterpret_cast<uint32_t*>(sm.ktT + row) = pack_bf16x2(ktv[0][e], ktv[1][e]);
-    *reinterpret_cast<uint32_t*>(sm.vT + row) = pack_bf16x2(vv[0][e], vv[1][e]);
+    for (int e = 0; e < 8; ++e) t[e] = on0 * x0[e] * dn0[e];
+    store8_bf16(sm.kh + t0 * kOpStride + 8 * kg, t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = on1 * x1[e] * dn1[e];
+    store8_bf16(sm.kh + (t0 + 1) * kOpStride + 8 * kg, t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float gcv = exp2f(total[e]);
+      *reinterpret_cast<uint32_t*>(sm.ktT + (8 * kg + e) * kOpStride + t0) =
+          pack_bf16x2(on0 * x0[e] * (gcv * dn0[e]), on1 * x1[e] * (gcv * dn1[e]));
+    }
   }
   if (wave == 0 && tp == 0) {
 #pragma unroll
@@ -287,9 +314,17 @@ __device__ Spans prepare(ChunkSmem& sm, const RawRows& raw, const float (&bias)[
   return spans;
 }
 
-// Intra-chunk products: 40 lower-triangular 16x16 tiles of Lab, Lak, Arb,
-// Ark, plus the fp32 inverse of each diagonal block I - Lab_pp. Ends with a
+// Intra-chunk products: the 40 lower-triangular 16x16 blocks of Lab, Lak,
+// Arb, Ark, plus the inverse of each diagonal block I - Lab_pp. Ends with a
 // barrier.
+//
+// A stored block is M[t][i] = sum_k X[t][k] Y[i][k] (X = At or Rt for the
+// target block p, Y = Bh or Kh for the source block q); it is computed
+// transposed (A operand = Y rows, B operand = X rows) so each lane writes 4
+// consecutive i of one row t. Blocks sharing operands are computed together:
+// wave w does all four matrices of its diagonal pair (w, w), then three of
+// the twelve off-diagonal half-pairs ({Lab, Arb} share Bh_q, {Lak, Ark}
+// share Kh_q; both share At_p and Rt_p).
 __device__ void intra_chunk(ChunkSmem& sm) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -297,67 +332,75 @@ __device__ void intra_chunk(ChunkSmem& sm) {
   const int g = lane >> 4;
   const int n = lane & 15;
 
-  // Tile (matrix m, target block p, source block q <= p). The stored tile
-  // is M[t][i] = sum_k X[t][k] Y[i][k]; it is computed transposed (A = Y
-  // rows, B = X rows) so each lane writes 4 consecutive i of one row t.
-  auto tile = [&](int m, int p, int q) {
-    const uint16_t* x = (m < 2) ? sm.at : sm.rt;
-    const uint16_t* y = (m & 1) ? sm.kh : sm.bh;
-    uint16_t* dst = (m == 0) ? sm.lab : (m == 1) ? sm.lak : (m == 2) ? sm.arb : sm.ark;
-    f32x4 acc = zero4();
+  auto store = [&](int m, int p, int q, f32x4 acc, bool strict) {
+    if (p == q) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      acc = mfma16(lds_operand(y, 16 * q + n, 16 * kb + 4 * g),
-                   lds_operand(x, 16 * p + n, 16 * kb + 4 * g), acc);
+      for (int j = 0; j < 4; ++j) {
+        const int i = 4 * g + j;
+        const bool keep = strict ? (i < n) : (i <= n);
+        acc[j] = keep ? acc[j] : 0.0f;
+      }
     }
-    const bool strict = m < 2;
-    const int t = 16 * p + n;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = 16 * q + 4 * g + j;
-      const bool keep = strict ? (i < t) : (i <= t);
-      acc[j] = keep ? acc[j] : 0.0f;
-    }
-    lds_store_transposed(dst + (16 * p) * kTileStride + 16 * q, kTileStride, g, n, acc);
-    if (m == 0 && p == q) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sm.lpp[p][n * 16 + 4 * g + j] = acc[j];
-    }
+    lds_store_transposed(sm.tri[m] + tri_index(p, q) * kTriBlock, kTriStride, g, n, acc);
   };
 
-  // Wave w first computes the diagonal Lab(w, w) and inverts it.
-  tile(0, wave, wave);
+  auto group = [&](int p, int q, bool with_b, bool with_k) {
+    f32x4 lab = zero4(), lak = zero4(), arb = zero4(), ark = zero4();
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const i16x4 xa = lds_operand<kOpStride>(sm.at, 16 * p + n, 16 * kb + 4 * g);
+      const i16x4 xr = lds_operand<kOpStride>(sm.rt, 16 * p + n, 16 * kb + 4 * g);
+      if (with_b) {
+        const i16x4 yb = lds_operand<kOpStride>(sm.bh, 16 * q + n, 16 * kb + 4 * g);
+        lab = mfma16(yb, xa, lab);
+        arb = mfma16(yb, xr, arb);
+      }
+      if (with_k) {
+        const i16x4 yk = lds_operand<kOpStride>(sm.kh, 16 * q + n, 16 * kb + 4 * g);
+        lak = mfma16(yk, xa, lak);
+        ark = mfma16(yk, xr, ark);
+      }
+    }
+    if (with_b) {
+      store(kLab, p, q, lab, true);
+      store(kArb, p, q, arb, false);
+    }
+    if (with_k) {
+      store(kLak, p, q, lak, true);
+      store(kArk, p, q, ark, false);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Diagonal pair first; its Lab block feeds the inverse.
+  group(wave, wave, true, true);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   if (lane < 16) {
-    // Column j of (I - L)^{-1}: x = e_j + L x, rows in order.
-    const float* l = sm.lpp[wave];
+    // Column j of (I - L)^{-1}: x = e_j + L x, rows in order (fp32).
+    const uint16_t* l = tri_block(sm, kLab, wave, wave);
     float x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       float acc = (i == lane) ? 1.0f : 0.0f;
 #pragma unroll
-      for (int m = 0; m < i; ++m) acc = fmaf(l[i * 16 + m], x[m], acc);
+      for (int m = 0; m < i; ++m) acc = fmaf(bf16_float(l[i * kTriStride + m]), x[m], acc);
       x[i] = acc;
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sm.tinv[wave][i * 24 + lane] = to_bf16_bits(x[i]);
+    for (int i = 0; i < 16; ++i) sm.tinv[wave][i * kTriStride + lane] = to_bf16_bits(x[i]);
   }
 
-  // The other 36 tiles, 9 per wave.
-  int item = 0;
+  // Off-diagonal half-pairs: pair index item / 2 over (1,0) (2,0) (2,1)
+  // (3,0) (3,1) (3,2), half item % 2 ({Lab, Arb} or {Lak, Ark}).
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-#pragma unroll
-      for (int q = 0; q <= p; ++q) {
-        if (m == 0 && p == q) continue;
-        if ((item & 3) == wave) tile(m, p, q);
-        ++item;
-      }
-    }
+  for (int r = 0; r < 3; ++r) {
+    const int item = wave + 4 * r;
+    const int pair = item >> 1;
+    const int p = pair < 1 ? 1 : (pair < 3 ? 2 : 3);
+    const int q = pair - (p * (p - 1)) / 2;
+    group(p, q, (item & 1) == 0, (item & 1) == 1);
   }
   __syncthreads();
 }
@@ -365,9 +408,13 @@ __device__ void intra_chunk(ChunkSmem& sm) {
 // State-dependent part of one prepared (sub-)chunk for wave w's value
 // columns. Tokens outside [lo, hi) are zero rows of every operand; their
 // outputs are not stored.
+// out_rs / sda_rs cover the chunk's rows of the output and of state_dot_a
+// (row t at byte t * row_bytes, resp. 2 * t * row_bytes); sda_rs is unused
+// when with_sda is false.
 template <typename T>
-__device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const ChunkFwdParams& p,
-                           int head, int64_t chunk_base, int lo, int hi) {
+__device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const i16x4 (&vs)[4],
+                           __amdgpu_buffer_rsrc_t out_rs, __amdgpu_buffer_rsrc_t sda_rs,
+                           bool with_sda, uint32_t row_bytes, float scale, int lo, int hi) {
   const int tid = threadIdx.x;
   const int w = tid >> 6;
   const int lane = tid & 63;
@@ -379,6 +426,7 @@ __device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const ChunkFwdPar
   for (int kb = 0; kb < 4; ++kb) sb[kb] = to_operand(S[kb]);
 
   // rhs_p = At_p S0 + sum_q Lak_pq V_q      (rows t of block p, cols v of w)
+  // SA_p  = T_pp (rhs_p + sum_{q<p} Lab_pq SA_q)
   f32x4 sa[4];
   i16x4 sab[4];
 #pragma unroll
@@ -386,57 +434,63 @@ __device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const ChunkFwdPar
     f32x4 acc = zero4();
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      acc = mfma16(lds_operand(sm.at, 16 * pb + n, 16 * kb + 4 * g), sb[kb], acc);
+      acc = mfma16(lds_operand<kOpStride>(sm.at, 16 * pb + n, 16 * kb + 4 * g), sb[kb], acc);
     }
 #pragma unroll
     for (int q = 0; q <= pb; ++q) {
-      acc = mfma16(lds_operand(sm.lak, 16 * pb + n, 16 * q + 4 * g),
-                   lds_operand(sm.vT, 16 * w + n, 16 * q + 4 * g), acc);
+      acc = mfma16(lds_operand<kTriStride>(tri_block(sm, kLak, pb, q), n, 4 * g), vs[q], acc);
     }
-    // Block forward substitution: SA_p = T_pp (rhs_p + sum_{q<p} Lab_pq SA_q).
 #pragma unroll
     for (int q = 0; q < pb; ++q) {
-      acc = mfma16(lds_operand(sm.lab, 16 * pb + n, 16 * q + 4 * g), sab[q], acc);
+      acc = mfma16(lds_operand<kTriStride>(tri_block(sm, kLab, pb, q), n, 4 * g), sab[q], acc);
     }
-    sa[pb] = mfma16(lds_operand<24>(sm.tinv[pb], n, 4 * g), to_operand(acc), zero4());
+    sa[pb] = mfma16(lds_operand<kTriStride>(sm.tinv[pb], n, 4 * g), to_operand(acc), zero4());
     sab[pb] = to_operand(sa[pb]);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
-  const int heads = p.num_heads;
-  if (p.state_dot_a != nullptr) {
+  if (with_sda) {
+    const uint32_t off = static_cast<uint32_t>(4 * g) * 2 * row_bytes + 4 * (16 * w + n);
 #pragma unroll
     for (int pb = 0; pb < 4; ++pb) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int t = 16 * pb + 4 * g + j;
         if (t >= lo && t < hi) {
-          p.state_dot_a[((chunk_base + t) * heads + head) * kHead + 16 * w + n] = sa[pb][j];
+          __builtin_amdgcn_raw_buffer_store_b32(
+              __float_as_uint(sa[pb][j]), sda_rs, off,
+              static_cast<int>((16 * pb + j) * 2 * row_bytes), 0);
         }
       }
     }
   }
 
-  // Y^T tiles: rows v of w, cols t of block p.
-  using S16 = typename IoTraits<T>::storage;
-  S16* out = static_cast<S16*>(p.out);
+  // Y^T blocks: rows v of w, cols t of block p; lane (g, n) stores
+  // Y[16p + n][16w + 4g .. 16w + 4g + 3] (8 bytes).
+  const uint32_t y_off = static_cast<uint32_t>(n) * row_bytes + 2 * (16 * w + 4 * g);
 #pragma unroll
   for (int pb = 0; pb < 4; ++pb) {
     f32x4 acc = zero4();
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      acc = mfma16(sb[kb], lds_operand(sm.rt, 16 * pb + n, 16 * kb + 4 * g), acc);
+      acc = mfma16(sb[kb], lds_operand<kOpStride>(sm.rt, 16 * pb + n, 16 * kb + 4 * g), acc);
     }
 #pragma unroll
     for (int q = 0; q <= pb; ++q) {
-      acc = mfma16(sab[q], lds_operand(sm.arb, 16 * pb + n, 16 * q + 4 * g), acc);
-      acc = mfma16(lds_operand(sm.vT, 16 * w + n, 16 * q + 4 * g),
-                   lds_operand(sm.ark, 16 * pb + n, 16 * q + 4 * g), acc);
+      acc = mfma16(sab[q], lds_operand<kTriStride>(tri_block(sm, kArb, pb, q), n, 4 * g), acc);
+      acc = mfma16(vs[q], lds_operand<kTriStride>(tri_block(sm, kArk, pb, q), n, 4 * g), acc);
     }
     const int t = 16 * pb + n;
     if (t >= lo && t < hi) {
-      store4<T>(out + ((chunk_base + t) * heads + head) * kHead + 16 * w + 4 * g,
-                p.scale * acc[0], p.scale * acc[1], p.scale * acc[2], p.scale * acc[3]);
+      u32x2 q;
+      q.x = static_cast<uint32_t>(from_f32<T>(scale * acc[0])) |
+            (static_cast<uint32_t>(from_f32<T>(scale * acc[1])) << 16);
+      q.y = static_cast<uint32_t>(from_f32<T>(scale * acc[2])) |
+            (static_cast<uint32_t>(from_f32<T>(scale * acc[3])) << 16);
+      __builtin_amdgcn_raw_buffer_store_b64(q, out_rs, y_off,
+                                            static_cast<int>(16 * pb * row_bytes), 0);
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   // S' = diag(2^GC) S0 + Bt^T SA + Kt^T V.
@@ -447,16 +501,16 @@ __device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const ChunkFwdPar
     for (int j = 0; j < 4; ++j) acc[j] = S[kb][j] * sm.gc[16 * kb + 4 * g + j];
 #pragma unroll
     for (int pb = 0; pb < 4; ++pb) {
-      acc = mfma16(lds_operand(sm.btT, 16 * kb + n, 16 * pb + 4 * g), sab[pb], acc);
-      acc = mfma16(lds_operand(sm.ktT, 16 * kb + n, 16 * pb + 4 * g),
-                   lds_operand(sm.vT, 16 * w + n, 16 * pb + 4 * g), acc);
+      acc = mfma16(lds_operand<kOpStride>(sm.btT, 16 * kb + n, 16 * pb + 4 * g), sab[pb], acc);
+      acc = mfma16(lds_operand<kOpStride>(sm.ktT, 16 * kb + n, 16 * pb + 4 * g), vs[pb], acc);
     }
     S[kb] = acc;
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
 template <typename T, DecayMode M, typename PoolT>
-__global__ __launch_bounds__(kChunkThreads, 1) void chunk_fwd_kernel(ChunkFwdParams p) {
+__global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdParams p) {
   __shared__ ChunkSmem sm;
   using S16 = typename IoTraits<T>::storage;
 
@@ -484,31 +538,37 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_fwd_kernel(ChunkFwdPar
   }
 
   float bias[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) bias[e] = 0.0f;
   if constexpr (M == DecayMode::kLogits) {
     if (p.bias != nullptr) {
       unpack8<T>(load_row8<T>(p.bias, static_cast<int64_t>(head) * kHead + 8 * kg), bias);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) bias[e] = 0.0f;
     }
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) bias[e] = 0.0f;
   }
 
-  // Wave w's state slice: S[16kb + 4g + j][16w + n] in acc[kb][j].
+  // Wave w's state slice: S[16kb + 4g + j][16w + n] in S[kb][j]. Element
+  // (row, col) of a 64 x 64 state is at byte (row * 64 + col) * size.
+  using PS = typename IoTraits<PoolT>::storage;
+  constexpr int kPoolBytes = static_cast<int>(sizeof(PS));
   const int64_t sbase = (static_cast<int64_t>(slot) * heads + head) * kHead * kHead;
+  const auto state_rs =
+      buffer_rsrc(static_cast<PS*>(p.state) + sbase, kHead * kHead * kPoolBytes);
+  const uint32_t s_off = static_cast<uint32_t>((4 * g) * kHead + 16 * wave + n) * kPoolBytes;
   f32x4 S[4];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      S[kb][j] = pool_load<PoolT>(p.state, sbase + (16 * kb + 4 * g + j) * kHead + 16 * wave + n);
+      const int so = (16 * kb + j) * kHead * kPoolBytes;
+      if constexpr (kPoolBytes == 4) {
+        S[kb][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(state_rs, s_off, so, 0));
+      } else {
+        S[kb][j] = to_f32<PoolT>(__builtin_amdgcn_raw_buffer_load_b16(state_rs, s_off, so, 0));
+      }
     }
   }
 
-  for (int seg = seg_lo; seg < seg_hi; ++seg) {
-    int t_begin, t_end;
+  auto seg_range = [&](int seg, int& t_begin, int& t_end) {
     if (p.seg_offsets != nullptr) {
       t_begin = p.seg_starts[seg];
       t_end = p.seg_ends[seg];
@@ -518,52 +578,128 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_fwd_kernel(ChunkFwdPar
     }
     t_begin = max(t_begin, 0);
     t_end = min(t_end, p.total_tokens);
+  };
+  // Chunk following (seg, c0): c0 + 64 in the same segment, else the start
+  // of the next non-empty segment. Returns false at the end of the sequence.
+  auto next_chunk = [&](int& seg, int& c0, int& c_end) {
+    c0 += kChunk;
+    while (c0 >= c_end) {
+      if (++seg >= seg_hi) return false;
+      seg_range(seg, c0, c_end);
+    }
+    return true;
+  };
+  using S16c = typename IoTraits<T>::storage;
+  const uint32_t row_bytes = static_cast<uint32_t>(heads) * kHead * 2;
+  // Per-lane byte offsets inside a chunk's rows: prepare layout (token
+  // 16w + 2tp [+1], features 8kg..8kg+7) and V operand layout (token
+  // 16q + 4g + e, feature 16w + n; the (q, e) part is a scalar offset).
+  const uint32_t prep_off = static_cast<uint32_t>(16 * wave + 2 * tp) * row_bytes + 16 * kg;
+  const uint32_t v_off = static_cast<uint32_t>(4 * g) * row_bytes + 2 * (16 * wave + n);
+  auto load_rows = [&](ChunkRows& rows, int c0, int ntok) {
+    const int64_t base = (static_cast<int64_t>(c0) * heads + head) * kHead;
+    const uint32_t bytes = static_cast<uint32_t>(ntok) * row_bytes;
+    auto rs = [&](const void* x) { return buffer_rsrc(static_cast<const S16c*>(x) + base, bytes); };
+    const auto rr = rs(p.r), rw = rs(p.decay), rk = rs(p.k), ra = rs(p.a), rb = rs(p.b);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int so = s * static_cast<int>(row_bytes);
+      auto ld = [&](__amdgpu_buffer_rsrc_t r) {
+        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, prep_off, so, 0);
+        return make_uint4(x.x, x.y, x.z, x.w);
+      };
+      rows.r[s] = ld(rr);
+      rows.w[s] = ld(rw);
+      rows.k[s] = ld(rk);
+      rows.a[s] = ld(ra);
+      rows.b[s] = ld(rb);
+    }
+    const auto rv = rs(p.v);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint16_t x = __builtin_amdgcn_raw_buffer_load_b16(
+            rv, v_off, static_cast<int>((16 * q + e) * row_bytes), 0);
+        // MFMA operands are bf16: fp16 tokens are converted, bf16 ones pass.
+        if constexpr (__is_same(T, Bf16)) {
+          rows.vs[q][e] = static_cast<short>(x);
+        } else {
+          rows.vs[q][e] = static_cast<short>(to_bf16_bits(to_f32<T>(x)));
+        }
+      }
+    }
+  };
+
+  ChunkRows rows;
+  {
+    int seg = seg_lo, c0 = 0, c_end = 0;
+    if (seg < seg_hi) seg_range(seg, c0, c_end);
+    if (seg < seg_hi && c0 < c_end) load_rows(rows, c0, min(kChunk, c_end - c0));
+  }
+  for (int seg = seg_lo; seg < seg_hi; ++seg) {
+    int t_begin, t_end;
+    seg_range(seg, t_begin, t_end);
     if (p.boundary != nullptr) {
-      const int64_t bbase = (static_cast<int64_t>(seg) * heads + head) * kHead * kHead;
+      const auto brs = buffer_rsrc(
+          p.boundary + (static_cast<int64_t>(seg) * heads + head) * kHead * kHead,
+          kHead * kHead * 4);
+      const uint32_t b_off = static_cast<uint32_t>((4 * g) * kHead + 16 * wave + n) * 4;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          p.boundary[bbase + (16 * kb + 4 * g + j) * kHead + 16 * wave + n] = S[kb][j];
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(S[kb][j]), brs, b_off,
+                                                (16 * kb + j) * kHead * 4, 0);
         }
       }
     }
     for (int c0 = t_begin; c0 < t_end; c0 += kChunk) {
       const int ntok = min(kChunk, t_end - c0);
-      RawRows raw;
+      int nseg = seg, nc0 = c0, nend = t_end;
+      const bool has_next = next_chunk(nseg, nc0, nend);
+      // One pass over [lo, hi) per iteration. The first pass prepares the
+      // whole chunk; if its decay span is above the limit (strong decay), the
+      // chunk is redone as 16-token sub-chunks, or 4-token ones where a
+      // 16-token block is still too strong, and `rows` keeps this chunk's
+      // rows until the last pass. Otherwise the next chunk's rows are loaded
+      // right after the first prepare, while the products run.
+      Spans spans{};
+      bool whole = true, first = true;
+      int lo = 0, hi = ntok;
+      i16x4 vs[4];
+      for (;;) {
+        const Spans cur = prepare<T, M>(sm, rows, bias, lo, hi);
+        if (first) {
+          first = false;
+          spans = cur;
+          whole = cur.all <= kSpanLimit;
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const int t = 16 * wave + 2 * tp + s;
-        if (t < ntok) {
-          const int64_t off = ((static_cast<int64_t>(c0) + t) * heads + head) * kHead + 8 * kg;
-          raw.r[s] = load_row8<T>(p.r, off);
-          raw.w[s] = load_row8<T>(p.decay, off);
-          raw.k[s] = load_row8<T>(p.k, off);
-          raw.v[s] = load_row8<T>(p.v, off);
-          raw.a[s] = load_row8<T>(p.a, off);
-          raw.b[s] = load_row8<T>(p.b, off);
-        } else {
-          raw.r[s] = raw.w[s] = raw.k[s] = raw.v[s] = raw.a[s] = raw.b[s] =
-              make_uint4(0, 0, 0, 0);
-        }
-      }
-      const Spans spans = prepare<T, M>(sm, raw, bias, 0, ntok);
-      if (spans.all <= kSpanLimit) {
-        intra_chunk(sm);
-        state_pass<T>(sm, S, p, head, c0, 0, ntok);
-      } else {
-        // Strong decay: 16-token sub-chunks, or 4-token ones where needed.
-        for (int q = 0; q < 4 && 16 * q < ntok; ++q) {
-          const int hi16 = min(16 * q + 16, ntok);
-          const int step = spans.block[q] <= kSpanLimit ? 16 : 4;
-          for (int lo = 16 * q; lo < hi16; lo += step) {
-            const int hi = min(lo + step, hi16);
-            prepare<T, M>(sm, raw, bias, lo, hi);
-            intra_chunk(sm);
-            state_pass<T>(sm, S, p, head, c0, lo, hi);
+          for (int q = 0; q < 4; ++q) vs[q] = rows.vs[q];
+          if (!whole) {
+            hi = min(spans.block[0] <= kSpanLimit ? 16 : 4, ntok);
+            continue;
           }
+          if (has_next) load_rows(rows, nc0, min(kChunk, nend - nc0));
         }
+        intra_chunk(sm);
+        {
+          const int64_t base = (static_cast<int64_t>(c0) * heads + head) * kHead;
+          const auto out_rs = buffer_rsrc(static_cast<S16c*>(p.out) + base,
+                                          static_cast<uint32_t>(ntok) * row_bytes);
+          const auto sda_rs = buffer_rsrc(
+              p.state_dot_a != nullptr ? p.state_dot_a + base : nullptr,
+              p.state_dot_a != nullptr ? 2u * static_cast<uint32_t>(ntok) * row_bytes : 0u);
+          state_pass<T>(sm, S, vs, out_rs, sda_rs, p.state_dot_a != nullptr, row_bytes,
+                        p.scale, lo, hi);
+        }
+        if (whole) break;
+        lo = hi;
+        if (lo >= ntok) break;
+        const int q = lo >> 4;
+        hi = min(lo + (spans.block_at(q) <= kSpanLimit ? 16 : 4), min(16 * q + 16, ntok));
       }
+      if (!whole && has_next) load_rows(rows, nc0, min(kChunk, nend - nc0));
     }
   }
 
@@ -571,8 +707,12 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_fwd_kernel(ChunkFwdPar
   for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      pool_store<PoolT>(p.state, sbase + (16 * kb + 4 * g + j) * kHead + 16 * wave + n,
-                        S[kb][j]);
+      const int so = (16 * kb + j) * kHead * kPoolBytes;
+      if constexpr (kPoolBytes == 4) {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(S[kb][j]), state_rs, s_off, so, 0);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b16(from_f32<PoolT>(S[kb][j]), state_rs, s_off, so, 0);
+      }
     }
   }
 }

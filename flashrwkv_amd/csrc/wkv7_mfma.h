@@ -26,6 +26,18 @@ namespace frwkv {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// Buffer resource over [base, base + bytes): loads beyond the range return
+// zero and stores beyond it are dropped by the hardware. Descriptor word 3
+// for gfx9-family raw buffers.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base,
+                                                              uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0,
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
 constexpr int kTileStride = 72;                  // bf16 elements per LDS row
 constexpr int kTileElems = 64 * kTileStride;     // one 64 x 64 tile
 
