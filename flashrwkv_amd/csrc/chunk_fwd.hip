@@ -71,6 +71,13 @@ enum TriMatrix { kLab = 0, kLak = 1, kArb = 2, kArk = 3 };
 
 __device__ __forceinline__ int tri_index(int p, int q) { return (p * (p + 1)) / 2 + q; }
 
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// 2^x on the hardware exponential (v_exp_f32). Every exponent here lies in
+// [-80, 80] (the decay span limit), inside fp32's normal range, so the
+// denormal-range handling of exp2f is not needed.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 struct ChunkSmem {
   uint16_t at[kOpTile];   // [t][k]
   uint16_t rt[kOpTile];   // [t][k]
@@ -139,10 +146,17 @@ __device__ __forceinline__ uint4 load_row8(const void* base, int64_t offset) {
       static_cast<const typename IoTraits<T>::storage*>(base) + offset);
 }
 
-// log2 of the retention, clamped to [kLog2Min, 0].
+// log2 of the retention, clamped to [kLog2Min, 0]. Logits mode:
+// log2 w = -e^{-1/2} log2(e) sigmoid(x); raw mode: log2 w (v_log_f32).
 template <DecayMode M>
 __device__ __forceinline__ float log2_retention(float x) {
-  const float lg = decay_log<M>(x) * kLog2E;
+  float lg;
+  if constexpr (M == DecayMode::kLogits) {
+    const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-kLog2E * x));
+    lg = -(kExpNegHalf * kLog2E) * sig;
+  } else {
+    lg = __builtin_amdgcn_logf(x);
+  }
   return fminf(fmaxf(lg, kLog2Min), 0.0f);
 }
 
@@ -247,20 +261,21 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
   spans.all = span_all;
 
   // Token t0: gp = gp0, g = g0; token t0 + 1: gp = g0, g = g1.
-  float up0[8], up1[8], dn0[8], dn1[8];
+  float up0[8], up1[8], dn0[8], dn1[8], gcv[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    up0[e] = exp2f(g0[e]);   // 2^G(t0)  (= 2^Gp(t0+1))
-    up1[e] = exp2f(g1[e]);   // 2^G(t0+1)
-    dn0[e] = exp2f(-g0[e]);
-    dn1[e] = exp2f(-g1[e]);
+    up0[e] = fast_exp2(g0[e]);   // 2^G(t0)  (= 2^Gp(t0+1))
+    up1[e] = fast_exp2(g1[e]);   // 2^G(t0+1)
+    dn0[e] = fast_exp2(-g0[e]);
+    dn1[e] = fast_exp2(-g1[e]);
+    gcv[e] = fast_exp2(total[e]);
   }
   {
     float x0[8], x1[8], t[8];
     unpack8<T>(rows.a[0], x0);
     unpack8<T>(rows.a[1], x1);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) t[e] = on0 * x0[e] * exp2f(gp0[e]);
+    for (int e = 0; e < 8; ++e) t[e] = on0 * x0[e] * fast_exp2(gp0[e]);
     store8_bf16(sm.at + t0 * kOpStride + 8 * kg, t);
 #pragma unroll
     for (int e = 0; e < 8; ++e) t[e] = on1 * x1[e] * up0[e];
@@ -286,9 +301,8 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
     // Token-contiguous tile: the thread's two tokens form one 32-bit pair.
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float gcv = exp2f(total[e]);
       *reinterpret_cast<uint32_t*>(sm.btT + (8 * kg + e) * kOpStride + t0) =
-          pack_bf16x2(on0 * x0[e] * (gcv * dn0[e]), on1 * x1[e] * (gcv * dn1[e]));
+          pack_bf16x2(on0 * x0[e] * (gcv[e] * dn0[e]), on1 * x1[e] * (gcv[e] * dn1[e]));
     }
 
     unpack8<T>(rows.k[0], x0);
@@ -301,14 +315,13 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
     store8_bf16(sm.kh + (t0 + 1) * kOpStride + 8 * kg, t);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float gcv = exp2f(total[e]);
       *reinterpret_cast<uint32_t*>(sm.ktT + (8 * kg + e) * kOpStride + t0) =
-          pack_bf16x2(on0 * x0[e] * (gcv * dn0[e]), on1 * x1[e] * (gcv * dn1[e]));
+          pack_bf16x2(on0 * x0[e] * (gcv[e] * dn0[e]), on1 * x1[e] * (gcv[e] * dn1[e]));
     }
   }
   if (wave == 0 && tp == 0) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sm.gc[8 * kg + e] = exp2f(total[e]);
+    for (int e = 0; e < 8; ++e) sm.gc[8 * kg + e] = gcv[e];
   }
   __syncthreads();
   return spans;
@@ -374,22 +387,39 @@ __device__ void intra_chunk(ChunkSmem& sm) {
 
   // Diagonal pair first; its Lab block feeds the inverse.
   group(wave, wave, true, true);
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (lane < 16) {
-    // Column j of (I - L)^{-1}: x = e_j + L x, rows in order (fp32).
-    const uint16_t* l = tri_block(sm, kLab, wave, wave);
-    float x[16];
+  // T_pp = (I - L)^{-1} for the strictly lower 16 x 16 block L = Lab_pp:
+  // L^16 = 0, so (I - L)^{-1} = (I + L)(I + L^2)(I + L^4)(I + L^8). All
+  // factors are polynomials in L and commute. With X_R the register layout
+  // "lane (g, n) holds X[n][4g + j]" (A operand of X, C layout of X^T) and
+  // X_C the C layout of X (B operand of X), a product Z = X Y is
+  // Z_C = mfma(X_R, Y_C) and Z_R = mfma(Y_C, X_R).
+  {
+    f32x4 l_r = zero4(), l_c = zero4();
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float acc = (i == lane) ? 1.0f : 0.0f;
-#pragma unroll
-      for (int m = 0; m < i; ++m) acc = fmaf(bf16_float(l[i * kTriStride + m]), x[m], acc);
-      x[i] = acc;
+    for (int kb = 0; kb < 4; ++kb) {
+      const i16x4 xa = lds_operand<kOpStride>(sm.at, 16 * wave + n, 16 * kb + 4 * g);
+      const i16x4 yb = lds_operand<kOpStride>(sm.bh, 16 * wave + n, 16 * kb + 4 * g);
+      l_r = mfma16(yb, xa, l_r);  // lane (g, n): L[n][4g + j]
+      l_c = mfma16(xa, yb, l_c);  // lane (g, n): L[4g + j][n]
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sm.tinv[wave][i * kTriStride + lane] = to_bf16_bits(x[i]);
+    for (int j = 0; j < 4; ++j) {
+      l_r[j] = (4 * g + j < n) ? l_r[j] : 0.0f;
+      l_c[j] = (n < 4 * g + j) ? l_c[j] : 0.0f;
+    }
+    const i16x4 lr = to_operand(l_r), lc = to_operand(l_c);
+    const i16x4 p2c = to_operand(mfma16(lr, lc, zero4()));
+    const i16x4 p2r = to_operand(mfma16(lc, lr, zero4()));
+    const i16x4 p4c = to_operand(mfma16(p2r, p2c, zero4()));
+    const i16x4 p4r = to_operand(mfma16(p2c, p2r, zero4()));
+    const i16x4 p8c = to_operand(mfma16(p4r, p4c, zero4()));
+    f32x4 t = l_r;  // T1 = I + L
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t[j] += (4 * g + j == n) ? 1.0f : 0.0f;
+    t = mfma16(p2c, to_operand(t), t);  // T2 = T1 + P2 T1
+    t = mfma16(p4c, to_operand(t), t);  // T3 = T2 + P4 T2
+    t = mfma16(p8c, to_operand(t), t);  // T  = T3 + P8 T3
+    lds_store_transposed(sm.tinv[wave], kTriStride, g, n, t);
   }
 
   // Off-diagonal half-pairs: pair index item / 2 over (1,0) (2,0) (2,1)
@@ -528,13 +558,15 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
   const int heads = p.num_heads;
   const int seq = blockIdx.x / heads;
   const int head = blockIdx.x % heads;
-  const int slot = p.slots != nullptr ? p.slots[seq] : seq;
+  // Metadata values are workgroup-uniform; readfirstlane keeps them (and
+  // every buffer descriptor derived from them) in scalar registers.
+  const int slot = uniform(p.slots != nullptr ? p.slots[seq] : seq);
   if (slot < 0 || slot >= p.state_slots) return;
 
   int seg_lo = 0, seg_hi = 1;
   if (p.seg_offsets != nullptr) {
-    seg_lo = max(p.seg_offsets[seq], 0);
-    seg_hi = min(p.seg_offsets[seq + 1], p.num_segments);
+    seg_lo = uniform(max(p.seg_offsets[seq], 0));
+    seg_hi = uniform(min(p.seg_offsets[seq + 1], p.num_segments));
   }
 
   float bias[8];
@@ -576,8 +608,8 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
       t_begin = p.cu_seqlens[seq];
       t_end = p.cu_seqlens[seq + 1];
     }
-    t_begin = max(t_begin, 0);
-    t_end = min(t_end, p.total_tokens);
+    t_begin = uniform(max(t_begin, 0));
+    t_end = uniform(min(t_end, p.total_tokens));
   };
   // Chunk following (seg, c0): c0 + 64 in the same segment, else the start
   // of the next non-empty segment. Returns false at the end of the sequence.
