@@ -171,15 +171,27 @@ __device__ __forceinline__ void store8_bf16(uint16_t* dst, const float (&x)[8]) 
   reinterpret_cast<uint2*>(dst)[1] = hi;
 }
 
+// Decay-span verdicts of a prepared range, uniform over the workgroup: is
+// the span of the whole range, resp. of each 16-token block, within the
+// limit of the single-reference factorisation?
 struct Spans {
-  float all;       // -GC over the prepared range
-  float block[4];  // per 16-token block
+  bool whole;
+  bool block[4];
 
   // block[q] for a runtime q without indexing a private array.
-  __device__ __forceinline__ float block_at(int q) const {
+  __device__ __forceinline__ bool block_ok(int q) const {
     return q == 0 ? block[0] : q == 1 ? block[1] : q == 2 ? block[2] : block[3];
   }
 };
+
+// Inclusive-scan step over groups of 8 lanes: lane l adds lane l - N when
+// l % 8 >= N (DPP row shift; the groups never straddle a 16-lane row).
+template <int N>
+__device__ __forceinline__ float scan8_step(float x, int tp) {
+  const float y = __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x110 + N, 0xf, 0xf, true));
+  return tp >= N ? x + y : x;
+}
 
 // Decodes the thread's rows restricted to tokens [lo, hi) of the chunk,
 // scans the decay and writes every scaled operand tile. Ends with a barrier.
@@ -189,8 +201,8 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int tp = lane >> 3;
-  const int kg = lane & 7;
+  const int tp = lane & 7;   // token pair
+  const int kg = lane >> 3;  // feature group
   const int t0 = 16 * wave + 2 * tp;
   const float on0 = (t0 >= lo && t0 < hi) ? 1.0f : 0.0f;
   const float on1 = (t0 + 1 >= lo && t0 + 1 < hi) ? 1.0f : 0.0f;
@@ -209,17 +221,15 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
     }
   }
 
-  // Inclusive scan over the wave's 8 token pairs (lanes 8 apart share kg).
+  // Inclusive scan over the wave's 8 token pairs (the 8 lanes of a feature
+  // group), then the carry of earlier waves through LDS.
   float incl[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) incl[e] = lg0[e] + lg1[e];
-#pragma unroll
-  for (int off = 8; off < 64; off <<= 1) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float y = __shfl_up(incl[e], off, 64);
-      if (lane >= off) incl[e] += y;
-    }
+  for (int e = 0; e < 8; ++e) {
+    float x = lg0[e] + lg1[e];
+    x = scan8_step<1>(x, tp);
+    x = scan8_step<2>(x, tp);
+    incl[e] = scan8_step<4>(x, tp);
   }
   if (tp == 7) {
 #pragma unroll
@@ -228,10 +238,7 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
   __syncthreads();
 
   float g0[8], g1[8], gp0[8], total[8];
-  Spans spans;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) spans.block[q] = 0.0f;
-  float span_all = 0.0f;
+  bool over_all = false, over_block[4] = {false, false, false, false};
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     float base = 0.0f, tot = 0.0f;
@@ -240,25 +247,19 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
       const float x = sm.wave_tot[q][8 * kg + e];
       base += (q < wave) ? x : 0.0f;
       tot += x;
-      spans.block[q] = fmaxf(spans.block[q], -x);
+      over_block[q] |= -x > kSpanLimit;
     }
     total[e] = tot;
-    span_all = fmaxf(span_all, -tot);
+    over_all |= -tot > kSpanLimit;
     gp0[e] = base + incl[e] - lg0[e] - lg1[e];
     g0[e] = gp0[e] + lg0[e];
     g1[e] = g0[e] + lg1[e];
   }
-  // Max over the 8 feature groups (lane bits 0..2): every lane of every wave
-  // ends with the same values, so branches on them are uniform.
+  // Every wave covers all 64 features, so the ballots agree across waves.
+  Spans spans;
+  spans.whole = __builtin_amdgcn_ballot_w64(over_all) == 0;
 #pragma unroll
-  for (int off = 1; off < 8; off <<= 1) {
-    span_all = fmaxf(span_all, __shfl_xor(span_all, off, 64));
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      spans.block[q] = fmaxf(spans.block[q], __shfl_xor(spans.block[q], off, 64));
-    }
-  }
-  spans.all = span_all;
+  for (int q = 0; q < 4; ++q) spans.block[q] = __builtin_amdgcn_ballot_w64(over_block[q]) == 0;
 
   // Token t0: gp = gp0, g = g0; token t0 + 1: gp = g0, g = g1.
   float up0[8], up1[8], dn0[8], dn1[8], gcv[8];
@@ -553,8 +554,8 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
   const int lane = tid & 63;
   const int g = lane >> 4;
   const int n = lane & 15;
-  const int tp = lane >> 3;
-  const int kg = lane & 7;
+  const int tp = lane & 7;   // token pair
+  const int kg = lane >> 3;  // feature group
   const int heads = p.num_heads;
   const int seq = blockIdx.x / heads;
   const int head = blockIdx.x % heads;
@@ -705,11 +706,11 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
         if (first) {
           first = false;
           spans = cur;
-          whole = cur.all <= kSpanLimit;
+          whole = cur.whole;
 #pragma unroll
           for (int q = 0; q < 4; ++q) vs[q] = rows.vs[q];
           if (!whole) {
-            hi = min(spans.block[0] <= kSpanLimit ? 16 : 4, ntok);
+            hi = min(spans.block[0] ? 16 : 4, ntok);
             continue;
           }
           if (has_next) load_rows(rows, nc0, min(kChunk, nend - nc0));
@@ -729,7 +730,7 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
         lo = hi;
         if (lo >= ntok) break;
         const int q = lo >> 4;
-        hi = min(lo + (spans.block_at(q) <= kSpanLimit ? 16 : 4), min(16 * q + 16, ntok));
+        hi = min(lo + (spans.block_ok(q) ? 16 : 4), min(16 * q + 16, ntok));
       }
       if (!whole && has_next) load_rows(rows, nc0, min(kChunk, nend - nc0));
     }
