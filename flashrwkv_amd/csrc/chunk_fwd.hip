@@ -361,18 +361,18 @@ __device__ void intra_chunk(ChunkSmem& sm) {
   auto group = [&](int p, int q, bool with_b, bool with_k) {
     f32x4 lab = zero4(), lak = zero4(), arb = zero4(), ark = zero4();
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const i16x4 xa = lds_operand<kOpStride>(sm.at, 16 * p + n, 16 * kb + 4 * g);
-      const i16x4 xr = lds_operand<kOpStride>(sm.rt, 16 * p + n, 16 * kb + 4 * g);
+    for (int c = 0; c < 64; c += 32) {
+      const i16x8 xa = lds_operand32<kOpStride>(sm.at, 16 * p + n, c, g);
+      const i16x8 xr = lds_operand32<kOpStride>(sm.rt, 16 * p + n, c, g);
       if (with_b) {
-        const i16x4 yb = lds_operand<kOpStride>(sm.bh, 16 * q + n, 16 * kb + 4 * g);
-        lab = mfma16(yb, xa, lab);
-        arb = mfma16(yb, xr, arb);
+        const i16x8 yb = lds_operand32<kOpStride>(sm.bh, 16 * q + n, c, g);
+        lab = mfma32(yb, xa, lab);
+        arb = mfma32(yb, xr, arb);
       }
       if (with_k) {
-        const i16x4 yk = lds_operand<kOpStride>(sm.kh, 16 * q + n, 16 * kb + 4 * g);
-        lak = mfma16(yk, xa, lak);
-        ark = mfma16(yk, xr, ark);
+        const i16x8 yk = lds_operand32<kOpStride>(sm.kh, 16 * q + n, c, g);
+        lak = mfma32(yk, xa, lak);
+        ark = mfma32(yk, xr, ark);
       }
     }
     if (with_b) {
@@ -397,11 +397,11 @@ __device__ void intra_chunk(ChunkSmem& sm) {
   {
     f32x4 l_r = zero4(), l_c = zero4();
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const i16x4 xa = lds_operand<kOpStride>(sm.at, 16 * wave + n, 16 * kb + 4 * g);
-      const i16x4 yb = lds_operand<kOpStride>(sm.bh, 16 * wave + n, 16 * kb + 4 * g);
-      l_r = mfma16(yb, xa, l_r);  // lane (g, n): L[n][4g + j]
-      l_c = mfma16(xa, yb, l_c);  // lane (g, n): L[4g + j][n]
+    for (int c = 0; c < 64; c += 32) {
+      const i16x8 xa = lds_operand32<kOpStride>(sm.at, 16 * wave + n, c, g);
+      const i16x8 yb = lds_operand32<kOpStride>(sm.bh, 16 * wave + n, c, g);
+      l_r = mfma32(yb, xa, l_r);  // lane (g, n): L[n][4g + j]
+      l_c = mfma32(xa, yb, l_c);  // lane (g, n): L[4g + j][n]
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -452,33 +452,64 @@ __device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const i16x4 (&vs)
   const int g = lane >> 4;
   const int n = lane & 15;
 
-  i16x4 sb[4];
-#pragma unroll
-  for (int kb = 0; kb < 4; ++kb) sb[kb] = to_operand(S[kb]);
+  // Operands: S0 (C layout; B operand of products over keys, A operand of
+  // the transposed output product), V slice, then SA as it is solved. A
+  // 32-wide K step concatenates two 16-blocks (see mfma32).
+  i16x8 s01, s23;
+  {
+    const i16x4 s0 = to_operand(S[0]), s1 = to_operand(S[1]);
+    const i16x4 s2 = to_operand(S[2]), s3 = to_operand(S[3]);
+    s01 = cat(s0, s1);
+    s23 = cat(s2, s3);
+  }
+  const i16x8 v01 = cat(vs[0], vs[1]), v23 = cat(vs[2], vs[3]);
+  auto tri16 = [&](int m, int p, int q) {
+    return lds_operand<kTriStride>(tri_block(sm, m, p, q), n, 4 * g);
+  };
+  auto tri32 = [&](int m, int p, int q) {  // blocks (p, q) and (p, q + 1)
+    return cat(tri16(m, p, q), tri16(m, p, q + 1));
+  };
+  // A single 16-wide K block as a 32-wide step with a zero upper half: every
+  // accumulator chain then uses one MFMA shape (same issue cost as the
+  // 16-wide form).
+  const i16x4 z4 = {0, 0, 0, 0};
+  auto lo32 = [&](i16x4 x) { return cat(x, z4); };
 
-  // rhs_p = At_p S0 + sum_q Lak_pq V_q      (rows t of block p, cols v of w)
-  // SA_p  = T_pp (rhs_p + sum_{q<p} Lab_pq SA_q)
-  f32x4 sa[4];
-  i16x4 sab[4];
+  // rhs_p = At_p S0 + sum_{q<=p} Lak_pq V_q: four independent chains.
+  f32x4 rhs[4];
 #pragma unroll
   for (int pb = 0; pb < 4; ++pb) {
-    f32x4 acc = zero4();
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      acc = mfma16(lds_operand<kOpStride>(sm.at, 16 * pb + n, 16 * kb + 4 * g), sb[kb], acc);
-    }
-#pragma unroll
-    for (int q = 0; q <= pb; ++q) {
-      acc = mfma16(lds_operand<kTriStride>(tri_block(sm, kLak, pb, q), n, 4 * g), vs[q], acc);
-    }
-#pragma unroll
-    for (int q = 0; q < pb; ++q) {
-      acc = mfma16(lds_operand<kTriStride>(tri_block(sm, kLab, pb, q), n, 4 * g), sab[q], acc);
-    }
-    sa[pb] = mfma16(lds_operand<kTriStride>(sm.tinv[pb], n, 4 * g), to_operand(acc), zero4());
-    sab[pb] = to_operand(sa[pb]);
-    __builtin_amdgcn_sched_barrier(0);
+    rhs[pb] = mfma32(lds_operand32<kOpStride>(sm.at, 16 * pb + n, 0, g), s01, zero4());
   }
+#pragma unroll
+  for (int pb = 0; pb < 4; ++pb) {
+    rhs[pb] = mfma32(lds_operand32<kOpStride>(sm.at, 16 * pb + n, 32, g), s23, rhs[pb]);
+  }
+  rhs[0] = mfma32(lo32(tri16(kLak, 0, 0)), lo32(vs[0]), rhs[0]);
+  rhs[1] = mfma32(tri32(kLak, 1, 0), v01, rhs[1]);
+  rhs[2] = mfma32(tri32(kLak, 2, 0), v01, rhs[2]);
+  rhs[3] = mfma32(tri32(kLak, 3, 0), v01, rhs[3]);
+  rhs[2] = mfma32(lo32(tri16(kLak, 2, 2)), lo32(vs[2]), rhs[2]);
+  rhs[3] = mfma32(tri32(kLak, 3, 2), v23, rhs[3]);
+
+  // Block forward substitution SA_p = T_pp (rhs_p + sum_{q<p} Lab_pq SA_q).
+  auto tinv = [&](int pb) { return lds_operand<kTriStride>(sm.tinv[pb], n, 4 * g); };
+  f32x4 sa[4];
+  i16x4 sab[4];
+  sa[0] = mfma32(lo32(tinv(0)), lo32(to_operand(rhs[0])), zero4());
+  sab[0] = to_operand(sa[0]);
+  rhs[1] = mfma32(lo32(tri16(kLab, 1, 0)), lo32(sab[0]), rhs[1]);
+  sa[1] = mfma32(lo32(tinv(1)), lo32(to_operand(rhs[1])), zero4());
+  sab[1] = to_operand(sa[1]);
+  const i16x8 sa01 = cat(sab[0], sab[1]);
+  rhs[2] = mfma32(tri32(kLab, 2, 0), sa01, rhs[2]);
+  rhs[3] = mfma32(tri32(kLab, 3, 0), sa01, rhs[3]);
+  sa[2] = mfma32(lo32(tinv(2)), lo32(to_operand(rhs[2])), zero4());
+  sab[2] = to_operand(sa[2]);
+  rhs[3] = mfma32(lo32(tri16(kLab, 3, 2)), lo32(sab[2]), rhs[3]);
+  sa[3] = mfma32(lo32(tinv(3)), lo32(to_operand(rhs[3])), zero4());
+  sab[3] = to_operand(sa[3]);
+  const i16x8 sa23 = cat(sab[2], sab[3]);
 
   if (with_sda) {
     const uint32_t off = static_cast<uint32_t>(4 * g) * 2 * row_bytes + 4 * (16 * w + n);
@@ -496,47 +527,64 @@ __device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const i16x4 (&vs)
     }
   }
 
-  // Y^T blocks: rows v of w, cols t of block p; lane (g, n) stores
-  // Y[16p + n][16w + 4g .. 16w + 4g + 3] (8 bytes).
+  // Y^T blocks (rows v of w, cols t of block p) and S' = diag(2^GC) S0 +
+  // Bt^T SA + Kt^T V: eight independent chains.
+  f32x4 y[4], sn[4];
+#pragma unroll
+  for (int pb = 0; pb < 4; ++pb) {
+    y[pb] = mfma32(s01, lds_operand32<kOpStride>(sm.rt, 16 * pb + n, 0, g), zero4());
+  }
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sn[kb][j] = S[kb][j] * sm.gc[16 * kb + 4 * g + j];
+    sn[kb] = mfma32(lds_operand32<kOpStride>(sm.btT, 16 * kb + n, 0, g), sa01, sn[kb]);
+  }
+#pragma unroll
+  for (int pb = 0; pb < 4; ++pb) {
+    y[pb] = mfma32(s23, lds_operand32<kOpStride>(sm.rt, 16 * pb + n, 32, g), y[pb]);
+  }
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    sn[kb] = mfma32(lds_operand32<kOpStride>(sm.btT, 16 * kb + n, 32, g), sa23, sn[kb]);
+  }
+  y[0] = mfma32(lo32(sab[0]), lo32(tri16(kArb, 0, 0)), y[0]);
+  y[1] = mfma32(sa01, tri32(kArb, 1, 0), y[1]);
+  y[2] = mfma32(sa01, tri32(kArb, 2, 0), y[2]);
+  y[3] = mfma32(sa01, tri32(kArb, 3, 0), y[3]);
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    sn[kb] = mfma32(lds_operand32<kOpStride>(sm.ktT, 16 * kb + n, 0, g), v01, sn[kb]);
+  }
+  y[0] = mfma32(lo32(vs[0]), lo32(tri16(kArk, 0, 0)), y[0]);
+  y[1] = mfma32(v01, tri32(kArk, 1, 0), y[1]);
+  y[2] = mfma32(v01, tri32(kArk, 2, 0), y[2]);
+  y[3] = mfma32(v01, tri32(kArk, 3, 0), y[3]);
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    sn[kb] = mfma32(lds_operand32<kOpStride>(sm.ktT, 16 * kb + n, 32, g), v23, sn[kb]);
+  }
+  y[2] = mfma32(lo32(sab[2]), lo32(tri16(kArb, 2, 2)), y[2]);
+  y[3] = mfma32(sa23, tri32(kArb, 3, 2), y[3]);
+  y[2] = mfma32(lo32(vs[2]), lo32(tri16(kArk, 2, 2)), y[2]);
+  y[3] = mfma32(v23, tri32(kArk, 3, 2), y[3]);
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) S[kb] = sn[kb];
+
+  // Lane (g, n) stores Y[16p + n][16w + 4g .. 16w + 4g + 3] (8 bytes).
   const uint32_t y_off = static_cast<uint32_t>(n) * row_bytes + 2 * (16 * w + 4 * g);
 #pragma unroll
   for (int pb = 0; pb < 4; ++pb) {
-    f32x4 acc = zero4();
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      acc = mfma16(sb[kb], lds_operand<kOpStride>(sm.rt, 16 * pb + n, 16 * kb + 4 * g), acc);
-    }
-#pragma unroll
-    for (int q = 0; q <= pb; ++q) {
-      acc = mfma16(sab[q], lds_operand<kTriStride>(tri_block(sm, kArb, pb, q), n, 4 * g), acc);
-      acc = mfma16(vs[q], lds_operand<kTriStride>(tri_block(sm, kArk, pb, q), n, 4 * g), acc);
-    }
     const int t = 16 * pb + n;
     if (t >= lo && t < hi) {
       u32x2 q;
-      q.x = static_cast<uint32_t>(from_f32<T>(scale * acc[0])) |
-            (static_cast<uint32_t>(from_f32<T>(scale * acc[1])) << 16);
-      q.y = static_cast<uint32_t>(from_f32<T>(scale * acc[2])) |
-            (static_cast<uint32_t>(from_f32<T>(scale * acc[3])) << 16);
+      q.x = static_cast<uint32_t>(from_f32<T>(scale * y[pb][0])) |
+            (static_cast<uint32_t>(from_f32<T>(scale * y[pb][1])) << 16);
+      q.y = static_cast<uint32_t>(from_f32<T>(scale * y[pb][2])) |
+            (static_cast<uint32_t>(from_f32<T>(scale * y[pb][3])) << 16);
       __builtin_amdgcn_raw_buffer_store_b64(q, out_rs, y_off,
                                             static_cast<int>(16 * pb * row_bytes), 0);
     }
-    __builtin_amdgcn_sched_barrier(0);
-  }
-
-  // S' = diag(2^GC) S0 + Bt^T SA + Kt^T V.
-#pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
-    f32x4 acc;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] = S[kb][j] * sm.gc[16 * kb + 4 * g + j];
-#pragma unroll
-    for (int pb = 0; pb < 4; ++pb) {
-      acc = mfma16(lds_operand<kOpStride>(sm.btT, 16 * kb + n, 16 * pb + 4 * g), sab[pb], acc);
-      acc = mfma16(lds_operand<kOpStride>(sm.ktT, 16 * kb + n, 16 * pb + 4 * g), vs[pb], acc);
-    }
-    S[kb] = acc;
-    __builtin_amdgcn_sched_barrier(0);
   }
 }
 

@@ -41,8 +41,29 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base,
 constexpr int kTileStride = 72;                  // bf16 elements per LDS row
 constexpr int kTileElems = 64 * kTileStride;     // one 64 x 64 tile
 
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
 __device__ __forceinline__ f32x4 mfma16(i16x4 a, i16x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// v_mfma_f32_16x16x32_bf16: same issue cost as the 16x16x16 form on gfx950
+// for twice the work. An accumulator chain must keep one MFMA shape: with
+// this toolchain, a 16x16x16 MFMA taking a 16x16x32 result as its
+// accumulator a few instructions later produced wrong sums on MI355X (the
+// wait states between the two were too few), so single 16-blocks are fed as
+// zero-padded 32-wide steps instead. Operand register e of lane (g, n) carries
+// k = 4g + e (e < 4) and k = 16 + 4g + (e - 4) (e >= 4) of the 32-wide K
+// block: two 16-row blocks in C layout concatenate into one operand, and an
+// LDS operand is two 8-byte reads 16 columns apart.
+__device__ __forceinline__ f32x4 mfma32(i16x8 a, i16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ i16x8 cat(i16x4 lo, i16x4 hi) {
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
@@ -80,6 +101,14 @@ __device__ __forceinline__ i16x4 to_operand(f32x4 c) {
 template <int Stride = kTileStride>
 __device__ __forceinline__ i16x4 lds_operand(const uint16_t* tile, int row, int col) {
   return *reinterpret_cast<const i16x4*>(tile + row * Stride + col);
+}
+
+// 32-wide K operand from an LDS tile: columns col + 4g .. +3 and
+// col + 16 + 4g .. +3 of row `row` (lane group g), matching mfma32's K order.
+template <int Stride = kTileStride>
+__device__ __forceinline__ i16x8 lds_operand32(const uint16_t* tile, int row, int col, int g) {
+  return cat(lds_operand<Stride>(tile, row, col + 4 * g),
+             lds_operand<Stride>(tile, row, col + 16 + 4 * g));
 }
 
 // Stores a C-layout tile transposed: lane (g, n) writes its 4 values to
