@@ -91,3 +91,25 @@ def statetune_forward_internal(sequence_chunk_offsets, chunk_token_starts,
     ops.statetune_forward_internal(
         sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, state, r, decay,
         k, v, a, b, output, boundary, state_dot_a, float(scale), int(decay_mode))
+
+
+def statetune_recurrent_fp32io16_backward(sequence_chunk_offsets, chunk_token_starts,
+                                          chunk_token_ends, final_state, r, decay_logits, k,
+                                          v, a, b, state_dot_a, grad_output, grad_final_state,
+                                          boundary, grad_r, grad_decay_logits, grad_k, grad_v,
+                                          grad_a, grad_b, grad_initial_state, scale=1.0):
+    ops.statetune_recurrent_fp32io16_backward(
+        sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, final_state, r,
+        decay_logits, k, v, a, b, state_dot_a, grad_output, grad_final_state, boundary,
+        grad_r, grad_decay_logits, grad_k, grad_v, grad_a, grad_b, grad_initial_state,
+        float(scale))
+
+
+def statetune_backward_internal(sequence_chunk_offsets, chunk_token_starts, chunk_token_ends,
+                                r, decay, k, v, a, b, grad_output, grad_final_state, boundary,
+                                grad_r, grad_decay, grad_k, grad_v, grad_a, grad_b,
+                                grad_initial_state, scale, decay_mode):
+    ops.statetune_backward_internal(
+        sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, r, decay, k, v, a, b,
+        grad_output, grad_final_state, boundary, grad_r, grad_decay, grad_k, grad_v, grad_a,
+        grad_b, grad_initial_state, float(scale), int(decay_mode))

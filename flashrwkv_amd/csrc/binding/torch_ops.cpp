@@ -541,6 +541,115 @@ void statetune_forward_internal(Tensor offsets, Tensor starts, Tensor ends, Tens
                          boundary, state_dot_a, scale, static_cast<int>(decay_mode));
 }
 
+// Reference statetune_recurrent_fp32io16_backward.cpp:34-82: optional
+// gradient outputs (allocated here when omitted), final_state and
+// state_dot_a accepted for contract compatibility (the recompute-based
+// backward does not need them).
+void statetune_backward_impl(const Tensor& offsets, const Tensor& starts, const Tensor& ends,
+                             const Tensor& r, const Tensor& decay, const Tensor& k,
+                             const Tensor& v, const Tensor& a, const Tensor& b,
+                             const std::optional<Tensor>& grad_output,
+                             const std::optional<Tensor>& grad_final_state,
+                             const Tensor& boundary, std::optional<Tensor> grad_r,
+                             std::optional<Tensor> grad_decay, std::optional<Tensor> grad_k,
+                             std::optional<Tensor> grad_v, std::optional<Tensor> grad_a,
+                             std::optional<Tensor> grad_b,
+                             std::optional<Tensor> grad_initial_state, int64_t num_sequences,
+                             double scale, int decay_mode) {
+  TORCH_CHECK(std::isfinite(scale), "scale must be finite");
+  check_chunk_tokens(r, decay, k, v, a, b, /*bf16_only=*/false);
+  const int64_t heads = r.size(1);
+  check_device_contiguous(boundary, "boundary");
+  TORCH_CHECK(boundary.scalar_type() == at::kFloat && boundary.dim() == 4 &&
+                  boundary.size(0) == starts.numel() && boundary.size(1) == heads &&
+                  boundary.size(2) == 64 && boundary.size(3) == 64,
+              "boundary must have shape [chunks,H,64,64] float32");
+  for (const auto* t : {&offsets, &starts, &ends}) {
+    check_device_contiguous(*t, "chunk metadata");
+    TORCH_CHECK(t->scalar_type() == at::kInt && t->dim() == 1, "chunk metadata must be int32 1-D");
+    TORCH_CHECK(t->device() == r.device(), "chunk metadata must share the token device");
+  }
+  TORCH_CHECK(offsets.numel() == num_sequences + 1,
+              "sequence_chunk_offsets must have shape [B+1]");
+  TORCH_CHECK(starts.numel() > 0 && ends.numel() == starts.numel(),
+              "chunk token metadata must have matching shape [C]");
+  if (grad_output.has_value() && grad_output->defined()) {
+    check_device_contiguous(*grad_output, "grad_output");
+    TORCH_CHECK(grad_output->sizes() == r.sizes() && grad_output->scalar_type() == r.scalar_type(),
+                "grad_output must match r");
+  }
+  const auto state_opts = r.options().dtype(at::kFloat);
+  if (grad_final_state.has_value() && grad_final_state->defined()) {
+    check_device_contiguous(*grad_final_state, "grad_final_state");
+    TORCH_CHECK(grad_final_state->scalar_type() == at::kFloat &&
+                    grad_final_state->dim() == 4 && grad_final_state->size(0) == num_sequences &&
+                    grad_final_state->size(1) == heads && grad_final_state->size(2) == 64 &&
+                    grad_final_state->size(3) == 64,
+                "grad_final_state must have shape [B,H,64,64] float32");
+  }
+  auto token_grad = [&](std::optional<Tensor>& t, const char* name) {
+    if (!t.has_value() || !t->defined()) t = at::empty_like(r);
+    check_device_contiguous(*t, name);
+    TORCH_CHECK(t->sizes() == r.sizes() && t->scalar_type() == r.scalar_type(), name,
+                " must match r");
+    return t->data_ptr();
+  };
+  void* gr = token_grad(grad_r, "grad_r");
+  void* gd = token_grad(grad_decay, "grad_decay_logits");
+  void* gk = token_grad(grad_k, "grad_k");
+  void* gv = token_grad(grad_v, "grad_v");
+  void* ga = token_grad(grad_a, "grad_a");
+  void* gb = token_grad(grad_b, "grad_b");
+  if (!grad_initial_state.has_value() || !grad_initial_state->defined()) {
+    grad_initial_state = at::empty({num_sequences, heads, 64, 64}, state_opts);
+  }
+  check_device_contiguous(*grad_initial_state, "grad_initial_state");
+  TORCH_CHECK(grad_initial_state->scalar_type() == at::kFloat &&
+                  grad_initial_state->numel() == num_sequences * heads * 64 * 64,
+              "grad_initial_state must have shape [B,H,64,64] float32");
+  c10::DeviceGuard guard(r.device());
+  const bool has_dy = grad_output.has_value() && grad_output->defined();
+  const bool has_ds = grad_final_state.has_value() && grad_final_state->defined();
+  check_rc(frwkv_statetune_backward(
+      io_code(r.scalar_type()), decay_mode, static_cast<int32_t>(num_sequences),
+      static_cast<int32_t>(heads), 64, static_cast<int32_t>(r.size(0)),
+      static_cast<int32_t>(starts.numel()), offsets.data_ptr<int32_t>(),
+      starts.data_ptr<int32_t>(), ends.data_ptr<int32_t>(), boundary.data_ptr<float>(),
+      r.data_ptr(), decay.data_ptr(), nullptr, k.data_ptr(), v.data_ptr(), a.data_ptr(),
+      b.data_ptr(), has_dy ? grad_output->data_ptr() : nullptr,
+      has_ds ? grad_final_state->data_ptr<float>() : nullptr, gr, gd, gk, gv, ga, gb,
+      grad_initial_state->data_ptr<float>(), static_cast<float>(scale), current_stream(r)));
+}
+
+void statetune_recurrent_fp32io16_backward(
+    Tensor offsets, Tensor starts, Tensor ends, Tensor final_state, Tensor r,
+    Tensor decay_logits, Tensor k, Tensor v, Tensor a, Tensor b, Tensor state_dot_a,
+    std::optional<Tensor> grad_output, std::optional<Tensor> grad_final_state, Tensor boundary,
+    std::optional<Tensor> grad_r, std::optional<Tensor> grad_decay_logits,
+    std::optional<Tensor> grad_k, std::optional<Tensor> grad_v, std::optional<Tensor> grad_a,
+    std::optional<Tensor> grad_b, std::optional<Tensor> grad_initial_state, double scale) {
+  (void)state_dot_a;
+  check_device_contiguous(final_state, "final_state");
+  statetune_backward_impl(offsets, starts, ends, r, decay_logits, k, v, a, b, grad_output,
+                          grad_final_state, boundary, grad_r, grad_decay_logits, grad_k,
+                          grad_v, grad_a, grad_b, grad_initial_state, final_state.size(0),
+                          scale, FRWKV_DECAY_LOGITS);
+}
+
+void statetune_backward_internal(
+    Tensor offsets, Tensor starts, Tensor ends, Tensor r, Tensor decay, Tensor k, Tensor v,
+    Tensor a, Tensor b, std::optional<Tensor> grad_output,
+    std::optional<Tensor> grad_final_state, Tensor boundary, Tensor grad_r, Tensor grad_decay,
+    Tensor grad_k, Tensor grad_v, Tensor grad_a, Tensor grad_b, Tensor grad_initial_state,
+    double scale, int64_t decay_mode) {
+  TORCH_CHECK(decay_mode == FRWKV_DECAY_LOGITS || decay_mode == FRWKV_DECAY_RAW_W,
+              "decay_mode must be 0 (logits) or 1 (raw retention)");
+  statetune_backward_impl(offsets, starts, ends, r, decay, k, v, a, b, grad_output,
+                          grad_final_state, boundary, grad_r, grad_decay, grad_k, grad_v,
+                          grad_a, grad_b, grad_initial_state, offsets.numel() - 1, scale,
+                          static_cast<int>(decay_mode));
+}
+
 }  // namespace
 
 TORCH_LIBRARY(flashrwkv_amd, m) {
@@ -602,4 +711,21 @@ TORCH_LIBRARY(flashrwkv_amd, m) {
       "Tensor decay, Tensor k, Tensor v, Tensor a, Tensor b, Tensor(b!) output, "
       "Tensor(c!) boundary, Tensor(d!) state_dot_a, float scale, int decay_mode) -> ()",
       &statetune_forward_internal);
+  m.def(
+      "statetune_recurrent_fp32io16_backward(Tensor sequence_chunk_offsets, "
+      "Tensor chunk_token_starts, Tensor chunk_token_ends, Tensor final_state, Tensor r, "
+      "Tensor decay_logits, Tensor k, Tensor v, Tensor a, Tensor b, Tensor state_dot_a, "
+      "Tensor? grad_output, Tensor? grad_final_state, Tensor boundary, "
+      "Tensor(a!)? grad_r, Tensor(b!)? grad_decay_logits, Tensor(c!)? grad_k, "
+      "Tensor(d!)? grad_v, Tensor(e!)? grad_a, Tensor(f!)? grad_b, "
+      "Tensor(g!)? grad_initial_state, float scale=1.0) -> ()",
+      &statetune_recurrent_fp32io16_backward);
+  m.def(
+      "statetune_backward_internal(Tensor sequence_chunk_offsets, Tensor chunk_token_starts, "
+      "Tensor chunk_token_ends, Tensor r, Tensor decay, Tensor k, Tensor v, Tensor a, "
+      "Tensor b, Tensor? grad_output, Tensor? grad_final_state, Tensor boundary, "
+      "Tensor(a!) grad_r, Tensor(b!) grad_decay, Tensor(c!) grad_k, Tensor(d!) grad_v, "
+      "Tensor(e!) grad_a, Tensor(f!) grad_b, Tensor(g!) grad_initial_state, float scale, "
+      "int decay_mode) -> ()",
+      &statetune_backward_internal);
 }

@@ -47,36 +47,10 @@
 #include "capi_internal.h"
 #include "wkv7_device.h"
 #include "wkv7_mfma.h"
+#include "chunk_common.h"
 
 namespace frwkv {
 namespace {
-
-constexpr int kChunk = 64;
-constexpr int kHead = 64;
-constexpr int kChunkThreads = 256;
-constexpr float kSpanLimit = 80.0f;   // log2 units
-constexpr float kLog2Min = -20.0f;    // per-token clamp of log2 retention
-
-// Operand tiles: 64 rows x 64 bf16, row stride 68 elements (136 B = 34
-// dwords): the 16 rows of an 8-byte operand read hit 16 distinct dword pairs.
-constexpr int kOpStride = 68;
-constexpr int kOpTile = 64 * kOpStride;
-// Lower-triangular C x C matrices: the 10 blocks (p, q <= p) of 16 x 16,
-// packed, row stride 20 (40 B = 10 dwords, conflict-free the same way).
-constexpr int kTriStride = 20;
-constexpr int kTriBlock = 16 * kTriStride;
-constexpr int kTriBlocks = 10;
-
-enum TriMatrix { kLab = 0, kLak = 1, kArb = 2, kArk = 3 };
-
-__device__ __forceinline__ int tri_index(int p, int q) { return (p * (p + 1)) / 2 + q; }
-
-__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
-
-// 2^x on the hardware exponential (v_exp_f32). Every exponent here lies in
-// [-80, 80] (the decay span limit), inside fp32's normal range, so the
-// denormal-range handling of exp2f is not needed.
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 struct ChunkSmem {
   uint16_t at[kOpTile];   // [t][k]
@@ -132,45 +106,6 @@ struct ChunkRows {
   i16x4 vs[4];
 };
 
-template <typename T>
-__device__ __forceinline__ void unpack8(uint4 q, float (&out)[8]) {
-  const typename IoTraits<T>::storage* p =
-      reinterpret_cast<const typename IoTraits<T>::storage*>(&q);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) out[e] = to_f32<T>(p[e]);
-}
-
-template <typename T>
-__device__ __forceinline__ uint4 load_row8(const void* base, int64_t offset) {
-  return *reinterpret_cast<const uint4*>(
-      static_cast<const typename IoTraits<T>::storage*>(base) + offset);
-}
-
-// log2 of the retention, clamped to [kLog2Min, 0]. Logits mode:
-// log2 w = -e^{-1/2} log2(e) sigmoid(x); raw mode: log2 w (v_log_f32).
-template <DecayMode M>
-__device__ __forceinline__ float log2_retention(float x) {
-  float lg;
-  if constexpr (M == DecayMode::kLogits) {
-    const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-kLog2E * x));
-    lg = -(kExpNegHalf * kLog2E) * sig;
-  } else {
-    lg = __builtin_amdgcn_logf(x);
-  }
-  return fminf(fmaxf(lg, kLog2Min), 0.0f);
-}
-
-// 8 floats -> 8 bf16 at an 8-byte aligned LDS address (two 8-byte writes).
-__device__ __forceinline__ void store8_bf16(uint16_t* dst, const float (&x)[8]) {
-  uint2 lo, hi;
-  lo.x = pack_bf16x2(x[0], x[1]);
-  lo.y = pack_bf16x2(x[2], x[3]);
-  hi.x = pack_bf16x2(x[4], x[5]);
-  hi.y = pack_bf16x2(x[6], x[7]);
-  reinterpret_cast<uint2*>(dst)[0] = lo;
-  reinterpret_cast<uint2*>(dst)[1] = hi;
-}
-
 // Decay-span verdicts of a prepared range, uniform over the workgroup: is
 // the span of the whole range, resp. of each 16-token block, within the
 // limit of the single-reference factorisation?
@@ -183,15 +118,6 @@ struct Spans {
     return q == 0 ? block[0] : q == 1 ? block[1] : q == 2 ? block[2] : block[3];
   }
 };
-
-// Inclusive-scan step over groups of 8 lanes: lane l adds lane l - N when
-// l % 8 >= N (DPP row shift; the groups never straddle a 16-lane row).
-template <int N>
-__device__ __forceinline__ float scan8_step(float x, int tp) {
-  const float y = __int_as_float(
-      __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x110 + N, 0xf, 0xf, true));
-  return tp >= N ? x + y : x;
-}
 
 // Decodes the thread's rows restricted to tokens [lo, hi) of the chunk,
 // scans the decay and writes every scaled operand tile. Ends with a barrier.

@@ -157,6 +157,37 @@ int frwkv_statetune_forward(int io_dtype, int decay_mode, int32_t num_sequences,
                             void* output, float* boundary, float* state_dot_a,
                             float scale, void* stream);
 
+/*
+ * Training (StateTune) backward. Recomputes every chunk's forward quantities
+ * from boundary (the state at each chunk start, as written by
+ * frwkv_statetune_forward) and runs the chunked adjoint in reverse; it never
+ * divides by the decay. Each chunk must span at most 64 tokens (the training
+ * wrapper splits longer caller chunks and keeps their boundaries). grad_output
+ * [total_tokens,H,D] (io dtype) and grad_final_state [B,H,D,D] fp32 may be
+ * NULL (zero). Writes every token gradient (grad_decay is dL/d(decay input):
+ * logits or retention per decay_mode) and grad_initial_state [B,H,D,D] fp32.
+ * A chunk longer than 64 tokens, or whose decay span exceeds the kernels'
+ * single-reference limit, makes its sequence's gradients NaN.
+ * Replaces statetune_recurrent_fp32io16_backward_cuda
+ * (csrc/sm90/tmix/wkv7/statetune_recurrent_fp32io16_backward.cu:49-676;
+ * binding statetune_recurrent_fp32io16_backward.cpp:34-82). head_size 64.
+ */
+int frwkv_statetune_backward(int io_dtype, int decay_mode, int32_t num_sequences,
+                             int32_t num_heads, int32_t head_size,
+                             int32_t total_tokens, int32_t num_chunks,
+                             const int32_t* sequence_chunk_offsets,
+                             const int32_t* chunk_token_starts,
+                             const int32_t* chunk_token_ends,
+                             const float* boundary, const void* r,
+                             const void* decay, const void* decay_bias,
+                             const void* k, const void* v, const void* a,
+                             const void* b, const void* grad_output,
+                             const float* grad_final_state, void* grad_r,
+                             void* grad_decay, void* grad_k, void* grad_v,
+                             void* grad_a, void* grad_b,
+                             float* grad_initial_state, float scale,
+                             void* stream);
+
 #ifdef __cplusplus
 }
 #endif
