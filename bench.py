@@ -37,6 +37,29 @@ if str(ROOT) not in sys.path:
 
 HBM_PEAK_GBPS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
+
+# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, mean KiB per dispatch of each
+# kernel at its bench workload (the traffic summaries under profiles/ give the
+# runs and their commands). Calibration: a 256 MiB device copy (--workload copy) reads
+# FETCH_SIZE 131085.1 KiB and WRITE_SIZE 262144.0 KiB per dispatch, so fetched
+# bytes are FETCH_SIZE * 1024 * (262144 / 131085.1) and written bytes
+# WRITE_SIZE * 1024.
+_COPY_KIB = 262144.0
+_COPY_FETCH_KIB = 131085.1
+_COPY_WRITE_KIB = 262144.0
+PMC_KIB = {  # kernel -> (FETCH_SIZE, WRITE_SIZE)
+    "recurrent_fp32_kernel<64,64,64,Bf16,kRawW>": (85810.9, 165163.6),
+    "chunk_fwd_kernel<Bf16,kRawW,float>": (790724.0, 270338.2),
+    "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": (790893.0, 1318970.7),
+    "chunk_bwd_kernel<Bf16,kRawW>": (1730522.7, 2159326.8),
+}
+
+
+def pmc_traffic(kernel: str) -> int:
+    """Measured HBM bytes per dispatch of ``kernel`` (calibrated counters)."""
+    fetch, write = PMC_KIB[kernel]
+    return int(round(fetch * 1024 * _COPY_KIB / _COPY_FETCH_KIB
+                     + write * 1024 * _COPY_KIB / _COPY_WRITE_KIB))
 METRIC = "WKV7 tokens/s + % roofline (HBM GB/s decode, MFMA TFLOP/s chunked), h32d64"
 
 
@@ -46,10 +69,13 @@ def _parse():
     p.add_argument("--steps", type=int, default=1000)
     p.add_argument("--warmup", type=int, default=50)
     p.add_argument("--workload", default="all",
-                   choices=("all", "decode", "prefill"),
-                   help="all: decode headline line plus the chunked-prefill leg")
+                   choices=("all", "decode", "prefill", "training", "recurrent_long",
+                            "copy"),
+                   help="all: decode headline line plus the prefill, training and "
+                        "long-sequence legs")
     p.add_argument("--prefill-steps", type=int, default=20)
-    p.add_argument("--cpu-seconds", type=float, default=10.0,
+    p.add_argument("--training-steps", type=int, default=10)
+    p.add_argument("--cpu-seconds", type=float, default=8.0,
                    help="bound on the CPU-baseline sample (0 disables it)")
     return p.parse_args()
 
@@ -203,7 +229,7 @@ def bench_decode(args):
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": pmc_traffic("recurrent_fp32_kernel<64,64,64,Bf16,kRawW>"),
             "kernel": "recurrent_fp32_kernel<64,64,64,Bf16,kRawW>",
             "algorithmic_bytes_per_launch": nbytes,
         },
@@ -320,7 +346,8 @@ def bench_prefill(args):
                      "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
                      "frac_of_attainable": round(tflops / attainable, 4),
                      "attainable": round(attainable, 1),
-                     "traffic": None, "kernel": "chunk_fwd_kernel<Bf16,kRawW,float>",
+                     "traffic": pmc_traffic("chunk_fwd_kernel<Bf16,kRawW,float>"),
+                     "kernel": "chunk_fwd_kernel<Bf16,kRawW,float>",
                      "algorithmic_flops_per_launch": flops},
         "hbm": {"achieved_GBps": round(gbps, 1), "peak": HBM_PEAK_GBPS,
                 "frac": round(gbps / HBM_PEAK_GBPS, 4),
@@ -329,6 +356,187 @@ def bench_prefill(args):
     if args.cpu_seconds > 0:
         out["cpu_baseline"] = cpu_baseline_prefill(t_len, heads, args.cpu_seconds)
     return out
+
+
+def bench_training(args):
+    """chunked forward + backward (StateTune), B=8, T=4096,
+    H=64, D=64, chunk 64, bf16 io, raw retention, S0 ~ N(0, 0.1), dY ~ N(0, 1),
+    dS_T ~ N(0, 0.01). One step = autograd forward + backward."""
+    import torch
+
+    import flashrwkv_amd
+    from flashrwkv_amd import workloads
+    from flashrwkv_amd.tmix.wkv7.statetune import statetune_recurrent_internal
+
+    if flashrwkv_amd._C is None:
+        raise SystemExit("flashrwkv_amd native library is not built")
+    dev = torch.device("cuda:0")
+    batch, t_len, heads, d = 8, 4096, 64, 64
+    n_tok = batch * t_len
+    tok = workloads.make_tokens(n_tok, heads, d, dtype=torch.bfloat16, seed=20260808,
+                                device=dev)
+    leaves = [tok[n].requires_grad_(True) for n in ("r", "w", "k", "v", "a", "b")]
+    gen = torch.Generator(device=dev).manual_seed(20260809)
+    s0 = (torch.randn((batch, heads, d, d), generator=gen, device=dev) * 0.1).requires_grad_(True)
+    dy = torch.randn((n_tok, heads, d), generator=gen, device=dev).to(torch.bfloat16)
+    ds = torch.randn((batch, heads, d, d), generator=gen, device=dev) * 0.01
+    offsets = torch.arange(0, batch + 1, device=dev, dtype=torch.int32) * (t_len // 64)
+    starts = torch.arange(0, n_tok, 64, device=dev, dtype=torch.int32)
+    ends = starts + 64
+
+    def step():
+        for t in (*leaves, s0):
+            t.grad = None  # fresh gradients each step, as after optimizer.zero_grad()
+        y, st, _, _ = statetune_recurrent_internal(s0, offsets, starts, ends, *leaves)
+        torch.autograd.backward([y, st], [dy, ds])
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.training_steps):
+        step()
+    end.record()
+    end.synchronize()
+    ms = start.elapsed_time(end) / args.training_steps
+    chunk_heads = batch * heads * (t_len // 64)
+    flops = 3 * chunk_heads * chunk_flops()
+    tok_bytes = n_tok * heads * d * 2
+    state_bytes = batch * heads * d * d * 4
+    boundary_bytes = chunk_heads * d * d * 4
+    # forward: 6 token reads, y write, boundary and state_dot_a writes, S0/S_T;
+    # backward: 6 token reads + dY, boundary read, 6 gradient writes, dS_T/dS0.
+    nbytes = (6 + 1) * tok_bytes + 2 * boundary_bytes + 2 * state_bytes \
+        + 7 * tok_bytes + boundary_bytes + 6 * tok_bytes + 2 * state_bytes
+    tflops = flops / (ms * 1e-3) / 1e12
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    out = {
+        "workload": "wkv7_training_cfg4: chunked forward + backward (StateTune), B=8, T=4096, "
+                    "H=64, D=64, chunk 64, bf16 io, raw retention, fp32 state and boundaries",
+        "ms_per_step": round(ms, 4),
+        "train_tokens_per_s": round(n_tok / (ms * 1e-3), 1),
+        "steps": args.training_steps,
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                     "algorithmic_flops_per_step": flops,
+                     "traffic": pmc_traffic("chunk_fwd_kernel<Bf16,kRawW,float>/statetune")
+                     + pmc_traffic("chunk_bwd_kernel<Bf16,kRawW>"),
+                     "kernel": "chunk_fwd_kernel<Bf16,kRawW,float> + chunk_bwd_kernel<Bf16,kRawW>"},
+        "hbm": {"achieved_GBps": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                "frac": round(gbps / HBM_PEAK_GBPS, 4), "algorithmic_bytes_per_step": nbytes},
+    }
+    if args.cpu_seconds > 0:
+        out["cpu_baseline"] = cpu_baseline_training(t_len, heads, args.cpu_seconds)
+    return out
+
+
+def cpu_baseline_training(t_len, heads_total, seconds):
+    """fp64 C oracle forward + adjoint on a bounded sample of whole (sequence,
+    head) recurrences (heads are independent, so the rate scales exactly)."""
+    import numpy as np
+    import torch
+
+    from flashrwkv_amd import workloads
+    from oracle import oracle
+
+    cores = len(os.sched_getaffinity(0))
+    sample_heads = max(1, cores)
+    case = workloads.make_case(lengths=[t_len], heads=sample_heads, head_size=64,
+                               dtype=torch.bfloat16, seed=97, state_std=0.1)
+    args = [case[n].double().numpy() for n in ("r", "w", "k", "v", "a", "b")]
+    s0 = case["state_pool"].double().numpy()
+    so, ss, se = oracle.segments_from_cu_seqlens(case["cu_seqlens"].numpy())
+    slots = np.zeros(1, dtype=np.int32)
+    dy = np.random.default_rng(0).standard_normal(args[0].shape)
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        oracle.forward(*args, s0, seg_offsets=so, seg_starts=ss, seg_ends=se,
+                       state_slots=slots, num_threads=cores)
+        oracle.backward(*args, s0, seg_offsets=so, seg_starts=ss, seg_ends=se,
+                        state_slots=slots, dy=dy, num_threads=cores)
+        reps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            break
+    return {
+        "value": reps * t_len * sample_heads / elapsed / heads_total,
+        "unit": "train tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{reps} x (1 sequence x {sample_heads} heads x T={t_len}) forward + adjoint "
+                  f"through the fp64 C oracle, OpenMP over heads, {elapsed:.1f} s; "
+                  f"token-heads/s divided by H={heads_total}",
+    }
+
+
+def bench_copy(args):
+    """A plain device copy of known size: the calibration run for the
+    FETCH_SIZE / WRITE_SIZE counters (bytes per dispatch vs counter KiB)."""
+    import torch
+
+    n = 256 * 1024 * 1024 // 4  # 256 MiB of fp32
+    src = torch.rand(n, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"workload": "copy_calibration", "bytes_read": n * 4, "bytes_written": n * 4,
+            "dispatches": 5}
+
+
+def bench_recurrent_long(args):
+    """B=8, T=4096, H=32, D=64, bf16 io, fp32 state, S0 = 0,
+    through the per-token recurrent kernel and through the chunked kernel."""
+    import torch
+
+    import flashrwkv_amd
+    from flashrwkv_amd import workloads
+    from flashrwkv_amd.tmix.wkv7 import DECAY_RAW_W
+
+    if flashrwkv_amd._C is None:
+        raise SystemExit("flashrwkv_amd native library is not built")
+    ops = flashrwkv_amd._C.ops
+    dev = torch.device("cuda:0")
+    batch, t_len, heads, d = 8, 4096, 32, 64
+    n_tok = batch * t_len
+    tok = workloads.make_tokens(n_tok, heads, d, dtype=torch.bfloat16, seed=20260806,
+                                device=dev)
+    cu = torch.arange(0, n_tok + 1, t_len, device=dev, dtype=torch.int32)
+    slots = torch.arange(batch, device=dev, dtype=torch.int32)
+    pool = torch.zeros((batch, heads, d, d), device=dev)
+    out = torch.empty((n_tok, heads, d), device=dev, dtype=torch.bfloat16)
+    args_tok = (tok["r"], tok["w"], tok["k"], tok["v"], tok["a"], tok["b"])
+
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            fn()
+        end.record()
+        end.synchronize()
+        return start.elapsed_time(end) / reps
+
+    rec_ms = timed(lambda: ops.recurrent_fp32_forward_internal(
+        cu, slots, pool, *args_tok, out, 1.0, DECAY_RAW_W, None, None, t_len), 3)
+    chunk_ms = timed(lambda: ops.chunk_forward_internal(
+        *args_tok, pool, cu, slots, 1.0, DECAY_RAW_W, None), 10)
+    nbytes = n_tok * heads * 7 * d * 2 + 2 * batch * heads * d * d * 4
+    return {
+        "workload": "wkv7_recurrent_long_cfg2: B=8, T=4096, H=32, D=64, bf16 io, fp32 state",
+        "recurrent_kernel": {"ms": round(rec_ms, 4),
+                             "tokens_per_s": round(n_tok / (rec_ms * 1e-3), 1),
+                             "achieved_GBps": round(nbytes / (rec_ms * 1e-3) / 1e9, 1)},
+        "chunked_kernel": {"ms": round(chunk_ms, 4),
+                           "tokens_per_s": round(n_tok / (chunk_ms * 1e-3), 1),
+                           "achieved_GBps": round(nbytes / (chunk_ms * 1e-3) / 1e9, 1)},
+        "algorithmic_bytes": nbytes,
+    }
 
 
 def main():
@@ -352,10 +560,18 @@ def main():
         }
         if "cpu_baseline" in pre:
             line["cpu_baseline"] = pre["cpu_baseline"]
+    elif args.workload == "training":
+        line = {"metric": METRIC, "training": bench_training(args)}
+    elif args.workload == "copy":
+        line = {"metric": METRIC, "copy": bench_copy(args)}
+    elif args.workload == "recurrent_long":
+        line = {"metric": METRIC, "recurrent_long": bench_recurrent_long(args)}
     else:
         line = bench_decode(args)
         if args.workload == "all":
             line["chunked_prefill"] = bench_prefill(args)
+            line["training"] = bench_training(args)
+            line["recurrent_long"] = bench_recurrent_long(args)
     print(json.dumps(line), flush=True)
 
 

@@ -14,13 +14,17 @@ except ImportError:
     _C = None
 
 from .tmix.wkv7 import (
+    infer_chunk_bf16_forward_varlen,
     infer_recurrent_fp32io16_forward_varlen,
     prepare_recurrent_metadata,
 )
+from .tmix.wkv7.statetune import statetune_recurrent_fp32io16
 
 __all__ = [
+    "infer_chunk_bf16_forward_varlen",
     "infer_recurrent_fp32io16_forward_varlen",
     "prepare_recurrent_metadata",
+    "statetune_recurrent_fp32io16",
 ]
 
 __version__ = "0.1.0"

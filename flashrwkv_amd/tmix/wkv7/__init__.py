@@ -190,3 +190,8 @@ __all__ = [
     "infer_recurrent_fp32io16_forward_varlen",
     "prepare_recurrent_metadata",
 ]
+
+# Reference ``tmix/wkv7/__init__.py:350-354`` re-exports the chunk entry here.
+from .chunk import infer_chunk_bf16_forward_varlen  # noqa: E402
+
+__all__.append("infer_chunk_bf16_forward_varlen")

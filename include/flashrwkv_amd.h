@@ -94,8 +94,9 @@ int frwkv_metadata_validate(const int32_t* cu_seqlens,
  * [H*D] of io_dtype (logits mode only). metadata_status is the status word of
  * frwkv_metadata_validate: when it is non-zero at run time the kernels fill
  * output with NaN and leave the pool untouched. max_seqlen is the longest
- * sequence (<= 0: unknown); it selects between the per-token recurrent
- * kernel and the chunked kernel, never the result beyond rounding.
+ * sequence (<= 0: unknown); it selects the launch shape of the per-token
+ * kernel (one wave per state for decode, four for longer sequences), never
+ * the result. The arithmetic stays fp32 per token whatever the length.
  */
 int frwkv_recurrent_forward(int io_dtype, int decay_mode, int32_t num_sequences,
                             int32_t num_heads, int32_t head_size,
