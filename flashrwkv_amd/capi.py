@@ -1,0 +1,126 @@
+"""ctypes binding of the C ABI in ``include/flashrwkv_amd.h``.
+
+This is the binding a non-torch host (or a test of the boundary itself) uses:
+every call passes raw device pointers, sizes and the current HIP stream to
+``libflashrwkv_amd.so`` and turns a non-zero status into RuntimeError with
+``frwkv_last_error()``. Tensors are only a convenient way to own device
+memory here; the library never sees a torch type.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIBRARY = Path(__file__).resolve().parent / "libflashrwkv_amd.so"
+
+DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+DECAY_LOGITS, DECAY_RAW_W = 0, 1
+
+_INT, _I32, _F32, _VP = ctypes.c_int, ctypes.c_int32, ctypes.c_float, ctypes.c_void_p
+
+# name -> argtypes, in the header's parameter order.
+SIGNATURES = {
+    "frwkv_abi_version": [],
+    "frwkv_status_string": [_INT],
+    "frwkv_last_error": [],
+    "frwkv_metadata_validate": [_VP, _VP, _I32, _I32, _I32, _VP, _VP, _VP, _VP],
+    "frwkv_recurrent_forward": [_INT, _INT] + [_I32] * 6 + [_VP] * 12 + [_F32, _VP],
+    "frwkv_chunk_forward": [_INT] * 3 + [_I32] * 5 + [_VP] * 12 + [_F32, _VP],
+    "frwkv_statetune_forward": [_INT] * 2 + [_I32] * 5 + [_VP] * 14 + [_F32, _VP],
+    "frwkv_statetune_backward": [_INT] * 2 + [_I32] * 5 + [_VP] * 20 + [_F32, _VP],
+}
+
+_LIB = None
+
+
+def library() -> ctypes.CDLL:
+    """The loaded ``libflashrwkv_amd.so`` (ImportError if it is not built)."""
+    global _LIB
+    if _LIB is None:
+        if not LIBRARY.exists():
+            raise ImportError(f"{LIBRARY.name} is not built; run `python -m flashrwkv_amd._build`")
+        lib = ctypes.CDLL(str(LIBRARY))
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_int
+        lib.frwkv_status_string.restype = ctypes.c_char_p
+        lib.frwkv_last_error.restype = ctypes.c_char_p
+        _LIB = lib
+    return _LIB
+
+
+def _p(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        lib = library()
+        raise RuntimeError(f"{lib.frwkv_status_string(status).decode()}: "
+                           f"{lib.frwkv_last_error().decode()}")
+
+
+def metadata_validate(cu_seqlens, state_indices, total_tokens, state_pool_size):
+    """Device validation + snapshot; returns ``(status, cu_snapshot, slot_snapshot)``."""
+    status = torch.empty(1, dtype=torch.int32, device=cu_seqlens.device)
+    cu_snap = torch.empty_like(cu_seqlens)
+    slot_snap = torch.empty_like(state_indices)
+    _check(library().frwkv_metadata_validate(
+        _p(cu_seqlens), _p(state_indices), state_indices.numel(), int(total_tokens),
+        int(state_pool_size), _p(status), _p(cu_snap), _p(slot_snap), _stream()))
+    return status, cu_snap, slot_snap
+
+
+def recurrent_forward(r, decay, k, v, a, b, *, state_pool, cu_seqlens, state_indices,
+                      metadata_status, output, scale=1.0, decay_mode=DECAY_RAW_W,
+                      decay_bias=None, max_seqlen=-1):
+    n, h, d = r.shape
+    _check(library().frwkv_recurrent_forward(
+        DTYPE[r.dtype], decay_mode, state_indices.numel(), h, d, n, int(max_seqlen),
+        state_pool.shape[0], _p(cu_seqlens), _p(state_indices), _p(metadata_status),
+        _p(state_pool), _p(r), _p(decay), _p(decay_bias), _p(k), _p(v), _p(a), _p(b),
+        _p(output), float(scale), _stream()))
+
+
+def chunk_forward(r, decay, k, v, a, b, *, state_pool, cu_seqlens, state_indices,
+                  metadata_status, output, scale=1.0, decay_mode=DECAY_RAW_W,
+                  decay_bias=None):
+    n, h, d = r.shape
+    _check(library().frwkv_chunk_forward(
+        DTYPE[r.dtype], decay_mode, DTYPE[state_pool.dtype], state_indices.numel(), h, d,
+        n, state_pool.shape[0], _p(cu_seqlens), _p(state_indices), _p(metadata_status),
+        _p(state_pool), _p(r), _p(decay), _p(decay_bias), _p(k), _p(v), _p(a), _p(b),
+        _p(output), float(scale), _stream()))
+
+
+def statetune_forward(r, decay, k, v, a, b, *, sequence_chunk_offsets, chunk_token_starts,
+                      chunk_token_ends, state, output, boundary, state_dot_a, scale=1.0,
+                      decay_mode=DECAY_RAW_W, decay_bias=None):
+    n, h, d = r.shape
+    _check(library().frwkv_statetune_forward(
+        DTYPE[r.dtype], decay_mode, sequence_chunk_offsets.numel() - 1, h, d, n,
+        chunk_token_starts.numel(), _p(sequence_chunk_offsets), _p(chunk_token_starts),
+        _p(chunk_token_ends), _p(state), _p(r), _p(decay), _p(decay_bias), _p(k), _p(v),
+        _p(a), _p(b), _p(output), _p(boundary), _p(state_dot_a), float(scale), _stream()))
+
+
+def statetune_backward(r, decay, k, v, a, b, *, sequence_chunk_offsets, chunk_token_starts,
+                       chunk_token_ends, boundary, grad_output, grad_final_state, grads,
+                       grad_initial_state, scale=1.0, decay_mode=DECAY_RAW_W,
+                       decay_bias=None):
+    """``grads`` = (grad_r, grad_decay, grad_k, grad_v, grad_a, grad_b)."""
+    n, h, d = r.shape
+    _check(library().frwkv_statetune_backward(
+        DTYPE[r.dtype], decay_mode, sequence_chunk_offsets.numel() - 1, h, d, n,
+        chunk_token_starts.numel(), _p(sequence_chunk_offsets), _p(chunk_token_starts),
+        _p(chunk_token_ends), _p(boundary), _p(r), _p(decay), _p(decay_bias), _p(k), _p(v),
+        _p(a), _p(b), _p(grad_output), _p(grad_final_state), *(_p(g) for g in grads),
+        _p(grad_initial_state), float(scale), _stream()))

@@ -75,9 +75,11 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
   const int row0 = rg * kRpl;
   const int col = slab * CW + 4 * cg;
 
-  const int32_t t_begin = cu_seqlens[seq];
-  const int32_t t_end = cu_seqlens[seq + 1];
-  const int32_t slot = slots[seq];
+  // One wave handles one sequence, so its bounds and slot are wave-uniform;
+  // readfirstlane makes the token loop's branches scalar.
+  const int32_t t_begin = __builtin_amdgcn_readfirstlane(cu_seqlens[seq]);
+  const int32_t t_end = __builtin_amdgcn_readfirstlane(cu_seqlens[seq + 1]);
+  const int32_t slot = __builtin_amdgcn_readfirstlane(slots[seq]);
   // Validated metadata never fails these; they keep a bad direct launch from
   // touching memory outside the tensors.
   if (t_begin < 0 || t_end > total_tokens || t_begin >= t_end || slot < 0 ||
@@ -100,49 +102,90 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
     for (int j = 0; j < kRpl; ++j) bias[j] = 0.0f;
   }
 
-  for (int32_t t = t_begin; t < t_end; ++t) {
+  // Token rows are independent of the state, so their loads run ahead of the
+  // recurrence: a register ring holds the raw rows of the next kPrefetch
+  // tokens, and each step issues the loads of the token kPrefetch positions
+  // later before it computes. Long sequences are otherwise bound by one HBM
+  // round trip per token. Decode (one token, one wave per state) loads each
+  // token in place instead: it needs many waves per SIMD to cover HBM latency,
+  // so its register count must stay low.
+  struct TokenRows {
+    RawRow<T, kRpl> a, w, b, k, r;
+    RawRow<T, 4> v;
+  };
+  auto load_token = [&](TokenRows& dst, int32_t t) {
     const int64_t base = (static_cast<int64_t>(t) * num_heads + head) * D;
-    float rr[kRpl], ww[kRpl], kk[kRpl], aa[kRpl], bb[kRpl], vv[4];
-    load_vec<T, kRpl>(a_ptr + base + row0, aa);
-    load_vec<T, kRpl>(decay_ptr + base + row0, ww);
-    load_vec<T, kRpl>(b_ptr + base + row0, bb);
-    load_vec<T, kRpl>(k_ptr + base + row0, kk);
-    load_vec<T, kRpl>(r_ptr + base + row0, rr);
-    load_vec<T, 4>(v_ptr + base + col, vv);
-
-    float4 sa = make_float4(0.f, 0.f, 0.f, 0.f);
+    load_raw<T, kRpl>(a_ptr + base + row0, dst.a);
+    load_raw<T, kRpl>(decay_ptr + base + row0, dst.w);
+    load_raw<T, kRpl>(b_ptr + base + row0, dst.b);
+    load_raw<T, kRpl>(k_ptr + base + row0, dst.k);
+    load_raw<T, kRpl>(r_ptr + base + row0, dst.r);
+    load_raw<T, 4>(v_ptr + base + col, dst.v);
+  };
+  // About 96 registers of ring; the one-wave decode shape loads in place.
+  constexpr int kTokenWords = 5 * RawRow<T, kRpl>::kWords + RawRow<T, 4>::kWords;
+  constexpr int kRing = 96 / kTokenWords < 1 ? 1 : (96 / kTokenWords > 8 ? 8 : 96 / kTokenWords);
+  constexpr int kPrefetch = (CW == 64) ? 1 : kRing;
+  TokenRows ring[kPrefetch];
+  if constexpr (kPrefetch > 1) {
 #pragma unroll
-    for (int j = 0; j < kRpl; ++j) {
-      sa.x = fmaf(aa[j], s[j].x, sa.x);
-      sa.y = fmaf(aa[j], s[j].y, sa.y);
-      sa.z = fmaf(aa[j], s[j].z, sa.z);
-      sa.w = fmaf(aa[j], s[j].w, sa.w);
+    for (int j = 0; j < kPrefetch; ++j) {
+      if (t_begin + j < t_end) load_token(ring[j], t_begin + j);
     }
-    sa.x = reduce_row_groups<kNg>(sa.x);
-    sa.y = reduce_row_groups<kNg>(sa.y);
-    sa.z = reduce_row_groups<kNg>(sa.z);
-    sa.w = reduce_row_groups<kNg>(sa.w);
+  }
 
-    float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int32_t t0 = t_begin; t0 < t_end; t0 += kPrefetch) {
 #pragma unroll
-    for (int j = 0; j < kRpl; ++j) {
-      const float w = decay_retention<M>(ww[j] + bias[j]);
-      s[j].x = fmaf(w, s[j].x, fmaf(bb[j], sa.x, kk[j] * vv[0]));
-      s[j].y = fmaf(w, s[j].y, fmaf(bb[j], sa.y, kk[j] * vv[1]));
-      s[j].z = fmaf(w, s[j].z, fmaf(bb[j], sa.z, kk[j] * vv[2]));
-      s[j].w = fmaf(w, s[j].w, fmaf(bb[j], sa.w, kk[j] * vv[3]));
-      y.x = fmaf(rr[j], s[j].x, y.x);
-      y.y = fmaf(rr[j], s[j].y, y.y);
-      y.z = fmaf(rr[j], s[j].z, y.z);
-      y.w = fmaf(rr[j], s[j].w, y.w);
-    }
-    y.x = reduce_row_groups<kNg>(y.x);
-    y.y = reduce_row_groups<kNg>(y.y);
-    y.z = reduce_row_groups<kNg>(y.z);
-    y.w = reduce_row_groups<kNg>(y.w);
-    if (rg == 0) {
-      store4<T>(out_ptr + base + col, scale * y.x, scale * y.y, scale * y.z,
-                scale * y.w);
+    for (int jp = 0; jp < kPrefetch; ++jp) {
+      const int32_t t = t0 + jp;
+      if (t >= t_end) break;
+      if constexpr (kPrefetch == 1) load_token(ring[0], t);
+      float rr[kRpl], ww[kRpl], kk[kRpl], aa[kRpl], bb[kRpl], vv[4];
+      decode_raw<T, kRpl>(ring[jp].a, aa);
+      decode_raw<T, kRpl>(ring[jp].w, ww);
+      decode_raw<T, kRpl>(ring[jp].b, bb);
+      decode_raw<T, kRpl>(ring[jp].k, kk);
+      decode_raw<T, kRpl>(ring[jp].r, rr);
+      decode_raw<T, 4>(ring[jp].v, vv);
+      if constexpr (kPrefetch > 1) {
+        if (t + kPrefetch < t_end) load_token(ring[jp], t + kPrefetch);
+      }
+
+      float4 sa = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int j = 0; j < kRpl; ++j) {
+        sa.x = fmaf(aa[j], s[j].x, sa.x);
+        sa.y = fmaf(aa[j], s[j].y, sa.y);
+        sa.z = fmaf(aa[j], s[j].z, sa.z);
+        sa.w = fmaf(aa[j], s[j].w, sa.w);
+      }
+      sa.x = reduce_row_groups<kNg>(sa.x);
+      sa.y = reduce_row_groups<kNg>(sa.y);
+      sa.z = reduce_row_groups<kNg>(sa.z);
+      sa.w = reduce_row_groups<kNg>(sa.w);
+
+      float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int j = 0; j < kRpl; ++j) {
+        const float w = decay_retention<M>(ww[j] + bias[j]);
+        s[j].x = fmaf(w, s[j].x, fmaf(bb[j], sa.x, kk[j] * vv[0]));
+        s[j].y = fmaf(w, s[j].y, fmaf(bb[j], sa.y, kk[j] * vv[1]));
+        s[j].z = fmaf(w, s[j].z, fmaf(bb[j], sa.z, kk[j] * vv[2]));
+        s[j].w = fmaf(w, s[j].w, fmaf(bb[j], sa.w, kk[j] * vv[3]));
+        y.x = fmaf(rr[j], s[j].x, y.x);
+        y.y = fmaf(rr[j], s[j].y, y.y);
+        y.z = fmaf(rr[j], s[j].z, y.z);
+        y.w = fmaf(rr[j], s[j].w, y.w);
+      }
+      y.x = reduce_row_groups<kNg>(y.x);
+      y.y = reduce_row_groups<kNg>(y.y);
+      y.z = reduce_row_groups<kNg>(y.z);
+      y.w = reduce_row_groups<kNg>(y.w);
+      if (rg == 0) {
+        const int64_t base = (static_cast<int64_t>(t) * num_heads + head) * D;
+        store4<T>(out_ptr + base + col, scale * y.x, scale * y.y, scale * y.z,
+                  scale * y.w);
+      }
     }
   }
 

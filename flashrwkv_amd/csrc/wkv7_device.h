@@ -139,6 +139,53 @@ __device__ __forceinline__ void load_vec(const typename IoTraits<T>::storage* p,
   }
 }
 
+// Raw (undecoded) storage of N contiguous elements, loaded with 8- or
+// 16-byte vector loads. Decoding is split from loading so that a kernel can
+// issue the loads of later tokens long before it decodes them.
+template <typename T, int N>
+struct RawRow {
+  static constexpr int kWords = N * IoTraits<T>::kBytes / 4;
+  static_assert(kWords % 2 == 0, "rows load in 8-byte pieces");
+  uint32_t w[kWords];
+};
+
+template <typename T, int N>
+__device__ __forceinline__ void load_raw(const typename IoTraits<T>::storage* p,
+                                         RawRow<T, N>& out) {
+  constexpr int kWords = RawRow<T, N>::kWords;
+  if constexpr (kWords % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < kWords / 4; ++i) {
+      const uint4 q = reinterpret_cast<const uint4*>(p)[i];
+      out.w[4 * i + 0] = q.x;
+      out.w[4 * i + 1] = q.y;
+      out.w[4 * i + 2] = q.z;
+      out.w[4 * i + 3] = q.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kWords / 2; ++i) {
+      const uint2 q = reinterpret_cast<const uint2*>(p)[i];
+      out.w[2 * i + 0] = q.x;
+      out.w[2 * i + 1] = q.y;
+    }
+  }
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void decode_raw(const RawRow<T, N>& in, float (&out)[N]) {
+  if constexpr (__is_same(T, float)) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = __uint_as_float(in.w[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      out[2 * i + 0] = to_f32<T>(static_cast<uint16_t>(in.w[i] & 0xffffu));
+      out[2 * i + 1] = to_f32<T>(static_cast<uint16_t>(in.w[i] >> 16));
+    }
+  }
+}
+
 // Stores 4 contiguous values.
 template <typename T>
 __device__ __forceinline__ void store4(typename IoTraits<T>::storage* p, float x0,

@@ -62,7 +62,39 @@ def test_null_pointers_are_rejected_before_any_launch(lib):
     rc = lib.frwkv_metadata_validate(null, null, 1, 1, 1, null, null, null, null)
     assert rc == 1
     assert b"null pointer" in lib.frwkv_last_error()
-    args = [ctypes.c_int(2), ctypes.c_int(0)] + [ctypes.c_int32(1)] * 6 + [null] * 13 \
+    args = [ctypes.c_int(2), ctypes.c_int(0)] + [ctypes.c_int32(1)] * 6 + [null] * 12 \
         + [ctypes.c_float(1.0), null]
     assert lib.frwkv_recurrent_forward(*args) == 1
     assert b"null pointer" in lib.frwkv_last_error()
+
+
+def _header_parameter_counts() -> dict[str, int]:
+    text = (ROOT / "include" / "flashrwkv_amd.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.DOTALL)
+    counts = {}
+    for match in re.finditer(r"\b(frwkv_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = match.group(2).strip()
+        counts[match.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return counts
+
+
+def test_ctypes_binding_matches_header_signatures():
+    """flashrwkv_amd.capi (the binding the GPU boundary tests use) declares
+    every entry point with the header's parameter count."""
+    from flashrwkv_amd import capi
+
+    counts = _header_parameter_counts()
+    assert set(counts) == set(capi.SIGNATURES)
+    for name, argtypes in capi.SIGNATURES.items():
+        assert len(argtypes) == counts[name], name
+
+
+def test_ctypes_binding_reports_errors_without_a_gpu():
+    from flashrwkv_amd import capi
+
+    lib = capi.library()
+    null = ctypes.c_void_p()
+    rc = lib.frwkv_chunk_forward(2, 1, 0, 1, 1, 64, 1, 1, *([null] * 12), 1.0, null)
+    assert rc == 1 and b"null pointer" in lib.frwkv_last_error()
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        capi._check(rc)
