@@ -39,9 +39,12 @@
 //               substitution), dSA, dZ (backward substitution), dV, dS0 and
 //               the partial dg, all chained through registers;
 //   matrices    the four C x C gradient matrices in both layouts, spread over
-//               the waves, from LDS (SA, dZ) and HBM (dY, V) operands;
+//               the waves, from LDS operand tiles (SA, dZ, dY, V);
 //   tokens      wave p owns tokens 16p..16p+15: the [token][feature]
 //               gradients, the decay scan, and the stores.
+// Every HBM input of a chunk (token rows, dY and V tiles, the checkpoint
+// slice) is loaded while the chunk after it computes, so no phase waits on
+// HBM; the tokens phase loads its raw inputs one feature block ahead.
 // Chunks must be at most 64 tokens (segments); the training wrapper splits
 // longer caller chunks. A chunk whose decay span exceeds the forward's
 // single-reference limit is not supported here: its sequence's gradients are
@@ -62,9 +65,10 @@ struct BwdSmem {
   uint16_t ktT[kOpTile];  // [k][t]
   uint16_t atT[kOpTile];  // [k][t]
   uint16_t rtT[kOpTile];  // [k][t]
-  float gt[kChunk][kHead + 1];  // G_t[k]
+  uint16_t dy_x[kOpTile];       // dY [t][v] (unscaled)
+  uint16_t v_x[kOpTile];        // V  [t][v]
   float gc[kHead];              // 2^GC
-  float wave_tot[4][kHead];     // decay scan carry (prepare)
+  float wave_tot[4][kHead];     // per-block sums of log2 w (prepare; read by tokens)
   float carry[4][kHead];        // token scan carries
   float carry3[4][kHead];
   float dgamma[4][kHead];       // per-wave partial of rowsum(S0 o dS)
@@ -128,6 +132,22 @@ __device__ __forceinline__ float suffix16_step(float x) {
   return x + y;
 }
 
+// Prefix-scan step over the 16 lanes of a row: lane n adds lane n - N (zero
+// for n < N).
+template <int N>
+__device__ __forceinline__ float prefix16_step(float x) {
+  const float y = __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x110 + N, 0xf, 0xf, true));
+  return x + y;
+}
+
+__device__ __forceinline__ float prefix16(float x) {
+  x = prefix16_step<1>(x);
+  x = prefix16_step<2>(x);
+  x = prefix16_step<4>(x);
+  return prefix16_step<8>(x);
+}
+
 __device__ __forceinline__ float suffix16(float x) {
   x = suffix16_step<1>(x);
   x = suffix16_step<2>(x);
@@ -135,17 +155,34 @@ __device__ __forceinline__ float suffix16(float x) {
   return suffix16_step<8>(x);
 }
 
-// Token rows of one chunk: r, w, k, a, b in the prepare layout, V and dY in
-// operand layout (lane (g, n): X[16q + 4g + e][16w + n]).
+// HBM inputs of one chunk, loaded one chunk ahead of use: r, w, k, a, b in
+// the prepare layout (thread: tokens 16w + 2tp, +1, features 8kg .. +7), dY
+// and V as 16-byte pieces of [t][v] tiles (piece tid + 256 s: row
+// (tid + 256 s) / 8, columns 8 ((tid + 256 s) % 8) .. +7), and this lane's
+// slice of the chunk-start state.
 struct BwdRows {
   uint4 r[2], w[2], k[2], a[2], b[2];
-  i16x4 vs[4];
-  i16x4 dys[4];  // scale * dY, bf16
+  uint4 dy[2], v[2];
+  f32x4 s0[4];
 };
 
+// 8 io-dtype values -> 8 bf16 at an 8-byte aligned LDS address.
+template <typename T>
+__device__ __forceinline__ void store_piece_bf16(uint16_t* dst, uint4 q) {
+  if constexpr (__is_same(T, Bf16)) {
+    reinterpret_cast<uint2*>(dst)[0] = make_uint2(q.x, q.y);
+    reinterpret_cast<uint2*>(dst)[1] = make_uint2(q.z, q.w);
+  } else {
+    float x[8];
+    unpack8<T>(q, x);
+    store8_bf16(dst, x);
+  }
+}
+
 // Prepare: the forward's operand tiles restricted to the chunk, plus At^T,
-// Rt^T (token-contiguous) and G. Returns whether the decay span is within
-// the single-reference limit. Ends with a barrier.
+// Rt^T (token-contiguous), the per-block decay sums and the dY / V tiles.
+// Returns whether the decay span is within the single-reference limit. Ends
+// with a barrier.
 template <typename T, DecayMode M>
 __device__ bool prepare_bwd(BwdSmem& sm, const BwdRows& rows, const float (&bias)[8],
                             int ntok) {
@@ -205,9 +242,11 @@ __device__ bool prepare_bwd(BwdSmem& sm, const BwdRows& rows, const float (&bias
   const bool whole = __builtin_amdgcn_ballot_w64(over) == 0;
 
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    sm.gt[t0][8 * kg + e] = g0[e];
-    sm.gt[t0 + 1][8 * kg + e] = g1[e];
+  for (int s = 0; s < 2; ++s) {
+    const int piece = tid + 256 * s;
+    const int off = (piece >> 3) * kOpStride + 8 * (piece & 7);
+    store_piece_bf16<T>(sm.dy_x + off, rows.dy[s]);
+    store_piece_bf16<T>(sm.v_x + off, rows.v[s]);
   }
   float up0[8], up1[8], dn0[8], dn1[8], gcv[8], upp[8];
 #pragma unroll
@@ -366,28 +405,6 @@ __device__ void intra_bwd(BwdSmem& sm) {
   __syncthreads();
 }
 
-template <typename T>
-__device__ __forceinline__ i16x4 load_operand_bf16(__amdgpu_buffer_rsrc_t rs, uint32_t off,
-                                                   int so) {
-  // 4 consecutive io-dtype values as a bf16 operand.
-  const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rs, off, so, 0);
-  if constexpr (__is_same(T, Bf16)) {
-    i16x4 r;
-    r[0] = static_cast<short>(x.x & 0xffffu);
-    r[1] = static_cast<short>(x.x >> 16);
-    r[2] = static_cast<short>(x.y & 0xffffu);
-    r[3] = static_cast<short>(x.y >> 16);
-    return r;
-  } else {
-    f32x4 f;
-    f[0] = to_f32<T>(static_cast<uint16_t>(x.x & 0xffffu));
-    f[1] = to_f32<T>(static_cast<uint16_t>(x.x >> 16));
-    f[2] = to_f32<T>(static_cast<uint16_t>(x.y & 0xffffu));
-    f[3] = to_f32<T>(static_cast<uint16_t>(x.y >> 16));
-    return to_operand(f);
-  }
-}
-
 template <typename T, DecayMode M>
 __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdParams p) {
   __shared__ BwdSmem sm;
@@ -439,9 +456,82 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
   bool failed = false;
   const float kNaN = __int_as_float(0x7fc00000);
 
+  // Segment bounds, 64 segments at a time in VGPR lanes (lane i: segment
+  // cache_base + i), read back with readlane. A per-segment memory read would
+  // need a vmcnt wait, which on gfx9's in-order counter also waits for every
+  // gradient store still in flight.
+  int cache_base = seg_hi;
+  int starts_v = 0, ends_v = 0;
+  auto seg_bounds = [&](int seg, int& tb, int& te) {
+    if (seg < cache_base) {
+      cache_base = uniform(max(seg - 63, seg_lo));
+      const int idx = cache_base + lane;
+      starts_v = idx <= seg ? p.seg_starts[idx] : 0;
+      ends_v = idx <= seg ? p.seg_ends[idx] : 0;
+      __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): nothing pending at the join
+    }
+    tb = uniform(max(__builtin_amdgcn_readlane(starts_v, seg - cache_base), 0));
+    te = uniform(min(__builtin_amdgcn_readlane(ends_v, seg - cache_base), p.total_tokens));
+  };
+
+  // Inputs of a chunk (see BwdRows). Rows past the chunk's tokens read as
+  // zero through the buffer bounds.
+  auto load_chunk = [&](int seg, BwdRows& rows) {
+    int tb, te;
+    seg_bounds(seg, tb, te);
+    const int nt = uniform(max(min(te - tb, kChunk), 0));
+    const int64_t b0 = (static_cast<int64_t>(tb) * heads + head) * kHead;
+    const uint32_t nbytes = static_cast<uint32_t>(nt) * row_bytes;
+    auto brs = [&](const void* x) {
+      return buffer_rsrc(x != nullptr ? static_cast<const S16*>(x) + b0 : nullptr,
+                         x != nullptr ? nbytes : 0u);
+    };
+    auto ld = [&](__amdgpu_buffer_rsrc_t r, uint32_t off, int so) {
+      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, off, so, 0);
+      return make_uint4(x.x, x.y, x.z, x.w);
+    };
+    const auto r_rs = brs(p.r), w_rs = brs(p.decay), k_rs = brs(p.k), a_rs = brs(p.a),
+               b_rs = brs(p.b), v_rs = brs(p.v), dy_rs = brs(p.dy);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int so = s * static_cast<int>(row_bytes);
+      rows.r[s] = ld(r_rs, prep_off, so);
+      rows.w[s] = ld(w_rs, prep_off, so);
+      rows.k[s] = ld(k_rs, prep_off, so);
+      rows.a[s] = ld(a_rs, prep_off, so);
+      rows.b[s] = ld(b_rs, prep_off, so);
+      const int piece = tid + 256 * s;
+      const uint32_t tile_off = static_cast<uint32_t>(piece >> 3) * row_bytes + 16 * (piece & 7);
+      rows.dy[s] = ld(dy_rs, tile_off, 0);
+      rows.v[s] = ld(v_rs, tile_off, 0);
+    }
+    const auto ck = buffer_rsrc(
+        p.checkpoint + (static_cast<int64_t>(seg) * heads + head) * kHead * kHead,
+        kHead * kHead * 4);
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        rows.s0[kb][j] = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(ck, s_off, (16 * kb + j) * kHead * 4, 0));
+      }
+    }
+  };
+
+  BwdRows rows;
+  int loaded = seg_hi;
+
   for (int seg = seg_hi - 1; seg >= seg_lo; --seg) {
-    const int t_begin = uniform(max(p.seg_starts[seg], 0));
-    const int t_end = uniform(min(p.seg_ends[seg], p.total_tokens));
+    if (loaded != seg) {
+      // First chunk, or the one after an empty segment: load in place and
+      // drain (vmcnt(0)), so that only the prefetched rows are pending where
+      // the paths join.
+      load_chunk(seg, rows);
+      loaded = seg;
+      __builtin_amdgcn_s_waitcnt(0xF70);
+    }
+    int t_begin, t_end;
+    seg_bounds(seg, t_begin, t_end);
     const int ntok = uniform(min(t_end - t_begin, kChunk));
     if (ntok <= 0) continue;
     // Chunks longer than 64 tokens have no checkpoint inside: fail closed.
@@ -452,76 +542,52 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
       return buffer_rsrc(x != nullptr ? static_cast<const S16*>(x) + base : nullptr,
                          x != nullptr ? bytes : 0u);
     };
-    const auto r_rs = rs(p.r), w_rs = rs(p.decay), k_rs = rs(p.k), v_rs = rs(p.v),
-               a_rs = rs(p.a), b_rs = rs(p.b), dy_rs = rs(p.dy);
-
-    BwdRows rows;
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int so = s * static_cast<int>(row_bytes);
-      auto ld = [&](__amdgpu_buffer_rsrc_t r) {
-        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, prep_off, so, 0);
-        return make_uint4(x.x, x.y, x.z, x.w);
-      };
-      rows.r[s] = ld(r_rs);
-      rows.w[s] = ld(w_rs);
-      rows.k[s] = ld(k_rs);
-      rows.a[s] = ld(a_rs);
-      rows.b[s] = ld(b_rs);
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      f32x4 dyf;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int so = static_cast<int>((16 * q + e) * row_bytes);
-        const uint16_t xv = __builtin_amdgcn_raw_buffer_load_b16(v_rs, v_off, so, 0);
-        rows.vs[q][e] = __is_same(T, Bf16) ? static_cast<short>(xv)
-                                           : static_cast<short>(to_bf16_bits(to_f32<T>(xv)));
-        dyf[e] = p.scale * to_f32<T>(__builtin_amdgcn_raw_buffer_load_b16(dy_rs, v_off, so, 0));
-      }
-      rows.dys[q] = to_operand(dyf);
-    }
+    const auto r_rs = rs(p.r), w_rs = rs(p.decay), k_rs = rs(p.k), a_rs = rs(p.a),
+               b_rs = rs(p.b);
 
     const bool whole = prepare_bwd<T, M>(sm, rows, bias, ntok);
     failed = failed || !whole;
+    f32x4 S0[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) S0[kb] = rows.s0[kb];
+    // The rows are in LDS now: start loading the chunk before this one.
+    if (seg - 1 >= seg_lo) {
+      load_chunk(seg - 1, rows);
+      loaded = seg - 1;
+    }
     if (failed) {
       // Fail closed: NaN gradients for this chunk, and for every earlier one
       // (the adjoint would be wrong from here on).
+      // Rows past the chunk's tokens fall outside the buffer range and are
+      // dropped (as for every gradient store below).
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const int t = 16 * wave + 2 * tp + s;
-        if (t < ntok) {
-          const u32x4 nan4 = {0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
-          const int so = s * static_cast<int>(row_bytes);
-          const uint32_t off = prep_off;
-          (void)t;
-          __builtin_amdgcn_raw_buffer_store_b128(nan4, rs(p.dr), off, so, 0);
-          __builtin_amdgcn_raw_buffer_store_b128(nan4, rs(p.ddecay), off, so, 0);
-          __builtin_amdgcn_raw_buffer_store_b128(nan4, rs(p.dk), off, so, 0);
-          __builtin_amdgcn_raw_buffer_store_b128(nan4, rs(p.dv), off, so, 0);
-          __builtin_amdgcn_raw_buffer_store_b128(nan4, rs(p.da), off, so, 0);
-          __builtin_amdgcn_raw_buffer_store_b128(nan4, rs(p.db), off, so, 0);
-        }
+        const u32x4 nan4 = {0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
+        const int so = s * static_cast<int>(row_bytes);
+        __builtin_amdgcn_raw_buffer_store_b128(nan4, rs(p.dr), prep_off, so, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(nan4, rs(p.ddecay), prep_off, so, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(nan4, rs(p.dk), prep_off, so, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(nan4, rs(p.dv), prep_off, so, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(nan4, rs(p.da), prep_off, so, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(nan4, rs(p.db), prep_off, so, 0);
       }
       continue;
     }
     intra_bwd(sm);
 
     // ---------------------------------------------------------- columns --
-    f32x4 S0[4];
-    {
-      const auto ck = buffer_rsrc(
-          p.checkpoint + (static_cast<int64_t>(seg) * heads + head) * kHead * kHead,
-          kHead * kHead * 4);
+    // V and scale * dY in operand layout: lane (g, n) holds X[16q + 4g + e][16w + n].
+    i16x4 vs[4], dys[4];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
+    for (int q = 0; q < 4; ++q) {
+      f32x4 dyf;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          S0[kb][j] = __uint_as_float(
-              __builtin_amdgcn_raw_buffer_load_b32(ck, s_off, (16 * kb + j) * kHead * 4, 0));
-        }
+      for (int e = 0; e < 4; ++e) {
+        const int idx = (16 * q + 4 * g + e) * kOpStride + 16 * wave + n;
+        vs[q][e] = static_cast<short>(sm.v_x[idx]);
+        dyf[e] = p.scale * bf16_float(sm.dy_x[idx]);
       }
+      dys[q] = to_operand(dyf);
     }
     const i16x4 z4 = {0, 0, 0, 0};
     auto lo32 = [&](i16x4 x) { return cat(x, z4); };
@@ -530,8 +596,6 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
     };
     const i16x8 s01 = cat(to_operand(S0[0]), to_operand(S0[1]));
     const i16x8 s23 = cat(to_operand(S0[2]), to_operand(S0[3]));
-    const i16x4* vs = rows.vs;
-    const i16x4* dys = rows.dys;
     const i16x8 v01 = cat(vs[0], vs[1]), v23 = cat(vs[2], vs[3]);
 
     // SA = T (At S0 + Lak V), as in the forward.
@@ -644,16 +708,15 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
       dvv[2] = mfma32(cat(ft16(kBLakT, 2, 2), ft16(kBLakT, 3, 2)), dz23, dvv[2]);
       dvv[3] = mfma32(lo32(ft16(kBArkT, 3, 3)), lo32(dys[3]), dvv[3]);
       dvv[3] = mfma32(lo32(ft16(kBLakT, 3, 3)), lo32(dzb[3]), dvv[3]);
-      S16* dvp = static_cast<S16*>(p.dv);
+      const auto dv_rs = rs(p.dv);
 #pragma unroll
       for (int pb = 0; pb < 4; ++pb) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int t = 16 * pb + 4 * g + j;
-          if (t < ntok) {
-            dvp[base + static_cast<int64_t>(t) * heads * kHead + 16 * wave + n] =
-                from_f32<T>(dvv[pb][j]);
-          }
+          __builtin_amdgcn_raw_buffer_store_b16(
+              from_f32<T>(dvv[pb][j]), dv_rs,
+              static_cast<uint32_t>(t) * row_bytes + 2 * (16 * wave + n), 0, 0);
         }
       }
     }
@@ -696,14 +759,20 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
         sm.u.g.ds_x[kf * kOpStride + 16 * wave + n] = to_bf16_bits(dS_end[kb][j]);
       }
     }
-    // Operand rows over the value dimension: from HBM (dY, V) or LDS (SA, dZ).
-    const uint32_t hrow_off = static_cast<uint32_t>(n) * row_bytes + 8 * g;
-    auto hbm_row32 = [&](__amdgpu_buffer_rsrc_t r, int row0, int c) {
-      // Row row0 + n, columns c + 4g .. +3 and c + 16 + 4g .. +3.
-      const int so = static_cast<int>(row0 * row_bytes + 2 * c);
-      return cat(load_operand_bf16<T>(r, hrow_off, so),
-                 load_operand_bf16<T>(r, hrow_off, so + 32));
+    // The tokens phase's raw inputs: (token 16w + n, features 16kb + 4g .. +3).
+    const uint32_t tok_off = static_cast<uint32_t>(16 * wave + n) * row_bytes + 8 * g;
+    // Loaded one feature block ahead of use (block 0 here, block kb + 1
+    // while block kb computes).
+    u32x2 raw_next[5];
+    auto load_raw = [&](int kb) {
+      const int so = 2 * 16 * kb;
+      raw_next[0] = __builtin_amdgcn_raw_buffer_load_b64(a_rs, tok_off, so, 0);
+      raw_next[1] = __builtin_amdgcn_raw_buffer_load_b64(r_rs, tok_off, so, 0);
+      raw_next[2] = __builtin_amdgcn_raw_buffer_load_b64(b_rs, tok_off, so, 0);
+      raw_next[3] = __builtin_amdgcn_raw_buffer_load_b64(k_rs, tok_off, so, 0);
+      raw_next[4] = __builtin_amdgcn_raw_buffer_load_b64(w_rs, tok_off, so, 0);
     };
+    load_raw(0);
     // 40 (matrix, block pair) items, 10 per wave; both layouts each.
 #pragma unroll 1
     for (int item = wave; item < 40; item += 4) {
@@ -715,10 +784,8 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
       f32x4 mt = zero4(), mc = zero4();  // M^T in C layout (stores [t][i]), M (stores [i][t])
 #pragma unroll
       for (int c = 0; c < 64; c += 32) {
-        const i16x8 x = m < 2 ? hbm_row32(dy_rs, 16 * pb, c)
-                              : lds_operand32<kOpStride>(sm.dz_x, 16 * pb + n, c, g);
-        const i16x8 y = (m & 1) ? hbm_row32(v_rs, 16 * q, c)
-                                : lds_operand32<kOpStride>(sm.sa_x, 16 * q + n, c, g);
+        const i16x8 x = lds_operand32<kOpStride>(m < 2 ? sm.dy_x : sm.dz_x, 16 * pb + n, c, g);
+        const i16x8 y = lds_operand32<kOpStride>((m & 1) ? sm.v_x : sm.sa_x, 16 * q + n, c, g);
         mt = mfma32(y, x, mt);
         mc = mfma32(x, y, mc);
       }
@@ -749,20 +816,24 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
     auto gt16 = [&](int mm, int pp, int q) {
       return lds_operand<kTriStride>(gtri(sm, mm, pp, q), n, 4 * g);
     };
-    float e12[4][4], e2v[4][4], e3v[4][4], dec_in[4][4];
-    float grad_r[4][4], grad_a[4][4], grad_b[4][4], grad_k[4][4];
-    // Raw inputs and G for (token 16p + n, features 16kb + 4g .. +3).
-    const uint32_t tok_off = static_cast<uint32_t>(16 * pb + n) * row_bytes + 8 * g;
+    // Kept for the decay gradient after the barrier: the in-block suffix sums
+    // of e1 + e2, e2 itself and the decay input.
+    float suf[4][4], e2v[4][4], dec_in[4][4];
+#pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
+      u32x2 raw_cur[5];
+#pragma unroll
+      for (int i = 0; i < 5; ++i) raw_cur[i] = raw_next[i];
+      if (kb < 3) load_raw(kb + 1);
       f32x4 acc_s = zero4(), acc_z = zero4(), acc_bt = zero4(), acc_kt = zero4();
 #pragma unroll
       for (int c = 0; c < 64; c += 32) {
         const i16x8 s0r = lds_operand32<kOpStride>(sm.u.g.s0_x, 16 * kb + n, c, g);
         const i16x8 dsr = lds_operand32<kOpStride>(sm.u.g.ds_x, 16 * kb + n, c, g);
-        acc_s = mfma32(s0r, hbm_row32(dy_rs, 16 * pb, c), acc_s);                      // S0 dY^T
+        acc_s = mfma32(s0r, lds_operand32<kOpStride>(sm.dy_x, 16 * pb + n, c, g), acc_s);  // S0 dY^T
         acc_z = mfma32(s0r, lds_operand32<kOpStride>(sm.dz_x, 16 * pb + n, c, g), acc_z);  // S0 dZ^T
         acc_bt = mfma32(dsr, lds_operand32<kOpStride>(sm.sa_x, 16 * pb + n, c, g), acc_bt);  // dS SA^T
-        acc_kt = mfma32(dsr, hbm_row32(v_rs, 16 * pb, c), acc_kt);                      // dS V^T
+        acc_kt = mfma32(dsr, lds_operand32<kOpStride>(sm.v_x, 16 * pb + n, c, g), acc_kt);  // dS V^T
       }
       // Bt^T dArb^T + Kt^T dArk^T and Bt^T dLab^T + Kt^T dLak^T over source
       // blocks q <= p (K = tokens i).
@@ -832,19 +903,19 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
 
       // Elementwise chain rule for (token t = 16p + n, feature 16kb + 4g + j).
       const int so = static_cast<int>(2 * 16 * kb);
-      auto raw4 = [&](__amdgpu_buffer_rsrc_t r, float (&out)[4]) {
-        const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(r, tok_off, so, 0);
+      auto raw4 = [&](const u32x2 x, float (&out)[4]) {
         out[0] = to_f32<T>(static_cast<uint16_t>(x.x & 0xffffu));
         out[1] = to_f32<T>(static_cast<uint16_t>(x.x >> 16));
         out[2] = to_f32<T>(static_cast<uint16_t>(x.y & 0xffffu));
         out[3] = to_f32<T>(static_cast<uint16_t>(x.y >> 16));
       };
       float ra[4], rr[4], rb[4], rk[4], rw[4];
-      raw4(a_rs, ra);
-      raw4(r_rs, rr);
-      raw4(b_rs, rb);
-      raw4(k_rs, rk);
-      raw4(w_rs, rw);
+      raw4(raw_cur[0], ra);
+      raw4(raw_cur[1], rr);
+      raw4(raw_cur[2], rb);
+      raw4(raw_cur[3], rk);
+      raw4(raw_cur[4], rw);
+      float grad_r[4], grad_a[4], grad_b[4], grad_k[4];
       const int t = 16 * pb + n;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -858,7 +929,11 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
         const float lg = t < ntok ? log2_retention<M>(xin) : 0.0f;
         const float gam = sm.gc[kf];
         const float inv_g = __builtin_amdgcn_rcpf(gam);
-        const float G = sm.gt[t][kf];
+        // Inclusive cumulative log2 decay G_t: the block sums of earlier
+        // token blocks plus a scan over this block's 16 tokens (lane n).
+        float G = prefix16(lg);
+#pragma unroll
+        for (int q = 0; q < 3; ++q) G += q < pb ? sm.wave_tot[q][kf] : 0.0f;
         const float upg = fast_exp2(G);
         const float dng = fast_exp2(-G);
         const float upp = fast_exp2(G - lg);
@@ -866,24 +941,30 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
         const float dAt = acc_z[j] + inv_g * acc_a[j];
         const float dBc = acc_bh[j] + gam * acc_bt[j];  // dBh + g dBt
         const float dKc = acc_kh[j] + gam * acc_kt[j];  // dKh + g dKt
-        grad_r[kb][j] = dRt * upg;
-        grad_a[kb][j] = dAt * upp;
-        grad_b[kb][j] = dng * dBc;
-        grad_k[kb][j] = dng * dKc;
+        grad_r[j] = dRt * upg;
+        grad_a[j] = dAt * upp;
+        grad_b[j] = dng * dBc;
+        grad_k[j] = dng * dKc;
         const float rt_v = rr[j] * upg, at_v = ra[j] * upp;
         const float bh_v = rb[j] * dng, kh_v = rk[j] * dng;
         e2v[kb][j] = dAt * at_v;
-        e12[kb][j] = dRt * rt_v - dBc * bh_v - dKc * kh_v + e2v[kb][j];
-        e3v[kb][j] = gam * (acc_bt[j] * bh_v + acc_kt[j] * kh_v);
+        // Decay gradient pieces: suffix sum of e1 + e2 over the block's
+        // tokens and the block total of e3 (lane n = 0 holds the totals).
+        suf[kb][j] = suffix16(dRt * rt_v - dBc * bh_v - dKc * kh_v + e2v[kb][j]);
+        const float tot3 = suffix16(gam * (acc_bt[j] * bh_v + acc_kt[j] * kh_v));
+        if (n == 0) {
+          sm.carry[pb][kf] = suf[kb][j];
+          sm.carry3[pb][kf] = tot3;
+        }
         dec_in[kb][j] = xin;
       }
-      if (t < ntok) {
-        auto st4 = [&](void* dst, const float (&x)[4][4]) {
+      {
+        auto st4 = [&](void* dst, const float (&x)[4]) {
           u32x2 q;
-          q.x = static_cast<uint32_t>(from_f32<T>(x[kb][0])) |
-                (static_cast<uint32_t>(from_f32<T>(x[kb][1])) << 16);
-          q.y = static_cast<uint32_t>(from_f32<T>(x[kb][2])) |
-                (static_cast<uint32_t>(from_f32<T>(x[kb][3])) << 16);
+          q.x = static_cast<uint32_t>(from_f32<T>(x[0])) |
+                (static_cast<uint32_t>(from_f32<T>(x[1])) << 16);
+          q.y = static_cast<uint32_t>(from_f32<T>(x[2])) |
+                (static_cast<uint32_t>(from_f32<T>(x[3])) << 16);
           __builtin_amdgcn_raw_buffer_store_b64(q, rs(dst), tok_off, so, 0);
         };
         st4(p.dr, grad_r);
@@ -893,21 +974,7 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
       }
     }
 
-    // Decay gradient: suffix sums over the chunk's tokens of e12, total of e3.
-    float suf[4][4], tot3[4][4];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        suf[kb][j] = suffix16(e12[kb][j]);
-        tot3[kb][j] = suffix16(e3v[kb][j]);
-        if (n == 0) {
-          const int kf = 16 * kb + 4 * g + j;
-          sm.carry[pb][kf] = suf[kb][j];
-          sm.carry3[pb][kf] = tot3[kb][j];
-        }
-      }
-    }
+    // Decay gradient: combine the blocks' suffix sums and e3 totals.
     __syncthreads();
     {
       const int t = 16 * pb + n;
@@ -937,7 +1004,7 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
           }
           dwv[j] = d;
         }
-        if (t < ntok) {
+        {
           u32x2 q;
           q.x = static_cast<uint32_t>(from_f32<T>(dwv[0])) |
                 (static_cast<uint32_t>(from_f32<T>(dwv[1])) << 16);
