@@ -125,6 +125,74 @@ def cpu_baseline_decode(batch, heads, seconds):
     }
 
 
+def cpu_baseline_gate(cores):
+    """The reference bench's correctness gate (benchmarks/tmix/wkv7/bench.py:374-501),
+    run beside the CPU baseline with the same fp64 oracle as the checker.
+
+    Inputs follow the reference bench's recipe (bench.py:309-371) at config 1's
+    decode shape: B=256, H=40, D=64, T=1, bf16, r*0.15, decay logits*4.0,
+    k/v/a/b*0.08, a pool of B+4 slots ~ N(0, 0.02), state_indices reversed.
+    The public entry (decay logits) runs twice from the same state; the gate
+    checks relative RMSE of output and written state against the oracle
+    (limit 0.002, the fp32io16_recurrent entry of
+    tests/fixtures/tolerances-v1.json), bitwise-untouched unused slots,
+    bitwise determinism and finiteness."""
+    import numpy as np
+    import torch
+
+    import flashrwkv_amd
+    from oracle import oracle
+
+    batch, heads, d = 256, 40, 64
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(20260811)
+    shape = (batch, heads, d)
+
+    def rnd(scale):
+        return (torch.randn(shape, generator=gen) * scale).to(torch.bfloat16)
+
+    r, x, k, v, a, b = rnd(0.15), rnd(4.0), rnd(0.08), rnd(0.08), rnd(0.08), rnd(0.08)
+    pool = torch.randn((batch + 4, heads, d, d), generator=gen) * 0.02
+    cu = torch.arange(batch + 1, dtype=torch.int32)
+    slots = torch.arange(batch - 1, -1, -1, dtype=torch.int32)
+    dv = {n: t.to(dev) for n, t in (("r", r), ("x", x), ("k", k), ("v", v), ("a", a),
+                                    ("b", b), ("cu", cu), ("slots", slots))}
+    ticket = flashrwkv_amd.prepare_recurrent_metadata(
+        dv["cu"], dv["slots"], total_tokens=batch, state_pool_size=batch + 4)
+    runs = []
+    for _ in range(2):
+        state = pool.to(dev)
+        out = flashrwkv_amd.infer_recurrent_fp32io16_forward_varlen(
+            dv["r"], dv["x"], dv["k"], dv["v"], dv["a"], dv["b"], state_pool=state,
+            cu_seqlens=dv["cu"], state_indices=dv["slots"], validated_metadata=ticket)
+        torch.cuda.synchronize()
+        runs.append((out.cpu(), state.cpu()))
+    (out, state), (out2, state2) = runs
+    w = oracle.retention_from_logits(x.double().numpy())
+    y_ref, pool_ref = oracle.forward_varlen(
+        r.double().numpy(), w, k.double().numpy(), v.double().numpy(), a.double().numpy(),
+        b.double().numpy(), pool.double().numpy(), cu.numpy(), slots.numpy(),
+        num_threads=cores)
+    active = slots.long().numpy()
+    untouched = [i for i in range(batch + 4) if i not in set(active.tolist())]
+    out_rmse = oracle.relative_rmse(out.double().numpy(), y_ref)
+    state_rmse = oracle.relative_rmse(state.double().numpy()[active], pool_ref[active])
+    limit = 0.002
+    gate = {
+        "output_relative_rmse": out_rmse,
+        "state_relative_rmse": state_rmse,
+        "limit_relative_rmse": limit,
+        "untouched_slots": bool(torch.equal(state[untouched], pool[untouched])),
+        "deterministic": bool(torch.equal(out, out2) and torch.equal(state, state2)),
+        "finite": bool(torch.isfinite(out.float()).all() and torch.isfinite(state).all()),
+        "inputs": "reference bench recipe at B=256, H=40, D=64, bf16, public decay-logits entry",
+    }
+    gate["passed"] = bool(gate["finite"] and gate["untouched_slots"] and gate["deterministic"]
+                          and out_rmse <= limit and state_rmse <= limit
+                          and np.isfinite(out_rmse) and np.isfinite(state_rmse))
+    return gate
+
+
 def bench_decode(args):
     import torch
 
@@ -242,6 +310,7 @@ def bench_decode(args):
     }
     if args.cpu_seconds > 0:
         line["cpu_baseline"] = cpu_baseline_decode(batch, heads, args.cpu_seconds)
+        line["gate"] = cpu_baseline_gate(line["cpu_baseline"]["cores"])
     return line
 
 
@@ -356,6 +425,69 @@ def bench_prefill(args):
     if args.cpu_seconds > 0:
         out["cpu_baseline"] = cpu_baseline_prefill(t_len, heads, args.cpu_seconds)
     return out
+
+
+def bench_prefill_varlen(args):
+    """BASELINE config 3, varlen batch: 64 packed sequences with lengths
+    uniform in [128, 4096] (seeded), H=32, D=64, bf16 io, u ~ U(-8, 0), fp32
+    pool. Algorithmic FLOPs count each sequence's chunks at their real length
+    (a partial last chunk of c tokens costs chunk_flops(c))."""
+    import torch
+
+    import flashrwkv_amd
+    from flashrwkv_amd import workloads
+    from flashrwkv_amd.tmix.wkv7 import DECAY_RAW_W
+
+    ops = flashrwkv_amd._C.ops
+    dev = torch.device("cuda:0")
+    heads, d = 32, 64
+    lengths = workloads.varlen_lengths()
+    n_tok = sum(lengths)
+    tok = workloads.make_tokens(n_tok, heads, d, dtype=torch.bfloat16, seed=20260810,
+                                device=dev, u_low=-8.0)
+    offsets = [0]
+    for length in lengths:
+        offsets.append(offsets[-1] + length)
+    cu = torch.tensor(offsets, device=dev, dtype=torch.int32)
+    batch = len(lengths)
+    slots = torch.arange(batch, device=dev, dtype=torch.int32)
+    pool = torch.zeros((batch, heads, d, d), device=dev)
+    stream = torch.cuda.Stream(device=dev)
+
+    def step():
+        ops.chunk_forward_internal(tok["r"], tok["w"], tok["k"], tok["v"], tok["a"],
+                                   tok["b"], pool, cu, slots, 1.0, DECAY_RAW_W, None)
+
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            step()
+        stream.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(args.prefill_steps):
+            step()
+        end.record(stream)
+        end.synchronize()
+    ms = start.elapsed_time(end) / args.prefill_steps
+    flops = heads * sum((length // 64) * chunk_flops() + chunk_flops(length % 64)
+                        for length in lengths)
+    nbytes = n_tok * heads * 7 * d * 2 + 2 * batch * heads * d * d * 4
+    tflops = flops / (ms * 1e-3) / 1e12
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    return {
+        "workload": f"wkv7_chunked_prefill_cfg3_varlen: {batch} sequences, lengths "
+                    f"U[128,4096] (seeded; N={n_tok}), H=32, D=64, bf16 io, u~U(-8,0), "
+                    "fp32 pool",
+        "ms_per_step": round(ms, 4),
+        "tokens_per_s": round(n_tok / (ms * 1e-3), 1),
+        "achieved_TFLOPs": round(tflops, 2),
+        "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+        "achieved_GBps": round(gbps, 1),
+        "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+        "algorithmic_flops": flops,
+        "algorithmic_bytes": nbytes,
+    }
 
 
 def bench_training(args):
@@ -560,6 +692,7 @@ def main():
         }
         if "cpu_baseline" in pre:
             line["cpu_baseline"] = pre["cpu_baseline"]
+        line["varlen"] = bench_prefill_varlen(args)
     elif args.workload == "training":
         line = {"metric": METRIC, "training": bench_training(args)}
     elif args.workload == "copy":
@@ -570,6 +703,7 @@ def main():
         line = bench_decode(args)
         if args.workload == "all":
             line["chunked_prefill"] = bench_prefill(args)
+            line["chunked_prefill"]["varlen"] = bench_prefill_varlen(args)
             line["training"] = bench_training(args)
             line["recurrent_long"] = bench_recurrent_long(args)
     print(json.dumps(line), flush=True)

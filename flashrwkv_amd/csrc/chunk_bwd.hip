@@ -65,7 +65,7 @@ struct BwdSmem {
   uint16_t ktT[kOpTile];  // [k][t]
   uint16_t atT[kOpTile];  // [k][t]
   uint16_t rtT[kOpTile];  // [k][t]
-  uint16_t dy_x[kOpTile];       // dY [t][v] (unscaled)
+  uint16_t dy_x[kOpTile];       // scale * dY [t][v]
   uint16_t v_x[kOpTile];        // V  [t][v]
   float gc[kHead];              // 2^GC
   float wave_tot[4][kHead];     // per-block sums of log2 w (prepare; read by tokens)
@@ -179,13 +179,23 @@ __device__ __forceinline__ void store_piece_bf16(uint16_t* dst, uint4 q) {
   }
 }
 
+// 8 io-dtype values times `scale` -> 8 bf16 at an 8-byte aligned LDS address.
+template <typename T>
+__device__ __forceinline__ void store_piece_scaled_bf16(uint16_t* dst, uint4 q, float scale) {
+  float x[8];
+  unpack8<T>(q, x);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] *= scale;
+  store8_bf16(dst, x);
+}
+
 // Prepare: the forward's operand tiles restricted to the chunk, plus At^T,
 // Rt^T (token-contiguous), the per-block decay sums and the dY / V tiles.
 // Returns whether the decay span is within the single-reference limit. Ends
 // with a barrier.
 template <typename T, DecayMode M>
 __device__ bool prepare_bwd(BwdSmem& sm, const BwdRows& rows, const float (&bias)[8],
-                            int ntok) {
+                            int ntok, float scale) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -245,7 +255,7 @@ __device__ bool prepare_bwd(BwdSmem& sm, const BwdRows& rows, const float (&bias
   for (int s = 0; s < 2; ++s) {
     const int piece = tid + 256 * s;
     const int off = (piece >> 3) * kOpStride + 8 * (piece & 7);
-    store_piece_bf16<T>(sm.dy_x + off, rows.dy[s]);
+    store_piece_scaled_bf16<T>(sm.dy_x + off, rows.dy[s], scale);
     store_piece_bf16<T>(sm.v_x + off, rows.v[s]);
   }
   float up0[8], up1[8], dn0[8], dn1[8], gcv[8], upp[8];
@@ -545,7 +555,7 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
     const auto r_rs = rs(p.r), w_rs = rs(p.decay), k_rs = rs(p.k), a_rs = rs(p.a),
                b_rs = rs(p.b);
 
-    const bool whole = prepare_bwd<T, M>(sm, rows, bias, ntok);
+    const bool whole = prepare_bwd<T, M>(sm, rows, bias, ntok, p.scale);
     failed = failed || !whole;
     f32x4 S0[4];
 #pragma unroll
@@ -580,14 +590,8 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
     i16x4 vs[4], dys[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      f32x4 dyf;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int idx = (16 * q + 4 * g + e) * kOpStride + 16 * wave + n;
-        vs[q][e] = static_cast<short>(sm.v_x[idx]);
-        dyf[e] = p.scale * bf16_float(sm.dy_x[idx]);
-      }
-      dys[q] = to_operand(dyf);
+      vs[q] = lds_operand_tr<kOpStride>(sm.v_x, 16 * q, 16 * wave, g, n);
+      dys[q] = lds_operand_tr<kOpStride>(sm.dy_x, 16 * q, 16 * wave, g, n);
     }
     const i16x4 z4 = {0, 0, 0, 0};
     auto lo32 = [&](i16x4 x) { return cat(x, z4); };
@@ -789,11 +793,8 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
         mt = mfma32(y, x, mt);
         mc = mfma32(x, y, mc);
       }
-      const float sc = m < 2 ? p.scale : 1.0f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        mt[j] *= sc;
-        mc[j] *= sc;
         if (pb == q) {
           // mt: lane holds M[t = n][i = 4g + j]; mc: M[t = 4g + j][i = n].
           const int it = 4 * g + j;
@@ -937,7 +938,7 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
         const float upg = fast_exp2(G);
         const float dng = fast_exp2(-G);
         const float upp = fast_exp2(G - lg);
-        const float dRt = p.scale * acc_s[j] + inv_g * acc_r[j];
+        const float dRt = acc_s[j] + inv_g * acc_r[j];
         const float dAt = acc_z[j] + inv_g * acc_a[j];
         const float dBc = acc_bh[j] + gam * acc_bt[j];  // dBh + g dBt
         const float dKc = acc_kh[j] + gam * acc_kt[j];  // dKh + g dKt

@@ -99,12 +99,26 @@ struct ChunkFwdParams {
 };
 
 // Token rows of one chunk held by a thread: r, w, k, a, b for 2 tokens x 8
-// features (prepare layout), and V in MFMA operand layout for the wave's 16
-// value columns: lane (g, n) holds V[16q + 4g + e][16w + n] in vs[q][e].
+// features (prepare layout), and two 16-byte pieces of the chunk's V tile
+// (piece tid + 256 s: token (tid + 256 s) / 8, features 8 ((tid + 256 s) % 8)
+// .. +7). V goes through LDS to reach the MFMA operand layout.
 struct ChunkRows {
   uint4 r[2], w[2], k[2], a[2], b[2];
-  i16x4 vs[4];
+  uint4 v[2];
 };
+
+// 8 io-dtype values -> 8 bf16 at an 8-byte aligned LDS address.
+template <typename T>
+__device__ __forceinline__ void store_piece_bf16(uint16_t* dst, uint4 q) {
+  if constexpr (__is_same(T, Bf16)) {
+    reinterpret_cast<uint2*>(dst)[0] = make_uint2(q.x, q.y);
+    reinterpret_cast<uint2*>(dst)[1] = make_uint2(q.z, q.w);
+  } else {
+    float x[8];
+    unpack8<T>(q, x);
+    store8_bf16(dst, x);
+  }
+}
 
 // Decay-span verdicts of a prepared range, uniform over the workgroup: is
 // the span of the whole range, resp. of each 16-token block, within the
@@ -369,7 +383,7 @@ __device__ void intra_chunk(ChunkSmem& sm) {
 // (row t at byte t * row_bytes, resp. 2 * t * row_bytes); sda_rs is unused
 // when with_sda is false.
 template <typename T>
-__device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const i16x4 (&vs)[4],
+__device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const uint16_t* vtile,
                            __amdgpu_buffer_rsrc_t out_rs, __amdgpu_buffer_rsrc_t sda_rs,
                            bool with_sda, uint32_t row_bytes, float scale, int lo, int hi) {
   const int tid = threadIdx.x;
@@ -377,6 +391,10 @@ __device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const i16x4 (&vs)
   const int lane = tid & 63;
   const int g = lane >> 4;
   const int n = lane & 15;
+  // The wave's V columns in operand layout: vs[q] holds V[16q + 4g + e][16w + n].
+  i16x4 vs[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) vs[q] = lds_operand_tr<kOpStride>(vtile, 16 * q, 16 * w, g, n);
 
   // Operands: S0 (C layout; B operand of products over keys, A operand of
   // the transposed output product), V slice, then SA as it is solved. A
@@ -598,11 +616,9 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
   };
   using S16c = typename IoTraits<T>::storage;
   const uint32_t row_bytes = static_cast<uint32_t>(heads) * kHead * 2;
-  // Per-lane byte offsets inside a chunk's rows: prepare layout (token
-  // 16w + 2tp [+1], features 8kg..8kg+7) and V operand layout (token
-  // 16q + 4g + e, feature 16w + n; the (q, e) part is a scalar offset).
+  // Per-lane byte offset inside a chunk's rows in the prepare layout (token
+  // 16w + 2tp [+1], features 8kg..8kg+7).
   const uint32_t prep_off = static_cast<uint32_t>(16 * wave + 2 * tp) * row_bytes + 16 * kg;
-  const uint32_t v_off = static_cast<uint32_t>(4 * g) * row_bytes + 2 * (16 * wave + n);
   auto load_rows = [&](ChunkRows& rows, int c0, int ntok) {
     const int64_t base = (static_cast<int64_t>(c0) * heads + head) * kHead;
     const uint32_t bytes = static_cast<uint32_t>(ntok) * row_bytes;
@@ -623,18 +639,11 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
     }
     const auto rv = rs(p.v);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint16_t x = __builtin_amdgcn_raw_buffer_load_b16(
-            rv, v_off, static_cast<int>((16 * q + e) * row_bytes), 0);
-        // MFMA operands are bf16: fp16 tokens are converted, bf16 ones pass.
-        if constexpr (__is_same(T, Bf16)) {
-          rows.vs[q][e] = static_cast<short>(x);
-        } else {
-          rows.vs[q][e] = static_cast<short>(to_bf16_bits(to_f32<T>(x)));
-        }
-      }
+    for (int s = 0; s < 2; ++s) {
+      const int piece = tid + 256 * s;
+      const uint32_t off = static_cast<uint32_t>(piece >> 3) * row_bytes + 16 * (piece & 7);
+      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
+      rows.v[s] = make_uint4(x.x, x.y, x.z, x.w);
     }
   };
 
@@ -674,15 +683,15 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
       Spans spans{};
       bool whole = true, first = true;
       int lo = 0, hi = ntok;
-      i16x4 vs[4];
+      uint4 vpiece[2];
       for (;;) {
         const Spans cur = prepare<T, M>(sm, rows, bias, lo, hi);
         if (first) {
           first = false;
           spans = cur;
           whole = cur.whole;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) vs[q] = rows.vs[q];
+          vpiece[0] = rows.v[0];
+          vpiece[1] = rows.v[1];
           if (!whole) {
             hi = min(spans.block[0] ? 16 : 4, ntok);
             continue;
@@ -690,6 +699,14 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
           if (has_next) load_rows(rows, nc0, min(kChunk, nend - nc0));
         }
         intra_chunk(sm);
+        // Bh and Kh are dead after the intra-chunk products: the Bh tile
+        // holds the chunk's V ([t][v]) for the state pass.
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const int piece = tid + 256 * s;
+          store_piece_bf16<T>(sm.bh + (piece >> 3) * kOpStride + 8 * (piece & 7), vpiece[s]);
+        }
+        __syncthreads();
         {
           const int64_t base = (static_cast<int64_t>(c0) * heads + head) * kHead;
           const auto out_rs = buffer_rsrc(static_cast<S16c*>(p.out) + base,
@@ -697,7 +714,7 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
           const auto sda_rs = buffer_rsrc(
               p.state_dot_a != nullptr ? p.state_dot_a + base : nullptr,
               p.state_dot_a != nullptr ? 2u * static_cast<uint32_t>(ntok) * row_bytes : 0u);
-          state_pass<T>(sm, S, vs, out_rs, sda_rs, p.state_dot_a != nullptr, row_bytes,
+          state_pass<T>(sm, S, sm.bh, out_rs, sda_rs, p.state_dot_a != nullptr, row_bytes,
                         p.scale, lo, hi);
         }
         if (whole) break;

@@ -111,6 +111,29 @@ __device__ __forceinline__ i16x8 lds_operand32(const uint16_t* tile, int row, in
              lds_operand<Stride>(tile, row, col + 16 + 4 * g));
 }
 
+// B operand over tokens from a row-major [t][col] LDS tile via the gfx950
+// transpose read (ds_read_b64_tr_b16): lane (g, n) receives
+// X[t0 + 4g + e][c0 + n], e = 0..3, i.e. the MFMA operand layout for
+// K = tokens t0 .. t0 + 15. Within a 16-lane group, lane i's element e
+// comes from the 8 bytes addressed by lane 4e + i / 4, element i % 4, so
+// lane j addresses row t0 + 4g + j / 4, columns c0 + 4 (j % 4) .. +3. The
+// row stride (elements) must keep those addresses 8-byte aligned.
+template <int Stride>
+__device__ __forceinline__ i16x4 lds_operand_tr(const uint16_t* tile, int t0, int c0, int g,
+                                                int n) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  static_assert((Stride * 2) % 8 == 0, "rows must be 8-byte aligned");
+  const uint16_t* src = tile + (t0 + 4 * g + (n >> 2)) * Stride + c0 + 4 * (n & 3);
+  const v4i16 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16*)(src));
+  i16x4 r;
+  r[0] = x[0];
+  r[1] = x[1];
+  r[2] = x[2];
+  r[3] = x[3];
+  return r;
+}
+
 // Stores a C-layout tile transposed: lane (g, n) writes its 4 values to
 // dst[n][4g .. 4g+3] of a tile with the given row stride (one 8-byte write).
 __device__ __forceinline__ void lds_store_transposed(uint16_t* dst, int stride,

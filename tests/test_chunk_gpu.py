@@ -183,6 +183,40 @@ def test_config3_full_shape_sampled_heads():
         _check(f"state seq{seq} head{head}", pool[seq, head], s_ref[0, 0])
 
 
+def test_config3_varlen_batch_sampled_sequences():
+    """BASELINE config 3's varlen batch: 64 packed sequences with lengths
+    uniform in [128, 4096] (cu_seqlens offsets, slots permuted). Sequences and
+    heads are independent, so the oracle checks a sample of (sequence, head)
+    pairs at their full lengths, including the shortest and longest."""
+    lengths = workloads.varlen_lengths()
+    heads = 32
+    slots = tuple(reversed(range(len(lengths))))
+    case = workloads.make_case(lengths=lengths, heads=heads, head_size=64,
+                               dtype=torch.bfloat16, seed=20260810, state_std=0.1,
+                               u_low=-8.0, slots=slots)
+    d = _dev(case)
+    pool = d["state_pool"].clone()
+    y = chunk_forward_internal(d["r"], d["w"], d["k"], d["v"], d["a"], d["b"],
+                               state_pool=pool, cu_seqlens=d["cu_seqlens"],
+                               state_indices=d["state_indices"], decay_mode=DECAY_RAW_W)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all()
+    cu = case["cu_seqlens"].numpy()
+    shortest = int(np.argmin(lengths))
+    longest = int(np.argmax(lengths))
+    for seq, head in ((shortest, 3), (longest, 17), (21, 0), (63, 31)):
+        sl = slice(int(cu[seq]), int(cu[seq + 1]))
+        length = sl.stop - sl.start
+        sub = {n: case[n][sl, head:head + 1] for n in ("r", "w", "k", "v", "a", "b")}
+        slot = slots[seq]
+        s0 = _np(case["state_pool"][slot:slot + 1, head:head + 1])
+        y_ref, s_ref = oracle.forward_varlen(
+            *(_np(sub[n]) for n in ("r", "w", "k", "v", "a", "b")), s0,
+            np.array([0, length], dtype=np.int32), np.array([0], dtype=np.int32))
+        _check(f"y seq{seq} (L={length}) head{head}", y[sl, head:head + 1], y_ref)
+        _check(f"state seq{seq} head{head}", pool[slot, head], s_ref[0, 0])
+
+
 def test_invalid_metadata_fails_closed_with_nan_and_untouched_pool():
     lengths = (10, 20)
     case = workloads.make_case(lengths=lengths, heads=2, head_size=64,
