@@ -12,13 +12,15 @@
 //   y_t = scale S_t^T r_t.
 // Chunk form, tokens t = 0..63 of a chunk, G_t = sum_{j<=t} log2 w_j
 // (inclusive), Gp_t = G_t - log2 w_t, GC = G_63, S0 = state at chunk start:
-//   At = a 2^Gp, Rt = r 2^G, Bh = b 2^-G, Kh = k 2^-G, Bt = b 2^(GC-G),
-//   Kt = k 2^(GC-G);
+//   At = a 2^Gp, Rt = r 2^G, Bh = b 2^-G, Kh = k 2^-G;
 //   Lab = strict_lower(At Bh^T), Lak = strict_lower(At Kh^T),
 //   Arb = lower(Rt Bh^T),        Ark = lower(Rt Kh^T);
 //   SA = (I - Lab)^{-1} (At S0 + Lak V)       (rows are sa_t)
 //   Y  = scale (Rt S0 + Arb SA + Ark V)
-//   S' = diag(2^GC) S0 + Bt^T SA + Kt^T V.
+//   S' = diag(2^GC) (S0 + Bh^T SA + Kh^T V).
+// (The last product is accumulated in fp32 and scaled once: every term
+// carries the common factor 2^GC, so this keeps the relative precision of
+// scaling Bh, Kh by 2^GC first.)
 // Every exponent above is <= 0 except the 2^-G of Bh/Kh, bounded by the
 // chunk's decay span -GC. The kernel keeps that span <= 80 (log2 units): a
 // chunk whose span is larger is processed as 16-token sub-chunks, and a
@@ -32,14 +34,13 @@
 //   * prepare: the chunk's 64 tokens x 64 features are decoded once (two
 //     tokens x 8 features per thread), the cumulative decay is a wave
 //     shuffle scan plus a cross-wave carry, and the scaled operands go to LDS
-//     as bf16 ([token][feature] tiles and, for products contracting over
-//     tokens, [feature][token] tiles);
+//     as bf16 [token][feature] tiles (products contracting over tokens read
+//     them through gfx950's LDS transpose read);
 //   * intra-chunk products: the 40 lower-triangular 16x16 blocks of Lab,
 //     Lak, Arb, Ark (stored packed) are spread over the four waves; wave p
 //     also inverts the diagonal block I - Lab_pp (forward substitution);
 //   * state-dependent part: wave w owns value columns 16w..16w+15. Its slice
-//     of the fp32 state lives in MFMA accumulators for the whole sequence
-//     and its slice of V is loaded from HBM straight into operand registers;
+//     of the fp32 state lives in MFMA accumulators for the whole sequence;
 //     the block forward substitution SA_p = T_pp (rhs_p + sum_q Lab_pq SA_q),
 //     the output tiles and the state update chain through registers, so this
 //     part has no barrier.
@@ -57,8 +58,7 @@ struct ChunkSmem {
   uint16_t rt[kOpTile];   // [t][k]
   uint16_t bh[kOpTile];   // [t][k]
   uint16_t kh[kOpTile];   // [t][k]
-  uint16_t btT[kOpTile];  // [k][t]
-  uint16_t ktT[kOpTile];  // [k][t]
+  uint16_t vt[kOpTile];   // V [t][v]
   union {
     uint16_t tri[4][kTriBlocks * kTriBlock];  // Lab, Lak, Arb, Ark: [t][i]
     float wave_tot[4][kHead];                 // decay scan carry (prepare only)
@@ -134,7 +134,12 @@ struct Spans {
 };
 
 // Decodes the thread's rows restricted to tokens [lo, hi) of the chunk,
-// scans the decay and writes every scaled operand tile. Ends with a barrier.
+// scans the decay and writes the scaled operand tiles At, Rt, Bh, Kh
+// ([t][k]) and the V tile. Ends with a barrier.
+//
+// Per feature, the thread's tokens t0 and t0 + 1 need 2^Gp(t0), 2^G(t0)
+// (= 2^Gp(t0 + 1)), 2^G(t0 + 1), 2^-G(t0), 2^-G(t0 + 1): two exponentials
+// and products with the retentions w = 2^lg (G(t) = Gp(t) + lg(t)).
 template <typename T, DecayMode M>
 __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bias)[8],
                          int lo, int hi) {
@@ -144,20 +149,32 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
   const int tp = lane & 7;   // token pair
   const int kg = lane >> 3;  // feature group
   const int t0 = 16 * wave + 2 * tp;
-  const float on0 = (t0 >= lo && t0 < hi) ? 1.0f : 0.0f;
-  const float on1 = (t0 + 1 >= lo && t0 + 1 < hi) ? 1.0f : 0.0f;
+  const bool on0 = t0 >= lo && t0 < hi;
+  const bool on1 = t0 + 1 >= lo && t0 + 1 < hi;
 
   __syncthreads();  // earlier readers of the tiles are done
 
-  float lg0[8], lg1[8];
+  // log2 retention and the retention itself; tokens outside [lo, hi) get
+  // lg = 0, w = 1 (no decay, and their operand rows are zero below).
+  float lg0[8], lg1[8], w0[8], w1[8];
   {
-    float w0[8], w1[8];
-    unpack8<T>(rows.w[0], w0);
-    unpack8<T>(rows.w[1], w1);
+    float x0[8], x1[8];
+    unpack8<T>(rows.w[0], x0);
+    unpack8<T>(rows.w[1], x1);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      lg0[e] = on0 * log2_retention<M>(w0[e] + bias[e]);
-      lg1[e] = on1 * log2_retention<M>(w1[e] + bias[e]);
+      const float l0 = log2_retention<M>(x0[e] + bias[e]);
+      const float l1 = log2_retention<M>(x1[e] + bias[e]);
+      lg0[e] = on0 ? l0 : 0.0f;
+      lg1[e] = on1 ? l1 : 0.0f;
+      if constexpr (M == DecayMode::kRawW) {
+        // 2^lg is the input clamped to [2^-20, 1] (log2_retention's clamp).
+        w0[e] = on0 ? fminf(fmaxf(x0[e], 0x1p-20f), 1.0f) : 1.0f;
+        w1[e] = on1 ? fminf(fmaxf(x1[e], 0x1p-20f), 1.0f) : 1.0f;
+      } else {
+        w0[e] = fast_exp2(lg0[e]);
+        w1[e] = fast_exp2(lg1[e]);
+      }
     }
   }
 
@@ -177,23 +194,31 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
   }
   __syncthreads();
 
-  float g0[8], g1[8], gp0[8], total[8];
+  float gp0[8], g1[8], total[8];
   bool over_all = false, over_block[4] = {false, false, false, false};
+  {
+    float base[8], tot[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float base = 0.0f, tot = 0.0f;
+    for (int e = 0; e < 8; ++e) base[e] = tot[e] = 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const float x = sm.wave_tot[q][8 * kg + e];
-      base += (q < wave) ? x : 0.0f;
-      tot += x;
-      over_block[q] |= -x > kSpanLimit;
+      const float4 xa = *reinterpret_cast<const float4*>(&sm.wave_tot[q][8 * kg]);
+      const float4 xb = *reinterpret_cast<const float4*>(&sm.wave_tot[q][8 * kg + 4]);
+      const float x[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        base[e] += (q < wave) ? x[e] : 0.0f;
+        tot[e] += x[e];
+        over_block[q] |= -x[e] > kSpanLimit;
+      }
     }
-    total[e] = tot;
-    over_all |= -tot > kSpanLimit;
-    gp0[e] = base + incl[e] - lg0[e] - lg1[e];
-    g0[e] = gp0[e] + lg0[e];
-    g1[e] = g0[e] + lg1[e];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      total[e] = tot[e];
+      over_all |= -tot[e] > kSpanLimit;
+      gp0[e] = base[e] + incl[e] - lg0[e] - lg1[e];
+      g1[e] = gp0[e] + lg0[e] + lg1[e];
+    }
   }
   // Every wave covers all 64 features, so the ballots agree across waves.
   Spans spans;
@@ -201,64 +226,44 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
 #pragma unroll
   for (int q = 0; q < 4; ++q) spans.block[q] = __builtin_amdgcn_ballot_w64(over_block[q]) == 0;
 
-  // Token t0: gp = gp0, g = g0; token t0 + 1: gp = g0, g = g1.
-  float up0[8], up1[8], dn0[8], dn1[8], gcv[8];
+  // Scale factors of the thread's two token rows, zero outside [lo, hi).
+  float fa0[8], fa1[8], fr0[8], fr1[8], fd0[8], fd1[8], gcv[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    up0[e] = fast_exp2(g0[e]);   // 2^G(t0)  (= 2^Gp(t0+1))
-    up1[e] = fast_exp2(g1[e]);   // 2^G(t0+1)
-    dn0[e] = fast_exp2(-g0[e]);
-    dn1[e] = fast_exp2(-g1[e]);
+    const float up_p = fast_exp2(gp0[e]);  // 2^Gp(t0)
+    const float up0 = up_p * w0[e];        // 2^G(t0) = 2^Gp(t0 + 1)
+    const float up1 = up0 * w1[e];         // 2^G(t0 + 1)
+    const float dn1 = fast_exp2(-g1[e]);   // 2^-G(t0 + 1)
+    const float dn0 = dn1 * w1[e];         // 2^-G(t0)
+    fa0[e] = on0 ? up_p : 0.0f;
+    fa1[e] = on1 ? up0 : 0.0f;
+    fr0[e] = on0 ? up0 : 0.0f;
+    fr1[e] = on1 ? up1 : 0.0f;
+    fd0[e] = on0 ? dn0 : 0.0f;
+    fd1[e] = on1 ? dn1 : 0.0f;
     gcv[e] = fast_exp2(total[e]);
   }
-  {
-    float x0[8], x1[8], t[8];
-    unpack8<T>(rows.a[0], x0);
-    unpack8<T>(rows.a[1], x1);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) t[e] = on0 * x0[e] * fast_exp2(gp0[e]);
-    store8_bf16(sm.at + t0 * kOpStride + 8 * kg, t);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) t[e] = on1 * x1[e] * up0[e];
-    store8_bf16(sm.at + (t0 + 1) * kOpStride + 8 * kg, t);
-
-    unpack8<T>(rows.r[0], x0);
-    unpack8<T>(rows.r[1], x1);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) t[e] = on0 * x0[e] * up0[e];
-    store8_bf16(sm.rt + t0 * kOpStride + 8 * kg, t);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) t[e] = on1 * x1[e] * up1[e];
-    store8_bf16(sm.rt + (t0 + 1) * kOpStride + 8 * kg, t);
-
-    unpack8<T>(rows.b[0], x0);
-    unpack8<T>(rows.b[1], x1);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) t[e] = on0 * x0[e] * dn0[e];
-    store8_bf16(sm.bh + t0 * kOpStride + 8 * kg, t);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) t[e] = on1 * x1[e] * dn1[e];
-    store8_bf16(sm.bh + (t0 + 1) * kOpStride + 8 * kg, t);
-    // Token-contiguous tile: the thread's two tokens form one 32-bit pair.
+  auto tile_rows = [&](uint16_t* tile, uint4 q0, uint4 q1, const float (&f0)[8],
+                       const float (&f1)[8]) {
+    float x0[8], x1[8];
+    unpack8<T>(q0, x0);
+    unpack8<T>(q1, x1);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      *reinterpret_cast<uint32_t*>(sm.btT + (8 * kg + e) * kOpStride + t0) =
-          pack_bf16x2(on0 * x0[e] * (gcv[e] * dn0[e]), on1 * x1[e] * (gcv[e] * dn1[e]));
+      x0[e] *= f0[e];
+      x1[e] *= f1[e];
     }
-
-    unpack8<T>(rows.k[0], x0);
-    unpack8<T>(rows.k[1], x1);
+    store8_bf16(tile + t0 * kOpStride + 8 * kg, x0);
+    store8_bf16(tile + (t0 + 1) * kOpStride + 8 * kg, x1);
+  };
+  tile_rows(sm.at, rows.a[0], rows.a[1], fa0, fa1);
+  tile_rows(sm.rt, rows.r[0], rows.r[1], fr0, fr1);
+  tile_rows(sm.bh, rows.b[0], rows.b[1], fd0, fd1);
+  tile_rows(sm.kh, rows.k[0], rows.k[1], fd0, fd1);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) t[e] = on0 * x0[e] * dn0[e];
-    store8_bf16(sm.kh + t0 * kOpStride + 8 * kg, t);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) t[e] = on1 * x1[e] * dn1[e];
-    store8_bf16(sm.kh + (t0 + 1) * kOpStride + 8 * kg, t);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      *reinterpret_cast<uint32_t*>(sm.ktT + (8 * kg + e) * kOpStride + t0) =
-          pack_bf16x2(on0 * x0[e] * (gcv[e] * dn0[e]), on1 * x1[e] * (gcv[e] * dn1[e]));
-    }
+  for (int s = 0; s < 2; ++s) {
+    const int piece = tid + 256 * s;
+    store_piece_bf16<T>(sm.vt + (piece >> 3) * kOpStride + 8 * (piece & 7), rows.v[s]);
   }
   if (wave == 0 && tp == 0) {
 #pragma unroll
@@ -471,49 +476,47 @@ __device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const uint16_t* v
     }
   }
 
-  // Y^T blocks (rows v of w, cols t of block p) and S' = diag(2^GC) S0 +
-  // Bt^T SA + Kt^T V: eight independent chains.
+  // Y^T blocks (rows v of w, cols t of block p) and S' = diag(2^GC) (S0 +
+  // Bh^T SA + Kh^T V): eight independent chains. Bh^T and Kh^T (A operands
+  // over tokens) come from the [t][k] tiles through the transpose read.
+  auto tr32 = [&](const uint16_t* tile, int kb, int c) {
+    return cat(lds_operand_tr<kOpStride>(tile, c, 16 * kb, g, n),
+               lds_operand_tr<kOpStride>(tile, c + 16, 16 * kb, g, n));
+  };
   f32x4 y[4], sn[4];
 #pragma unroll
   for (int pb = 0; pb < 4; ++pb) {
     y[pb] = mfma32(s01, lds_operand32<kOpStride>(sm.rt, 16 * pb + n, 0, g), zero4());
   }
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) sn[kb][j] = S[kb][j] * sm.gc[16 * kb + 4 * g + j];
-    sn[kb] = mfma32(lds_operand32<kOpStride>(sm.btT, 16 * kb + n, 0, g), sa01, sn[kb]);
-  }
+  for (int kb = 0; kb < 4; ++kb) sn[kb] = mfma32(tr32(sm.bh, kb, 0), sa01, S[kb]);
 #pragma unroll
   for (int pb = 0; pb < 4; ++pb) {
     y[pb] = mfma32(s23, lds_operand32<kOpStride>(sm.rt, 16 * pb + n, 32, g), y[pb]);
   }
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
-    sn[kb] = mfma32(lds_operand32<kOpStride>(sm.btT, 16 * kb + n, 32, g), sa23, sn[kb]);
-  }
+  for (int kb = 0; kb < 4; ++kb) sn[kb] = mfma32(tr32(sm.bh, kb, 32), sa23, sn[kb]);
   y[0] = mfma32(lo32(sab[0]), lo32(tri16(kArb, 0, 0)), y[0]);
   y[1] = mfma32(sa01, tri32(kArb, 1, 0), y[1]);
   y[2] = mfma32(sa01, tri32(kArb, 2, 0), y[2]);
   y[3] = mfma32(sa01, tri32(kArb, 3, 0), y[3]);
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
-    sn[kb] = mfma32(lds_operand32<kOpStride>(sm.ktT, 16 * kb + n, 0, g), v01, sn[kb]);
-  }
+  for (int kb = 0; kb < 4; ++kb) sn[kb] = mfma32(tr32(sm.kh, kb, 0), v01, sn[kb]);
   y[0] = mfma32(lo32(vs[0]), lo32(tri16(kArk, 0, 0)), y[0]);
   y[1] = mfma32(v01, tri32(kArk, 1, 0), y[1]);
   y[2] = mfma32(v01, tri32(kArk, 2, 0), y[2]);
   y[3] = mfma32(v01, tri32(kArk, 3, 0), y[3]);
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
-    sn[kb] = mfma32(lds_operand32<kOpStride>(sm.ktT, 16 * kb + n, 32, g), v23, sn[kb]);
-  }
+  for (int kb = 0; kb < 4; ++kb) sn[kb] = mfma32(tr32(sm.kh, kb, 32), v23, sn[kb]);
   y[2] = mfma32(lo32(sab[2]), lo32(tri16(kArb, 2, 2)), y[2]);
   y[3] = mfma32(sa23, tri32(kArb, 3, 2), y[3]);
   y[2] = mfma32(lo32(vs[2]), lo32(tri16(kArk, 2, 2)), y[2]);
   y[3] = mfma32(v23, tri32(kArk, 3, 2), y[3]);
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) S[kb] = sn[kb];
+  for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) S[kb][j] = sn[kb][j] * sm.gc[16 * kb + 4 * g + j];
+  }
 
   // Lane (g, n) stores Y[16p + n][16w + 4g .. 16w + 4g + 3] (8 bytes).
   const uint32_t y_off = static_cast<uint32_t>(n) * row_bytes + 2 * (16 * w + 4 * g);
@@ -593,10 +596,23 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
     }
   }
 
+  // Segment bounds, 64 segments at a time in VGPR lanes (lane i: segment
+  // cache_base + i), read back with readlane: a per-segment memory read would
+  // need a vmcnt wait, which on gfx9's in-order counter also waits for every
+  // output store still in flight.
+  int cache_base = seg_hi;
+  int starts_v = 0, ends_v = 0;
   auto seg_range = [&](int seg, int& t_begin, int& t_end) {
     if (p.seg_offsets != nullptr) {
-      t_begin = p.seg_starts[seg];
-      t_end = p.seg_ends[seg];
+      if (seg < cache_base || seg >= cache_base + 64) {
+        cache_base = seg;
+        const int idx = seg + lane;
+        starts_v = idx < seg_hi ? p.seg_starts[idx] : 0;
+        ends_v = idx < seg_hi ? p.seg_ends[idx] : 0;
+        __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): nothing pending at the join
+      }
+      t_begin = __builtin_amdgcn_readlane(starts_v, seg - cache_base);
+      t_end = __builtin_amdgcn_readlane(ends_v, seg - cache_base);
     } else {
       t_begin = p.cu_seqlens[seq];
       t_end = p.cu_seqlens[seq + 1];
@@ -683,15 +699,12 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
       Spans spans{};
       bool whole = true, first = true;
       int lo = 0, hi = ntok;
-      uint4 vpiece[2];
       for (;;) {
         const Spans cur = prepare<T, M>(sm, rows, bias, lo, hi);
         if (first) {
           first = false;
           spans = cur;
           whole = cur.whole;
-          vpiece[0] = rows.v[0];
-          vpiece[1] = rows.v[1];
           if (!whole) {
             hi = min(spans.block[0] ? 16 : 4, ntok);
             continue;
@@ -699,14 +712,6 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
           if (has_next) load_rows(rows, nc0, min(kChunk, nend - nc0));
         }
         intra_chunk(sm);
-        // Bh and Kh are dead after the intra-chunk products: the Bh tile
-        // holds the chunk's V ([t][v]) for the state pass.
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const int piece = tid + 256 * s;
-          store_piece_bf16<T>(sm.bh + (piece >> 3) * kOpStride + 8 * (piece & 7), vpiece[s]);
-        }
-        __syncthreads();
         {
           const int64_t base = (static_cast<int64_t>(c0) * heads + head) * kHead;
           const auto out_rs = buffer_rsrc(static_cast<S16c*>(p.out) + base,
@@ -714,7 +719,7 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
           const auto sda_rs = buffer_rsrc(
               p.state_dot_a != nullptr ? p.state_dot_a + base : nullptr,
               p.state_dot_a != nullptr ? 2u * static_cast<uint32_t>(ntok) * row_bytes : 0u);
-          state_pass<T>(sm, S, sm.bh, out_rs, sda_rs, p.state_dot_a != nullptr, row_bytes,
+          state_pass<T>(sm, S, sm.vt, out_rs, sda_rs, p.state_dot_a != nullptr, row_bytes,
                         p.scale, lo, hi);
         }
         if (whole) break;
