@@ -17,6 +17,7 @@ from .tmix.wkv7 import (
     infer_chunk_bf16_forward_varlen,
     infer_recurrent_fp32io16_forward_varlen,
     prepare_recurrent_metadata,
+    pretrain_recurrent_bf16,
 )
 from .tmix.wkv7.statetune import statetune_recurrent_fp32io16
 
@@ -24,6 +25,7 @@ __all__ = [
     "infer_chunk_bf16_forward_varlen",
     "infer_recurrent_fp32io16_forward_varlen",
     "prepare_recurrent_metadata",
+    "pretrain_recurrent_bf16",
     "statetune_recurrent_fp32io16",
 ]
 

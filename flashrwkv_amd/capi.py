@@ -31,6 +31,8 @@ SIGNATURES = {
     "frwkv_chunk_forward": [_INT] * 3 + [_I32] * 5 + [_VP] * 12 + [_F32, _VP],
     "frwkv_statetune_forward": [_INT] * 2 + [_I32] * 5 + [_VP] * 14 + [_F32, _VP],
     "frwkv_statetune_backward": [_INT] * 2 + [_I32] * 5 + [_VP] * 20 + [_F32, _VP],
+    "frwkv_pretrain_forward": [_INT] * 2 + [_I32] * 4 + [_VP] * 10,
+    "frwkv_pretrain_backward": [_INT] * 2 + [_I32] * 4 + [_VP] * 15,
 }
 
 _LIB = None
@@ -124,3 +126,21 @@ def statetune_backward(r, decay, k, v, a, b, *, sequence_chunk_offsets, chunk_to
         _p(chunk_token_ends), _p(boundary), _p(r), _p(decay), _p(decay_bias), _p(k), _p(v),
         _p(a), _p(b), _p(grad_output), _p(grad_final_state), *(_p(g) for g in grads),
         _p(grad_initial_state), float(scale), _stream()))
+
+
+def pretrain_forward(r, decay, k, v, a, b, *, output, boundary, state_dot_a,
+                     decay_mode=DECAY_LOGITS):
+    """Dense [B,T,H,D] tokens; boundary [B,H,T/16,D,D]; state_dot_a [B,T,H,D]."""
+    bsz, t_len, h, d = r.shape
+    _check(library().frwkv_pretrain_forward(
+        DTYPE[r.dtype], decay_mode, bsz, t_len, h, d, _p(r), _p(decay), _p(k), _p(v), _p(a),
+        _p(b), _p(output), _p(boundary), _p(state_dot_a), _stream()))
+
+
+def pretrain_backward(r, decay, k, v, a, b, *, grad_output, boundary, grads,
+                      decay_mode=DECAY_LOGITS):
+    """``grads`` = (grad_r, grad_decay, grad_k, grad_v, grad_a, grad_b)."""
+    bsz, t_len, h, d = r.shape
+    _check(library().frwkv_pretrain_backward(
+        DTYPE[r.dtype], decay_mode, bsz, t_len, h, d, _p(r), _p(decay), _p(k), _p(v), _p(a),
+        _p(b), _p(grad_output), _p(boundary), *(_p(g) for g in grads), _stream()))

@@ -650,6 +650,83 @@ void statetune_backward_internal(
                           static_cast<int>(decay_mode));
 }
 
+// ---------------------------------------------------------------------------
+// rwkv7_clampw_v3 (pretraining): reference
+// csrc/sm90/tmix/wkv7/pretrain_recurrent_bf16_forward.cpp:20-53. Dense
+// [B,T,H,D] tokens with clampw decay logits, S0 = 0, no final state; s is the
+// state every 16 tokens [B,H,T/16,D,D] fp32 and sa is a^T S_{t-1} [B,T,H,D]
+// fp32. Head size 64 on the MI355X chunked kernels.
+
+void check_clampw_tokens(const std::vector<std::pair<const Tensor*, const char*>>& all,
+                         int64_t head_size) {
+  TORCH_CHECK(head_size == 64 || head_size == 128 || head_size == 256,
+              "head_size must be one of 64, 128, or 256");
+  const Tensor& r = *all[0].first;
+  TORCH_CHECK(r.dim() == 4 && r.size(3) == head_size,
+              "input head dimension must equal head_size");
+  TORCH_CHECK(head_size == 64, "head_size ", head_size,
+              " is not supported by the MI355X chunked kernels (64 only)");
+  for (const auto& item : all) {
+    check_device_contiguous(*item.first, item.second);
+    TORCH_CHECK(item.first->device() == r.device(), item.second,
+                " must be on the same device as r");
+    TORCH_CHECK(item.first->scalar_type() == r.scalar_type(),
+                "r,w,k,v,a,b dtype mismatch");
+    TORCH_CHECK(item.first->sizes() == r.sizes(), item.second,
+                " must have the same shape as r");
+  }
+  TORCH_CHECK(r.scalar_type() == at::kBFloat16 || r.scalar_type() == at::kHalf,
+              "token tensors must be float16 or bfloat16");
+  TORCH_CHECK(r.size(0) > 0 && r.size(1) > 0 && r.size(2) > 0 && r.size(1) % 16 == 0,
+              "tokens must have shape [B,T,H,D] with T a positive multiple of 16");
+  TORCH_CHECK(r.size(0) * r.size(1) <= std::numeric_limits<int32_t>::max(),
+              "B * T must fit int32");
+}
+
+void check_clampw_side(const Tensor& r, const Tensor& s, const Tensor& sa) {
+  const int64_t B = r.size(0), T = r.size(1), H = r.size(2), D = r.size(3);
+  check_device_contiguous(s, "s");
+  check_device_contiguous(sa, "sa");
+  TORCH_CHECK(s.device() == r.device() && sa.device() == r.device(),
+              "s and sa must be on the same device as r");
+  TORCH_CHECK(s.scalar_type() == at::kFloat && s.dim() == 5 && s.size(0) == B &&
+                  s.size(1) == H && s.size(2) == T / 16 && s.size(3) == D && s.size(4) == D,
+              "s must have shape [B,H,T/16,D,D] float32");
+  TORCH_CHECK(sa.scalar_type() == at::kFloat && sa.sizes() == r.sizes(),
+              "sa must have shape [B,T,H,D] float32");
+}
+
+void clampw_forward(Tensor r, Tensor w, Tensor k, Tensor v, Tensor a, Tensor b, Tensor y,
+                    Tensor s, Tensor sa, int64_t head_size) {
+  check_clampw_tokens({{&r, "r"}, {&w, "w"}, {&k, "k"}, {&v, "v"}, {&a, "a"}, {&b, "b"},
+                       {&y, "y"}}, head_size);
+  check_clampw_side(r, s, sa);
+  c10::DeviceGuard guard(r.device());
+  check_rc(frwkv_pretrain_forward(
+      io_code(r.scalar_type()), FRWKV_DECAY_LOGITS, static_cast<int32_t>(r.size(0)),
+      static_cast<int32_t>(r.size(1)), static_cast<int32_t>(r.size(2)),
+      static_cast<int32_t>(head_size), r.data_ptr(), w.data_ptr(), k.data_ptr(), v.data_ptr(),
+      a.data_ptr(), b.data_ptr(), y.data_ptr(), s.data_ptr<float>(), sa.data_ptr<float>(),
+      current_stream(r)));
+}
+
+void clampw_backward(Tensor r, Tensor w, Tensor k, Tensor v, Tensor a, Tensor b, Tensor dy,
+                     Tensor s, Tensor sa, Tensor dr, Tensor dw, Tensor dk, Tensor dv, Tensor da,
+                     Tensor db, int64_t head_size) {
+  check_clampw_tokens({{&r, "r"}, {&w, "w"}, {&k, "k"}, {&v, "v"}, {&a, "a"}, {&b, "b"},
+                       {&dy, "dy"}, {&dr, "dr"}, {&dw, "dw"}, {&dk, "dk"}, {&dv, "dv"},
+                       {&da, "da"}, {&db, "db"}}, head_size);
+  check_clampw_side(r, s, sa);
+  c10::DeviceGuard guard(r.device());
+  check_rc(frwkv_pretrain_backward(
+      io_code(r.scalar_type()), FRWKV_DECAY_LOGITS, static_cast<int32_t>(r.size(0)),
+      static_cast<int32_t>(r.size(1)), static_cast<int32_t>(r.size(2)),
+      static_cast<int32_t>(head_size), r.data_ptr(), w.data_ptr(), k.data_ptr(), v.data_ptr(),
+      a.data_ptr(), b.data_ptr(), dy.data_ptr(), s.data_ptr<float>(), dr.data_ptr(),
+      dw.data_ptr(), dk.data_ptr(), dv.data_ptr(), da.data_ptr(), db.data_ptr(),
+      current_stream(r)));
+}
+
 }  // namespace
 
 TORCH_LIBRARY(flashrwkv_amd, m) {
@@ -728,4 +805,17 @@ TORCH_LIBRARY(flashrwkv_amd, m) {
       "Tensor(e!) grad_a, Tensor(f!) grad_b, Tensor(g!) grad_initial_state, float scale, "
       "int decay_mode) -> ()",
       &statetune_backward_internal);
+}
+
+// The reference's pretraining operator namespace (pretrain_recurrent_bf16_forward.cpp:50-53).
+TORCH_LIBRARY(rwkv7_clampw_v3, m) {
+  m.def(
+      "forward(Tensor r, Tensor w, Tensor k, Tensor v, Tensor a, Tensor b, Tensor(a!) y, "
+      "Tensor(b!) s, Tensor(c!) sa, int head_size) -> ()",
+      &clampw_forward);
+  m.def(
+      "backward(Tensor r, Tensor w, Tensor k, Tensor v, Tensor a, Tensor b, Tensor dy, "
+      "Tensor s, Tensor sa, Tensor(a!) dr, Tensor(b!) dw, Tensor(c!) dk, Tensor(d!) dv, "
+      "Tensor(e!) da, Tensor(f!) db, int head_size) -> ()",
+      &clampw_backward);
 }

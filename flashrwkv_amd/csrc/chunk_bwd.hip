@@ -113,8 +113,14 @@ struct ChunkBwdParams {
   void* dv;
   void* da;
   void* db;
-  float* dstate0;
+  float* dstate0;               // or null (not needed)
   float scale;
+  // Dense layout: > 0 means every sequence has dense_t tokens and is walked
+  // in 64-token chunks, with no segment arrays.
+  int32_t dense_t;
+  // 1: checkpoint is [B, H, dense_t / 16, D, D] (the state every 16
+  // tokens); chunk c of a sequence starts at entry 4c.
+  int32_t ckpt16;
 };
 
 __device__ __forceinline__ const uint16_t* ftri(const BwdSmem& sm, int m, int p, int q) {
@@ -430,8 +436,9 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
   const int heads = p.num_heads;
   const int seq = blockIdx.x / heads;
   const int head = blockIdx.x % heads;
-  const int seg_lo = uniform(max(p.seg_offsets[seq], 0));
-  const int seg_hi = uniform(min(p.seg_offsets[seq + 1], p.num_segments));
+  const int seg_lo = p.dense_t > 0 ? 0 : uniform(max(p.seg_offsets[seq], 0));
+  const int seg_hi = p.dense_t > 0 ? (p.dense_t + kChunk - 1) / kChunk
+                                   : uniform(min(p.seg_offsets[seq + 1], p.num_segments));
 
   float bias[8];
 #pragma unroll
@@ -473,6 +480,11 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
   int cache_base = seg_hi;
   int starts_v = 0, ends_v = 0;
   auto seg_bounds = [&](int seg, int& tb, int& te) {
+    if (p.dense_t > 0) {
+      tb = seq * p.dense_t + kChunk * seg;
+      te = min(tb + kChunk, (seq + 1) * p.dense_t);
+      return;
+    }
     if (seg < cache_base) {
       cache_base = uniform(max(seg - 63, seg_lo));
       const int idx = cache_base + lane;
@@ -515,9 +527,10 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
       rows.dy[s] = ld(dy_rs, tile_off, 0);
       rows.v[s] = ld(v_rs, tile_off, 0);
     }
-    const auto ck = buffer_rsrc(
-        p.checkpoint + (static_cast<int64_t>(seg) * heads + head) * kHead * kHead,
-        kHead * kHead * 4);
+    const int64_t ck_index =
+        p.ckpt16 ? (static_cast<int64_t>(seq) * heads + head) * (p.dense_t / 16) + 4 * seg
+                 : static_cast<int64_t>(seg) * heads + head;
+    const auto ck = buffer_rsrc(p.checkpoint + ck_index * kHead * kHead, kHead * kHead * 4);
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
@@ -1019,7 +1032,7 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
   }
 
   // Gradient of the initial state.
-  {
+  if (p.dstate0 != nullptr) {
     const auto rs0 = buffer_rsrc(p.dstate0 + unit_state, kHead * kHead * 4);
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
@@ -1107,6 +1120,64 @@ extern "C" int frwkv_statetune_backward(
   p.dstate0 = grad_initial_state;
   p.scale = scale;
   const int units = num_sequences * num_heads;
+  auto s = static_cast<hipStream_t>(stream);
+  switch (io_dtype) {
+    case FRWKV_DTYPE_BF16:
+      return dispatch_bwd_decay<Bf16>(p, decay_mode, units, s);
+    case FRWKV_DTYPE_F16:
+      return dispatch_bwd_decay<F16>(p, decay_mode, units, s);
+    default:
+      return set_error(FRWKV_ERR_UNSUPPORTED,
+                       "chunked kernels take float16 or bfloat16 tokens (io dtype %d)", io_dtype);
+  }
+}
+
+extern "C" int frwkv_pretrain_backward(int io_dtype, int decay_mode, int32_t batch,
+                                       int32_t tokens, int32_t num_heads, int32_t head_size,
+                                       const void* r, const void* decay, const void* k,
+                                       const void* v, const void* a, const void* b,
+                                       const void* grad_output, const float* boundary,
+                                       void* grad_r, void* grad_decay, void* grad_k,
+                                       void* grad_v, void* grad_a, void* grad_b, void* stream) {
+  using namespace frwkv;
+  if (!boundary || !r || !decay || !k || !v || !a || !b || !grad_output || !grad_r ||
+      !grad_decay || !grad_k || !grad_v || !grad_a || !grad_b) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT,
+                     "frwkv_pretrain_backward: null pointer argument");
+  }
+  if (head_size != 64) {
+    return set_error(FRWKV_ERR_UNSUPPORTED, "chunked kernels support head size 64, got %d",
+                     head_size);
+  }
+  if (batch <= 0 || tokens <= 0 || num_heads <= 0 || tokens % 16 != 0) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT,
+                     "frwkv_pretrain_backward: B, H > 0 and T a positive multiple of 16 "
+                     "(B=%d, T=%d, H=%d)", batch, tokens, num_heads);
+  }
+  if (static_cast<int64_t>(batch) * tokens > INT32_MAX) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT, "frwkv_pretrain_backward: B * T too large");
+  }
+  ChunkBwdParams p{};
+  p.num_heads = num_heads;
+  p.total_tokens = batch * tokens;
+  p.dense_t = tokens;
+  p.ckpt16 = 1;
+  p.checkpoint = boundary;
+  p.r = r;
+  p.decay = decay;
+  p.k = k;
+  p.v = v;
+  p.a = a;
+  p.b = b;
+  p.dy = grad_output;
+  p.dr = grad_r;
+  p.ddecay = grad_decay;
+  p.dk = grad_k;
+  p.dv = grad_v;
+  p.da = grad_a;
+  p.db = grad_b;
+  p.scale = 1.0f;
+  const int units = batch * num_heads;
   auto s = static_cast<hipStream_t>(stream);
   switch (io_dtype) {
     case FRWKV_DTYPE_BF16:

@@ -65,6 +65,7 @@ struct ChunkSmem {
   };
   uint16_t tinv[4][kTriBlock];  // (I - Lab_pp)^{-1}, [t][i]
   float gc[kHead];              // 2^GC per key feature
+  float gsub[3][kHead];         // 2^G at tokens 15, 31, 47 (16-token boundaries)
 };
 static_assert(sizeof(ChunkSmem) <= 80 * 1024, "two workgroups per CU need <= 80 KB of LDS");
 
@@ -96,6 +97,11 @@ struct ChunkFwdParams {
   float* state_dot_a;           // per-token a^T S_{t-1}, or null
   float scale;
   int64_t out_elems;
+  // Dense layout: > 0 means every sequence has dense_t tokens (sequence s
+  // covers tokens s * dense_t ..), with no cu_seqlens or segment arrays.
+  int32_t dense_t;
+  // 1: boundary is [B, H, dense_t / 16, D, D], the state every 16 tokens.
+  int32_t boundary16;
 };
 
 // Token rows of one chunk held by a thread: r, w, k, a, b for 2 tokens x 8
@@ -269,6 +275,11 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
 #pragma unroll
     for (int e = 0; e < 8; ++e) sm.gc[8 * kg + e] = gcv[e];
   }
+  if (wave < 3 && tp == 7) {
+    // Token t0 + 1 = 16 wave + 15 ends a 16-token block.
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sm.gsub[wave][8 * kg + e] = fast_exp2(g1[e]);
+  }
   __syncthreads();
   return spans;
 }
@@ -387,10 +398,14 @@ __device__ void intra_chunk(ChunkSmem& sm) {
 // out_rs / sda_rs cover the chunk's rows of the output and of state_dot_a
 // (row t at byte t * row_bytes, resp. 2 * t * row_bytes); sda_rs is unused
 // when with_sda is false.
+// sub_rs / nsub: the first nsub (at most 3) 16-token boundary states of the
+// chunk (after tokens 15, 31, 47) go to sub_rs, one [D][D] fp32 block each;
+// nsub is 0 except for whole-chunk passes of the every-16-tokens layout.
 template <typename T>
 __device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const uint16_t* vtile,
                            __amdgpu_buffer_rsrc_t out_rs, __amdgpu_buffer_rsrc_t sda_rs,
-                           bool with_sda, uint32_t row_bytes, float scale, int lo, int hi) {
+                           bool with_sda, uint32_t row_bytes, float scale, int lo, int hi,
+                           __amdgpu_buffer_rsrc_t sub_rs, int nsub) {
   const int tid = threadIdx.x;
   const int w = tid >> 6;
   const int lane = tid & 63;
@@ -484,30 +499,61 @@ __device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const uint16_t* v
                lds_operand_tr<kOpStride>(tile, c + 16, 16 * kb, g, n));
   };
   f32x4 y[4], sn[4];
+  if (nsub > 0) {
+    // The state update in 16-token steps: after block q the accumulator
+    // holds S0 + sum_{t < 16(q+1)} (Bh_t^T SA_t + Kh_t^T V_t), which scaled
+    // by 2^G(16q + 15) is the state after that block.
+    const uint32_t b_off = static_cast<uint32_t>((4 * g) * kHead + 16 * w + n) * 4;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) sn[kb] = S[kb];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        sn[kb] = mfma32(lo32(lds_operand_tr<kOpStride>(sm.bh, 16 * q, 16 * kb, g, n)),
+                        lo32(sab[q]), sn[kb]);
+        sn[kb] = mfma32(lo32(lds_operand_tr<kOpStride>(sm.kh, 16 * q, 16 * kb, g, n)),
+                        lo32(vs[q]), sn[kb]);
+      }
+      if (q < 3 && q < nsub) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float x = sn[kb][j] * sm.gsub[q][16 * kb + 4 * g + j];
+            __builtin_amdgcn_raw_buffer_store_b32(
+                __float_as_uint(x), sub_rs, b_off,
+                static_cast<int>((q * kHead * kHead + (16 * kb + j) * kHead) * 4), 0);
+          }
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) sn[kb] = mfma32(tr32(sm.bh, kb, 0), sa01, S[kb]);
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) sn[kb] = mfma32(tr32(sm.bh, kb, 32), sa23, sn[kb]);
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) sn[kb] = mfma32(tr32(sm.kh, kb, 0), v01, sn[kb]);
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) sn[kb] = mfma32(tr32(sm.kh, kb, 32), v23, sn[kb]);
+  }
 #pragma unroll
   for (int pb = 0; pb < 4; ++pb) {
     y[pb] = mfma32(s01, lds_operand32<kOpStride>(sm.rt, 16 * pb + n, 0, g), zero4());
   }
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) sn[kb] = mfma32(tr32(sm.bh, kb, 0), sa01, S[kb]);
-#pragma unroll
   for (int pb = 0; pb < 4; ++pb) {
     y[pb] = mfma32(s23, lds_operand32<kOpStride>(sm.rt, 16 * pb + n, 32, g), y[pb]);
   }
-#pragma unroll
-  for (int kb = 0; kb < 4; ++kb) sn[kb] = mfma32(tr32(sm.bh, kb, 32), sa23, sn[kb]);
   y[0] = mfma32(lo32(sab[0]), lo32(tri16(kArb, 0, 0)), y[0]);
   y[1] = mfma32(sa01, tri32(kArb, 1, 0), y[1]);
   y[2] = mfma32(sa01, tri32(kArb, 2, 0), y[2]);
   y[3] = mfma32(sa01, tri32(kArb, 3, 0), y[3]);
-#pragma unroll
-  for (int kb = 0; kb < 4; ++kb) sn[kb] = mfma32(tr32(sm.kh, kb, 0), v01, sn[kb]);
   y[0] = mfma32(lo32(vs[0]), lo32(tri16(kArk, 0, 0)), y[0]);
   y[1] = mfma32(v01, tri32(kArk, 1, 0), y[1]);
   y[2] = mfma32(v01, tri32(kArk, 2, 0), y[2]);
   y[3] = mfma32(v01, tri32(kArk, 3, 0), y[3]);
-#pragma unroll
-  for (int kb = 0; kb < 4; ++kb) sn[kb] = mfma32(tr32(sm.kh, kb, 32), v23, sn[kb]);
   y[2] = mfma32(lo32(sab[2]), lo32(tri16(kArb, 2, 2)), y[2]);
   y[3] = mfma32(sa23, tri32(kArb, 3, 2), y[3]);
   y[2] = mfma32(lo32(vs[2]), lo32(tri16(kArk, 2, 2)), y[2]);
@@ -580,15 +626,20 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
   constexpr int kPoolBytes = static_cast<int>(sizeof(PS));
   const int64_t sbase = (static_cast<int64_t>(slot) * heads + head) * kHead * kHead;
   const auto state_rs =
-      buffer_rsrc(static_cast<PS*>(p.state) + sbase, kHead * kHead * kPoolBytes);
+      p.state != nullptr
+          ? buffer_rsrc(static_cast<PS*>(p.state) + sbase, kHead * kHead * kPoolBytes)
+          : buffer_rsrc(static_cast<PS*>(nullptr), 0u);
   const uint32_t s_off = static_cast<uint32_t>((4 * g) * kHead + 16 * wave + n) * kPoolBytes;
+  // A null state means S0 = 0 and no final state (the pretraining layout).
   f32x4 S[4];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int so = (16 * kb + j) * kHead * kPoolBytes;
-      if constexpr (kPoolBytes == 4) {
+      if (p.state == nullptr) {
+        S[kb][j] = 0.0f;
+      } else if constexpr (kPoolBytes == 4) {
         S[kb][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(state_rs, s_off, so, 0));
       } else {
         S[kb][j] = to_f32<PoolT>(__builtin_amdgcn_raw_buffer_load_b16(state_rs, s_off, so, 0));
@@ -613,6 +664,9 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
       }
       t_begin = __builtin_amdgcn_readlane(starts_v, seg - cache_base);
       t_end = __builtin_amdgcn_readlane(ends_v, seg - cache_base);
+    } else if (p.dense_t > 0) {
+      t_begin = seq * p.dense_t;
+      t_end = t_begin + p.dense_t;
     } else {
       t_begin = p.cu_seqlens[seq];
       t_end = p.cu_seqlens[seq + 1];
@@ -672,7 +726,7 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
   for (int seg = seg_lo; seg < seg_hi; ++seg) {
     int t_begin, t_end;
     seg_range(seg, t_begin, t_end);
-    if (p.boundary != nullptr) {
+    if (p.boundary != nullptr && !p.boundary16) {
       const auto brs = buffer_rsrc(
           p.boundary + (static_cast<int64_t>(seg) * heads + head) * kHead * kHead,
           kHead * kHead * 4);
@@ -690,6 +744,28 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
       const int ntok = min(kChunk, t_end - c0);
       int nseg = seg, nc0 = c0, nend = t_end;
       const bool has_next = next_chunk(nseg, nc0, nend);
+      // Every-16-tokens boundary layout [B, H, dense_t / 16, D, D]: the state
+      // at token c0 + i (i a multiple of 16) of this sequence.
+      const int64_t b16_base = (static_cast<int64_t>(seq) * heads + head) * (p.dense_t / 16) +
+                               (c0 - t_begin) / 16;
+      auto b16_rs = [&](int i, int count) {
+        if (!p.boundary16 || count <= 0) return buffer_rsrc(static_cast<float*>(nullptr), 0u);
+        return buffer_rsrc(p.boundary + (b16_base + i / 16) * kHead * kHead,
+                           static_cast<uint32_t>(count) * kHead * kHead * 4);
+      };
+      auto store_b16 = [&](int i) {
+        const auto brs = b16_rs(i, 1);
+        const uint32_t b_off = static_cast<uint32_t>((4 * g) * kHead + 16 * wave + n) * 4;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(S[kb][j]), brs, b_off,
+                                                  (16 * kb + j) * kHead * 4, 0);
+          }
+        }
+      };
+      if (p.boundary16) store_b16(0);
       // One pass over [lo, hi) per iteration. The first pass prepares the
       // whole chunk; if its decay span is above the limit (strong decay), the
       // chunk is redone as 16-token sub-chunks, or 4-token ones where a
@@ -719,10 +795,12 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
           const auto sda_rs = buffer_rsrc(
               p.state_dot_a != nullptr ? p.state_dot_a + base : nullptr,
               p.state_dot_a != nullptr ? 2u * static_cast<uint32_t>(ntok) * row_bytes : 0u);
+          const int nsub = (p.boundary16 && whole) ? (ntok - 1) / 16 : 0;
           state_pass<T>(sm, S, sm.vt, out_rs, sda_rs, p.state_dot_a != nullptr, row_bytes,
-                        p.scale, lo, hi);
+                        p.scale, lo, hi, b16_rs(16, nsub), nsub);
         }
         if (whole) break;
+        if (p.boundary16 && hi % 16 == 0 && hi < ntok) store_b16(hi);
         lo = hi;
         if (lo >= ntok) break;
         const int q = lo >> 4;
@@ -732,6 +810,7 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
     }
   }
 
+  if (p.state == nullptr) return;
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
@@ -895,5 +974,50 @@ extern "C" int frwkv_statetune_forward(
   p.scale = scale;
   p.out_elems = static_cast<int64_t>(total_tokens) * num_heads * head_size;
   return dispatch_chunk_io<float>(p, io_dtype, decay_mode, num_sequences * num_heads,
+                                  static_cast<hipStream_t>(stream));
+}
+
+extern "C" int frwkv_pretrain_forward(int io_dtype, int decay_mode, int32_t batch,
+                                      int32_t tokens, int32_t num_heads, int32_t head_size,
+                                      const void* r, const void* decay, const void* k,
+                                      const void* v, const void* a, const void* b,
+                                      void* output, float* boundary, float* state_dot_a,
+                                      void* stream) {
+  using namespace frwkv;
+  if (!boundary || !state_dot_a) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT, "frwkv_pretrain_forward: null pointer argument");
+  }
+  int rc = check_token_pointers(r, decay, k, v, a, b, output);
+  if (rc != FRWKV_OK) return rc;
+  if (head_size != 64) {
+    return set_error(FRWKV_ERR_UNSUPPORTED, "chunked kernels support head size 64, got %d",
+                     head_size);
+  }
+  if (batch <= 0 || tokens <= 0 || num_heads <= 0 || tokens % 16 != 0) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT,
+                     "frwkv_pretrain_forward: B, H > 0 and T a positive multiple of 16 "
+                     "(B=%d, T=%d, H=%d)", batch, tokens, num_heads);
+  }
+  if (static_cast<int64_t>(batch) * tokens > INT32_MAX) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT, "frwkv_pretrain_forward: B * T too large");
+  }
+  ChunkFwdParams p{};
+  p.num_heads = num_heads;
+  p.total_tokens = batch * tokens;
+  p.state_slots = batch;
+  p.dense_t = tokens;
+  p.boundary16 = 1;
+  p.r = r;
+  p.decay = decay;
+  p.k = k;
+  p.v = v;
+  p.a = a;
+  p.b = b;
+  p.out = output;
+  p.boundary = boundary;
+  p.state_dot_a = state_dot_a;
+  p.scale = 1.0f;
+  p.out_elems = static_cast<int64_t>(batch) * tokens * num_heads * head_size;
+  return dispatch_chunk_io<float>(p, io_dtype, decay_mode, batch * num_heads,
                                   static_cast<hipStream_t>(stream));
 }

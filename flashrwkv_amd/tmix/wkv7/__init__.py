@@ -191,7 +191,9 @@ __all__ = [
     "prepare_recurrent_metadata",
 ]
 
-# Reference ``tmix/wkv7/__init__.py:350-354`` re-exports the chunk entry here.
+# Reference ``tmix/wkv7/__init__.py:350-354`` re-exports the pretraining and
+# chunk entries here.
+from .pretrain import pretrain_recurrent_bf16  # noqa: E402
 from .chunk import infer_chunk_bf16_forward_varlen  # noqa: E402
 
-__all__.append("infer_chunk_bf16_forward_varlen")
+__all__.extend(["pretrain_recurrent_bf16", "infer_chunk_bf16_forward_varlen"])

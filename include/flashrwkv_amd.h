@@ -189,6 +189,37 @@ int frwkv_statetune_backward(int io_dtype, int decay_mode, int32_t num_sequences
                              float* grad_initial_state, float scale,
                              void* stream);
 
+/*
+ * Pretraining forward (clampw v3): dense tokens [B,T,H,D] (token t of
+ * sequence s at row s*T + t), S0 = 0, no final state. boundary
+ * [B,H,T/16,D,D] fp32 receives the state every 16 tokens (entry i: the state
+ * before token 16 i); state_dot_a [B,T,H,D] fp32 receives a_t^T S_{t-1}.
+ * T must be a multiple of 16; head_size 64.
+ * Replaces rwkv7_clampw_v3::forward / cuda_forward_v3
+ * (csrc/sm90/tmix/wkv7/pretrain_recurrent_bf16_forward.cpp:20-26, 50-53;
+ * kernel pretrain_recurrent_bf16_forward.cu).
+ */
+int frwkv_pretrain_forward(int io_dtype, int decay_mode, int32_t batch, int32_t tokens,
+                           int32_t num_heads, int32_t head_size, const void* r,
+                           const void* decay, const void* k, const void* v,
+                           const void* a, const void* b, void* output, float* boundary,
+                           float* state_dot_a, void* stream);
+
+/*
+ * Pretraining backward: recomputes every 64-token chunk from the boundary
+ * written by frwkv_pretrain_forward (every 4th entry) and writes the six
+ * token gradients (grad_decay is dL/d(decay input)). grad_output may not be
+ * NULL. Replaces rwkv7_clampw_v3::backward / cuda_backward_v3
+ * (csrc/sm90/tmix/wkv7/pretrain_recurrent_bf16_forward.cpp:31-53).
+ */
+int frwkv_pretrain_backward(int io_dtype, int decay_mode, int32_t batch, int32_t tokens,
+                            int32_t num_heads, int32_t head_size, const void* r,
+                            const void* decay, const void* k, const void* v,
+                            const void* a, const void* b, const void* grad_output,
+                            const float* boundary, void* grad_r, void* grad_decay,
+                            void* grad_k, void* grad_v, void* grad_a, void* grad_b,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif
