@@ -113,3 +113,21 @@ def statetune_backward_internal(sequence_chunk_offsets, chunk_token_starts, chun
         sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, r, decay, k, v, a, b,
         grad_output, grad_final_state, boundary, grad_r, grad_decay, grad_k, grad_v, grad_a,
         grad_b, grad_initial_state, float(scale), int(decay_mode))
+
+
+def rl_infctx_chunk_fp32io16_forward(sequence_chunk_offsets, chunk_token_starts,
+                                     chunk_token_ends, state, r, decay_logits, k, v, a, b,
+                                     strategy=1, scale=1.0, decay_bias=None):
+    """Reference rl_infctx_chunk_fp32io16_forward.cpp:168-245: returns (output, working_state)."""
+    return ops.rl_infctx_chunk_fp32io16_forward(
+        sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, state, r, decay_logits,
+        k, v, a, b, int(strategy), float(scale), decay_bias)
+
+
+def rl_infctx_chunk_fp32io16_backward_replay(chunk_token_starts, chunk_token_ends, boundary, r,
+                                             decay_logits, k, v, a, b, output, state_dot_a,
+                                             scale=1.0, decay_bias=None):
+    """Reference rl_infctx_chunk_fp32io16_backward.cpp:108-140."""
+    ops.rl_infctx_chunk_fp32io16_backward_replay(
+        chunk_token_starts, chunk_token_ends, boundary, r, decay_logits, k, v, a, b, output,
+        state_dot_a, float(scale), decay_bias)

@@ -33,6 +33,7 @@ SIGNATURES = {
     "frwkv_statetune_backward": [_INT] * 2 + [_I32] * 5 + [_VP] * 20 + [_F32, _VP],
     "frwkv_pretrain_forward": [_INT] * 2 + [_I32] * 4 + [_VP] * 10,
     "frwkv_pretrain_backward": [_INT] * 2 + [_I32] * 4 + [_VP] * 15,
+    "frwkv_chunk_replay": [_INT] * 2 + [_I32] * 4 + [_VP] * 12 + [_F32, _VP],
 }
 
 _LIB = None
@@ -144,3 +145,14 @@ def pretrain_backward(r, decay, k, v, a, b, *, grad_output, boundary, grads,
     _check(library().frwkv_pretrain_backward(
         DTYPE[r.dtype], decay_mode, bsz, t_len, h, d, _p(r), _p(decay), _p(k), _p(v), _p(a),
         _p(b), _p(grad_output), _p(boundary), *(_p(g) for g in grads), _stream()))
+
+
+def chunk_replay(r, decay, k, v, a, b, *, chunk_token_starts, chunk_token_ends, boundary,
+                 output, state_dot_a, scale=1.0, decay_mode=DECAY_LOGITS, decay_bias=None):
+    """RL/infctx replay stage: every chunk from its boundary state."""
+    n, h, d = r.shape
+    _check(library().frwkv_chunk_replay(
+        DTYPE[r.dtype], decay_mode, chunk_token_starts.numel(), h, d, n,
+        _p(chunk_token_starts), _p(chunk_token_ends), _p(boundary), _p(r), _p(decay),
+        _p(decay_bias), _p(k), _p(v), _p(a), _p(b), _p(output), _p(state_dot_a),
+        float(scale), _stream()))

@@ -727,6 +727,154 @@ void clampw_backward(Tensor r, Tensor w, Tensor k, Tensor v, Tensor a, Tensor b,
       current_stream(r)));
 }
 
+// ---------------------------------------------------------------------------
+// RL/infctx chunk family: reference
+// csrc/sm90/rl_infctx/wkv7/rl_infctx_chunk_fp32io16_forward.cpp:70-233 and
+// rl_infctx_chunk_fp32io16_backward.cpp:20-128. The forward's result does not
+// depend on the caller's chunking or strategy (both are validated): head size
+// 64 runs the chunked kernel, 128 and 256 the fp32 per-token kernel, on a
+// working copy of the state.
+
+// Host check of the chunk metadata (one small device-to-host copy, as in the
+// reference); returns the per-sequence token offsets [B+1].
+std::vector<int32_t> check_rl_chunk_metadata(const Tensor& offsets, const Tensor& starts,
+                                             const Tensor& ends, int64_t num_sequences,
+                                             int64_t total_tokens, const Tensor& state) {
+  const std::pair<const Tensor*, const char*> all[] = {
+      {&offsets, "sequence_chunk_offsets"},
+      {&starts, "chunk_token_starts"},
+      {&ends, "chunk_token_ends"}};
+  for (const auto& item : all) {
+    check_device_contiguous(*item.first, item.second);
+    TORCH_CHECK(item.first->device() == state.device(), item.second,
+                " must be on the same device as state");
+    TORCH_CHECK(item.first->scalar_type() == at::kInt, item.second, " must be int32");
+  }
+  TORCH_CHECK(offsets.dim() == 1 && offsets.numel() == num_sequences + 1,
+              "sequence_chunk_offsets must have shape [B+1]");
+  TORCH_CHECK(starts.dim() == 1 && starts.numel() > 0 && starts.sizes() == ends.sizes(),
+              "chunk token metadata must have matching shape [C]");
+  TORCH_CHECK(starts.numel() * state.size(1) <= std::numeric_limits<int>::max(),
+              "chunk/head grid must fit in int32");
+  const Tensor seq_cpu = offsets.to(at::kCPU).contiguous();
+  const Tensor starts_cpu = starts.to(at::kCPU).contiguous();
+  const Tensor ends_cpu = ends.to(at::kCPU).contiguous();
+  const int32_t* seq = seq_cpu.data_ptr<int32_t>();
+  const int32_t* st = starts_cpu.data_ptr<int32_t>();
+  const int32_t* en = ends_cpu.data_ptr<int32_t>();
+  const int64_t chunks = starts.numel();
+  TORCH_CHECK(seq[0] == 0 && seq[num_sequences] == chunks,
+              "sequence_chunk_offsets must cover all chunks");
+  std::vector<int32_t> cu(num_sequences + 1, 0);
+  int32_t previous_end = 0;
+  for (int64_t s = 0; s < num_sequences; ++s) {
+    const int32_t c0 = seq[s], c1 = seq[s + 1];
+    TORCH_CHECK(c0 >= 0 && c1 > c0 && c1 <= chunks,
+                "each sequence must own at least one ordered chunk");
+    TORCH_CHECK(st[c0] == previous_end, "chunks must cover packed tokens without gaps");
+    for (int32_t c = c0; c < c1; ++c) {
+      TORCH_CHECK(st[c] >= 0 && en[c] > st[c] && en[c] <= total_tokens &&
+                      (c == c0 || st[c] == en[c - 1]),
+                  "chunk token ranges must be contiguous and non-empty");
+    }
+    cu[s] = st[c0];
+    previous_end = en[c1 - 1];
+  }
+  TORCH_CHECK(previous_end == total_tokens, "chunks must cover exactly all packed tokens");
+  cu[num_sequences] = previous_end;
+  return cu;
+}
+
+std::tuple<Tensor, Tensor> rl_infctx_forward(Tensor offsets, Tensor starts, Tensor ends,
+                                             Tensor state, Tensor r, Tensor decay_logits,
+                                             Tensor k, Tensor v, Tensor a, Tensor b,
+                                             int64_t strategy, double scale,
+                                             std::optional<Tensor> decay_bias) {
+  TORCH_CHECK(strategy == 0 || strategy == 1,
+              "strategy must be 0 (materialized) or 1 (recompute)");
+  TORCH_CHECK(state.is_cuda() && state.is_contiguous() && state.scalar_type() == at::kFloat,
+              "RL/Infctx state must be contiguous CUDA float32");
+  TORCH_CHECK(state.dim() == 4 && state.size(0) > 0 && state.size(1) > 0 &&
+                  state.size(2) == state.size(3) &&
+                  (state.size(2) == 64 || state.size(2) == 128 || state.size(2) == 256),
+              "RL/Infctx state must have shape [B,H,D,D], D in {64,128,256}");
+  const int64_t batch = state.size(0);
+  TORCH_CHECK(r.dim() == 3, "RL/Infctx token tensors must have shape [N,H,D]");
+  const std::vector<int32_t> cu_host =
+      check_rl_chunk_metadata(offsets, starts, ends, batch, r.size(0), state);
+  c10::DeviceGuard guard(state.device());
+  Tensor working = state.clone();
+  Tensor output = at::empty_like(v);
+  const Tensor cu = at::tensor(cu_host, at::TensorOptions().dtype(at::kInt)).to(state.device());
+  const Tensor slots = at::arange(batch, at::TensorOptions().dtype(at::kInt).device(state.device()));
+  if (state.size(2) == 64) {
+    check_chunk_tokens(r, decay_logits, k, v, a, b, /*bf16_only=*/false);
+    chunk_impl(r, decay_logits, k, v, a, b, working, cu, slots, scale, decay_bias,
+               FRWKV_DECAY_LOGITS, output);
+  } else {
+    int64_t max_len = 0;
+    for (int64_t s = 0; s < batch; ++s) max_len = std::max<int64_t>(max_len, cu_host[s + 1] - cu_host[s]);
+    recurrent_impl(cu, slots, working, r, decay_logits, k, v, a, b, output, scale, decay_bias,
+                   std::nullopt, max_len, FRWKV_DECAY_LOGITS, /*allow_fp32_tokens=*/false);
+  }
+  return {output, working};
+}
+
+void rl_infctx_replay(Tensor starts, Tensor ends, Tensor boundary, Tensor r, Tensor decay_logits,
+                      Tensor k, Tensor v, Tensor a, Tensor b, Tensor output, Tensor state_dot_a,
+                      double scale, std::optional<Tensor> decay_bias) {
+  for (const auto* t : {&boundary, &r, &decay_logits, &k, &v, &a, &b, &output, &state_dot_a,
+                        &starts, &ends}) {
+    check_device_contiguous(*t, "replay tensors");
+  }
+  TORCH_CHECK(std::isfinite(scale), "scale must be finite");
+  TORCH_CHECK(starts.scalar_type() == at::kInt && ends.scalar_type() == at::kInt,
+              "chunk token metadata must be int32");
+  TORCH_CHECK(starts.dim() == 1 && starts.numel() > 0 && starts.sizes() == ends.sizes(),
+              "chunk token metadata must have shape [C]");
+  TORCH_CHECK(r.dim() == 3 && r.size(0) > 0 &&
+                  (r.size(2) == 64 || r.size(2) == 128 || r.size(2) == 256),
+              "replay token tensors must have shape [N,H,D], D in {64,128,256}");
+  TORCH_CHECK(boundary.dim() == 4 && boundary.size(0) == starts.numel() &&
+                  boundary.size(1) == r.size(1) && boundary.size(2) == r.size(2) &&
+                  boundary.size(3) == r.size(2) && boundary.scalar_type() == at::kFloat,
+              "boundary must have shape [C,H,D,D] and be float32");
+  const std::pair<const Tensor*, const char*> toks[] = {
+      {&decay_logits, "decay_logits"}, {&k, "k"}, {&v, "v"}, {&a, "a"}, {&b, "b"},
+      {&output, "output"}};
+  for (const auto& item : toks) {
+    TORCH_CHECK(item.first->sizes() == r.sizes(), item.second, " must match r shape");
+    TORCH_CHECK(item.first->scalar_type() == r.scalar_type(), item.second, " must match r dtype");
+    TORCH_CHECK(item.first->device() == r.device(), item.second,
+                " must be on the same device as r");
+  }
+  TORCH_CHECK(r.scalar_type() == at::kHalf || r.scalar_type() == at::kBFloat16,
+              "replay token tensors must be float16 or bfloat16");
+  TORCH_CHECK(state_dot_a.sizes() == r.sizes() && state_dot_a.scalar_type() == at::kFloat,
+              "state_dot_a must match r shape and be float32");
+  for (const auto* t : {&starts, &ends, &boundary, &state_dot_a}) {
+    TORCH_CHECK(t->device() == r.device(), "replay metadata/workspace must be on the same device as r");
+  }
+  if (decay_bias.has_value()) {
+    check_device_contiguous(*decay_bias, "decay_bias");
+    TORCH_CHECK(decay_bias->device() == r.device(), "decay_bias must be on the same device as r");
+    TORCH_CHECK(decay_bias->scalar_type() == r.scalar_type(), "decay_bias must match r dtype");
+    TORCH_CHECK((decay_bias->dim() == 1 && decay_bias->numel() == r.size(1) * r.size(2)) ||
+                    (decay_bias->dim() == 2 && decay_bias->size(0) == r.size(1) &&
+                     decay_bias->size(1) == r.size(2)),
+                "decay_bias must have shape [H*D] or [H,D]");
+  }
+  c10::DeviceGuard guard(r.device());
+  check_rc(frwkv_chunk_replay(
+      io_code(r.scalar_type()), FRWKV_DECAY_LOGITS, static_cast<int32_t>(starts.numel()),
+      static_cast<int32_t>(r.size(1)), static_cast<int32_t>(r.size(2)),
+      static_cast<int32_t>(r.size(0)), starts.data_ptr<int32_t>(), ends.data_ptr<int32_t>(),
+      boundary.data_ptr<float>(), r.data_ptr(), decay_logits.data_ptr(),
+      decay_bias.has_value() ? decay_bias->data_ptr() : nullptr, k.data_ptr(), v.data_ptr(),
+      a.data_ptr(), b.data_ptr(), output.data_ptr(), state_dot_a.data_ptr<float>(),
+      static_cast<float>(scale), current_stream(r)));
+}
+
 }  // namespace
 
 TORCH_LIBRARY(flashrwkv_amd, m) {
@@ -805,6 +953,18 @@ TORCH_LIBRARY(flashrwkv_amd, m) {
       "Tensor(e!) grad_a, Tensor(f!) grad_b, Tensor(g!) grad_initial_state, float scale, "
       "int decay_mode) -> ()",
       &statetune_backward_internal);
+  m.def(
+      "rl_infctx_chunk_fp32io16_forward(Tensor sequence_chunk_offsets, Tensor chunk_token_starts, "
+      "Tensor chunk_token_ends, Tensor state, Tensor r, Tensor decay_logits, Tensor k, "
+      "Tensor v, Tensor a, Tensor b, int strategy=1, float scale=1.0, "
+      "Tensor? decay_bias=None) -> (Tensor, Tensor)",
+      &rl_infctx_forward);
+  m.def(
+      "rl_infctx_chunk_fp32io16_backward_replay(Tensor chunk_token_starts, "
+      "Tensor chunk_token_ends, Tensor boundary, Tensor r, Tensor decay_logits, Tensor k, "
+      "Tensor v, Tensor a, Tensor b, Tensor(a!) output, Tensor(b!) state_dot_a, "
+      "float scale=1.0, Tensor? decay_bias=None) -> ()",
+      &rl_infctx_replay);
 }
 
 // The reference's pretraining operator namespace (pretrain_recurrent_bf16_forward.cpp:50-53).

@@ -17,3 +17,13 @@ int set_error(int status, const char* fmt, ...);
 int check_launch(const char* what);
 
 }  // namespace frwkv
+
+// The replay stage on the per-token kernel (recurrent.hip), used by
+// frwkv_chunk_replay for head sizes other than 64. Arguments as there.
+int frwkv_replay_recurrent(int io_dtype, int decay_mode, int32_t num_chunks, int32_t num_heads,
+                           int32_t head_size, int32_t total_tokens,
+                           const int32_t* chunk_token_starts, const int32_t* chunk_token_ends,
+                           const float* boundary, const void* r, const void* decay,
+                           const void* decay_bias, const void* k, const void* v,
+                           const void* a, const void* b, void* output, float* state_dot_a,
+                           float scale, void* stream);

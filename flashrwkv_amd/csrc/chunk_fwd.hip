@@ -102,6 +102,9 @@ struct ChunkFwdParams {
   int32_t dense_t;
   // 1: boundary is [B, H, dense_t / 16, D, D], the state every 16 tokens.
   int32_t boundary16;
+  // 1: the initial states are read and never written back (replay from
+  // stored boundaries).
+  int32_t read_only_state;
 };
 
 // Token rows of one chunk held by a thread: r, w, k, a, b for 2 tokens x 8
@@ -605,10 +608,16 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
   const int slot = uniform(p.slots != nullptr ? p.slots[seq] : seq);
   if (slot < 0 || slot >= p.state_slots) return;
 
+  // Segments: the lists of seg_offsets, or (seg_offsets null, seg_starts
+  // given) exactly one segment per sequence, segment s for sequence s.
+  const bool segmented = p.seg_starts != nullptr;
   int seg_lo = 0, seg_hi = 1;
   if (p.seg_offsets != nullptr) {
     seg_lo = uniform(max(p.seg_offsets[seq], 0));
     seg_hi = uniform(min(p.seg_offsets[seq + 1], p.num_segments));
+  } else if (segmented) {
+    seg_lo = seq;
+    seg_hi = min(seq + 1, p.num_segments);
   }
 
   float bias[8];
@@ -654,7 +663,7 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
   int cache_base = seg_hi;
   int starts_v = 0, ends_v = 0;
   auto seg_range = [&](int seg, int& t_begin, int& t_end) {
-    if (p.seg_offsets != nullptr) {
+    if (segmented) {
       if (seg < cache_base || seg >= cache_base + 64) {
         cache_base = seg;
         const int idx = seg + lane;
@@ -810,7 +819,7 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
     }
   }
 
-  if (p.state == nullptr) return;
+  if (p.state == nullptr || p.read_only_state) return;
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
@@ -1019,5 +1028,56 @@ extern "C" int frwkv_pretrain_forward(int io_dtype, int decay_mode, int32_t batc
   p.scale = 1.0f;
   p.out_elems = static_cast<int64_t>(batch) * tokens * num_heads * head_size;
   return dispatch_chunk_io<float>(p, io_dtype, decay_mode, batch * num_heads,
+                                  static_cast<hipStream_t>(stream));
+}
+
+extern "C" int frwkv_chunk_replay(int io_dtype, int decay_mode, int32_t num_chunks,
+                                  int32_t num_heads, int32_t head_size, int32_t total_tokens,
+                                  const int32_t* chunk_token_starts,
+                                  const int32_t* chunk_token_ends, const float* boundary,
+                                  const void* r, const void* decay, const void* decay_bias,
+                                  const void* k, const void* v, const void* a, const void* b,
+                                  void* output, float* state_dot_a, float scale,
+                                  void* stream) {
+  using namespace frwkv;
+  if (!chunk_token_starts || !chunk_token_ends || !boundary || !state_dot_a) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT, "frwkv_chunk_replay: null pointer argument");
+  }
+  int rc = check_token_pointers(r, decay, k, v, a, b, output);
+  if (rc != FRWKV_OK) return rc;
+  if (num_chunks <= 0 || num_heads <= 0 || total_tokens <= 0) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT, "frwkv_chunk_replay: sizes must be positive");
+  }
+  if (!__builtin_isfinite(scale)) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT, "scale must be finite");
+  }
+  if (head_size != 64) {
+    // Other head sizes: the fp32 per-token kernel, one unit per chunk.
+    return frwkv_replay_recurrent(io_dtype, decay_mode, num_chunks, num_heads, head_size,
+                                  total_tokens, chunk_token_starts, chunk_token_ends,
+                                  boundary, r, decay, decay_bias, k, v, a, b, output,
+                                  state_dot_a, scale, stream);
+  }
+  ChunkFwdParams p{};
+  p.num_heads = num_heads;
+  p.total_tokens = total_tokens;
+  p.state_slots = num_chunks;
+  p.seg_starts = chunk_token_starts;
+  p.seg_ends = chunk_token_ends;
+  p.num_segments = num_chunks;
+  p.state = const_cast<float*>(boundary);
+  p.read_only_state = 1;
+  p.r = r;
+  p.decay = decay;
+  p.bias = decay_bias;
+  p.k = k;
+  p.v = v;
+  p.a = a;
+  p.b = b;
+  p.out = output;
+  p.state_dot_a = state_dot_a;
+  p.scale = scale;
+  p.out_elems = static_cast<int64_t>(total_tokens) * num_heads * head_size;
+  return dispatch_chunk_io<float>(p, io_dtype, decay_mode, num_chunks * num_heads,
                                   static_cast<hipStream_t>(stream));
 }

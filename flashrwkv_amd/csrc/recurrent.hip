@@ -39,12 +39,28 @@ __device__ __forceinline__ float reduce_row_groups(float x) {
   return x;
 }
 
+// Unit ranges: sequence s covers tokens cu_seqlens[s] .. cu_seqlens[s+1]-1,
+// or cu_seqlens[s] .. seg_ends[s]-1 when seg_ends is given (independent
+// chunks, the replay stage). state_dot_a (optional) receives a_t^T S_{t-1};
+// read_only_state keeps the pool unwritten (the replay stage starts from
+// stored boundaries); status may be null (no metadata word to check).
+struct RecurrentKernelParams {
+  int32_t num_heads, num_units;
+  int64_t output_elements;
+  int32_t total_tokens, state_pool_size;
+  const int32_t* cu_seqlens;
+  const int32_t* seg_ends;
+  const int32_t* slots;
+  const int32_t* status;
+  float* state;
+  float* state_dot_a;
+  int32_t read_only_state;
+  float scale;
+};
+
 template <int D, int CW, int WG, typename T, DecayMode M>
 __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
-    int32_t num_heads, int32_t num_units, int64_t output_elements,
-    int32_t total_tokens, int32_t state_pool_size,
-    const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ slots,
-    const int32_t* __restrict__ status, float* __restrict__ state,
+    RecurrentKernelParams p,
     const typename IoTraits<T>::storage* __restrict__ r_ptr,
     const typename IoTraits<T>::storage* __restrict__ decay_ptr,
     const typename IoTraits<T>::storage* __restrict__ bias_ptr,
@@ -52,21 +68,24 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
     const typename IoTraits<T>::storage* __restrict__ v_ptr,
     const typename IoTraits<T>::storage* __restrict__ a_ptr,
     const typename IoTraits<T>::storage* __restrict__ b_ptr,
-    typename IoTraits<T>::storage* __restrict__ out_ptr, float scale) {
+    typename IoTraits<T>::storage* __restrict__ out_ptr) {
+  const int32_t num_heads = p.num_heads;
+  const int32_t total_tokens = p.total_tokens;
+  const float scale = p.scale;
   constexpr int kWavesPerUnit = D / CW;
   constexpr int kCg = CW / 4;       // lanes per row group (float4 columns)
   constexpr int kNg = 64 / kCg;     // row groups per wave
   constexpr int kRpl = D / kNg;     // key rows per lane
   static_assert(kRpl % 4 == 0, "lane rows load in 4-element pieces");
 
-  if (status[0] != 0) {
-    fill_nan<T>(out_ptr, output_elements);
+  if (p.status != nullptr && p.status[0] != 0) {
+    fill_nan<T>(out_ptr, p.output_elements);
     return;
   }
   const int lane = threadIdx.x & 63;
   const int wave = blockIdx.x * (WG / 64) + (threadIdx.x >> 6);
   const int unit = wave / kWavesPerUnit;
-  if (unit >= num_units) return;
+  if (unit >= p.num_units) return;
   const int slab = wave % kWavesPerUnit;
   const int seq = unit / num_heads;
   const int head = unit % num_heads;
@@ -77,17 +96,18 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
 
   // One wave handles one sequence, so its bounds and slot are wave-uniform;
   // readfirstlane makes the token loop's branches scalar.
-  const int32_t t_begin = __builtin_amdgcn_readfirstlane(cu_seqlens[seq]);
-  const int32_t t_end = __builtin_amdgcn_readfirstlane(cu_seqlens[seq + 1]);
-  const int32_t slot = __builtin_amdgcn_readfirstlane(slots[seq]);
+  const int32_t t_begin = __builtin_amdgcn_readfirstlane(p.cu_seqlens[seq]);
+  const int32_t t_end = __builtin_amdgcn_readfirstlane(
+      p.seg_ends != nullptr ? p.seg_ends[seq] : p.cu_seqlens[seq + 1]);
+  const int32_t slot = __builtin_amdgcn_readfirstlane(p.slots != nullptr ? p.slots[seq] : seq);
   // Validated metadata never fails these; they keep a bad direct launch from
   // touching memory outside the tensors.
   if (t_begin < 0 || t_end > total_tokens || t_begin >= t_end || slot < 0 ||
-      slot >= state_pool_size) {
+      slot >= p.state_pool_size) {
     return;
   }
 
-  float* sbase = state + ((static_cast<int64_t>(slot) * num_heads + head) * D) * D;
+  float* sbase = p.state + ((static_cast<int64_t>(slot) * num_heads + head) * D) * D;
   float4 s[kRpl];
 #pragma unroll
   for (int j = 0; j < kRpl; ++j) {
@@ -163,6 +183,10 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
       sa.y = reduce_row_groups<kNg>(sa.y);
       sa.z = reduce_row_groups<kNg>(sa.z);
       sa.w = reduce_row_groups<kNg>(sa.w);
+      if (p.state_dot_a != nullptr && rg == 0) {
+        *reinterpret_cast<float4*>(
+            p.state_dot_a + (static_cast<int64_t>(t) * num_heads + head) * D + col) = sa;
+      }
 
       float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
@@ -189,6 +213,7 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
     }
   }
 
+  if (p.read_only_state) return;
 #pragma unroll
   for (int j = 0; j < kRpl; ++j) {
     store_f4_stream(sbase + static_cast<int64_t>(row0 + j) * D + col, s[j]);
@@ -206,6 +231,9 @@ struct RecurrentArgs {
   void* out;
   float scale;
   hipStream_t stream;
+  const int32_t* seg_ends = nullptr;
+  float* state_dot_a = nullptr;
+  int32_t read_only_state = 0;
 };
 
 template <int D, int CW, int WG, typename T, DecayMode M>
@@ -215,14 +243,26 @@ int launch_recurrent(const RecurrentArgs& p) {
   const int64_t waves = static_cast<int64_t>(units) * (D / CW);
   const int blocks = static_cast<int>((waves + WG / 64 - 1) / (WG / 64));
   const int64_t out_elems = static_cast<int64_t>(p.total_tokens) * p.num_heads * D;
+  RecurrentKernelParams kp{};
+  kp.num_heads = p.num_heads;
+  kp.num_units = units;
+  kp.output_elements = out_elems;
+  kp.total_tokens = p.total_tokens;
+  kp.state_pool_size = p.state_pool_size;
+  kp.cu_seqlens = p.cu;
+  kp.seg_ends = p.seg_ends;
+  kp.slots = p.slots;
+  kp.status = p.status;
+  kp.state = p.state;
+  kp.state_dot_a = p.state_dot_a;
+  kp.read_only_state = p.read_only_state;
+  kp.scale = p.scale;
   hipLaunchKernelGGL((recurrent_fp32_kernel<D, CW, WG, T, M>), dim3(blocks),
-                     dim3(WG), 0, p.stream, p.num_heads, units, out_elems,
-                     p.total_tokens, p.state_pool_size, p.cu, p.slots, p.status,
-                     p.state, static_cast<const S*>(p.r),
+                     dim3(WG), 0, p.stream, kp, static_cast<const S*>(p.r),
                      static_cast<const S*>(p.decay), static_cast<const S*>(p.bias),
                      static_cast<const S*>(p.k), static_cast<const S*>(p.v),
                      static_cast<const S*>(p.a), static_cast<const S*>(p.b),
-                     static_cast<S*>(p.out), p.scale);
+                     static_cast<S*>(p.out));
   return check_launch("recurrent_fp32_kernel");
 }
 
@@ -300,5 +340,34 @@ extern "C" int frwkv_recurrent_forward(
       return dispatch_decay<float>(p, decay_mode);
     default:
       return set_error(FRWKV_ERR_INVALID_ARGUMENT, "unknown io dtype %d", io_dtype);
+  }
+}
+
+// Replay stage for head sizes other than 64 (called by frwkv_chunk_replay):
+// unit c runs tokens chunk_token_starts[c] .. chunk_token_ends[c]-1 from
+// boundary[c], which stays unwritten, and writes output and a^T S_{t-1}.
+int frwkv_replay_recurrent(int io_dtype, int decay_mode, int32_t num_chunks, int32_t num_heads,
+                           int32_t head_size, int32_t total_tokens,
+                           const int32_t* chunk_token_starts, const int32_t* chunk_token_ends,
+                           const float* boundary, const void* r, const void* decay,
+                           const void* decay_bias, const void* k, const void* v,
+                           const void* a, const void* b, void* output, float* state_dot_a,
+                           float scale, void* stream) {
+  using namespace frwkv;
+  RecurrentArgs p{num_chunks, num_heads, head_size, total_tokens, /*max_seqlen=*/-1,
+                  num_chunks, chunk_token_starts, /*slots=*/nullptr, /*status=*/nullptr,
+                  const_cast<float*>(boundary), r, decay, decay_bias, k, v, a, b, output,
+                  scale, static_cast<hipStream_t>(stream)};
+  p.seg_ends = chunk_token_ends;
+  p.state_dot_a = state_dot_a;
+  p.read_only_state = 1;
+  switch (io_dtype) {
+    case FRWKV_DTYPE_BF16:
+      return dispatch_decay<Bf16>(p, decay_mode);
+    case FRWKV_DTYPE_F16:
+      return dispatch_decay<F16>(p, decay_mode);
+    default:
+      return set_error(FRWKV_ERR_UNSUPPORTED,
+                       "replay takes float16 or bfloat16 tokens (io dtype %d)", io_dtype);
   }
 }

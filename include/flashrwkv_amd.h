@@ -220,6 +220,27 @@ int frwkv_pretrain_backward(int io_dtype, int decay_mode, int32_t batch, int32_t
                             void* grad_k, void* grad_v, void* grad_a, void* grad_b,
                             void* stream);
 
+/*
+ * Replay stage of the RL/infctx chunk family: chunk c runs tokens
+ * chunk_token_starts[c] .. chunk_token_ends[c]-1 starting from boundary[c]
+ * ([num_chunks,H,D,D] fp32, read only) and writes output [total_tokens,H,D]
+ * (io dtype) and state_dot_a [total_tokens,H,D] fp32 (a_t^T S_{t-1}) for
+ * those tokens. head_size 64 runs the chunked bf16-MFMA kernel, 128 and 256
+ * the fp32 per-token kernel. decay_bias NULL or [H*D] (logits mode only).
+ * Replaces rl_infctx_chunk_fp32io16_backward_replay
+ * (csrc/sm90/rl_infctx/wkv7/rl_infctx_chunk_fp32io16_backward.cpp:108-128).
+ * The RL/infctx forward (rl_infctx_chunk_fp32io16_forward.cpp:168-233) needs
+ * no entry of its own: it is frwkv_chunk_forward (head size 64) or
+ * frwkv_recurrent_forward (128, 256) on a working copy of the gathered pool.
+ */
+int frwkv_chunk_replay(int io_dtype, int decay_mode, int32_t num_chunks, int32_t num_heads,
+                       int32_t head_size, int32_t total_tokens,
+                       const int32_t* chunk_token_starts, const int32_t* chunk_token_ends,
+                       const float* boundary, const void* r, const void* decay,
+                       const void* decay_bias, const void* k, const void* v, const void* a,
+                       const void* b, void* output, float* state_dot_a, float scale,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif
