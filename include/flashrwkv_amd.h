@@ -228,8 +228,8 @@ int frwkv_pretrain_backward(int io_dtype, int decay_mode, int32_t batch, int32_t
  * those tokens. head_size 64 runs the chunked bf16-MFMA kernel, 128 and 256
  * the fp32 per-token kernel. decay_bias NULL or [H*D] (logits mode only).
  * Replaces rl_infctx_chunk_fp32io16_backward_replay
- * (csrc/sm90/rl_infctx/wkv7/rl_infctx_chunk_fp32io16_backward.cpp:108-128).
- * The RL/infctx forward (rl_infctx_chunk_fp32io16_forward.cpp:168-233) needs
+ * (csrc/sm90/rl_infctx/wkv7/rl_infctx_chunk_fp32io16_backward.cpp:102-124).
+ * The RL/infctx forward (rl_infctx_chunk_fp32io16_forward.cpp:157-229) needs
  * no entry of its own: it is frwkv_chunk_forward (head size 64) or
  * frwkv_recurrent_forward (128, 256) on a working copy of the gathered pool.
  */
