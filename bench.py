@@ -52,6 +52,7 @@ PMC_KIB = {  # kernel -> (FETCH_SIZE, WRITE_SIZE)
     "chunk_fwd_kernel<Bf16,kRawW,float>": (790724.0, 270338.2),
     "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": (790893.0, 1318970.7),
     "chunk_bwd_kernel<Bf16,kRawW>": (1730522.7, 2159326.8),
+    "recurrent_fp32_kernel<64,64,64,F16,kLogits,kFp16>": (44898.3, 83200.2),
 }
 
 
@@ -69,8 +70,8 @@ def _parse():
     p.add_argument("--steps", type=int, default=1000)
     p.add_argument("--warmup", type=int, default=50)
     p.add_argument("--workload", default="all",
-                   choices=("all", "decode", "prefill", "training", "recurrent_long",
-                            "copy"),
+                   choices=("all", "decode", "decode_fp16", "prefill", "training",
+                            "recurrent_long", "copy"),
                    help="all: decode headline line plus the prefill, training and "
                         "long-sequence legs")
     p.add_argument("--prefill-steps", type=int, default=20)
@@ -80,13 +81,14 @@ def _parse():
     return p.parse_args()
 
 
-def decode_bytes_per_step(batch: int, heads: int, d: int = 64, io_bytes: int = 2) -> int:
+def decode_bytes_per_step(batch: int, heads: int, d: int = 64, io_bytes: int = 2,
+                          state_bytes: int = 4) -> int:
     """Algorithmic HBM bytes of one decode launch.
 
-    Per (sequence, head): state read + write 2*D*D*4 B, six token rows
+    Per (sequence, head): state read + write 2*D*D*state_bytes, six token rows
     (r, w, k, v, a, b) 6*D*io_bytes, one output row D*io_bytes.
     """
-    per_unit = 2 * d * d * 4 + 7 * d * io_bytes
+    per_unit = 2 * d * d * state_bytes + 7 * d * io_bytes
     return batch * heads * per_unit
 
 
@@ -193,7 +195,9 @@ def cpu_baseline_gate(cores):
     return gate
 
 
-def bench_decode(args):
+def bench_decode(args, fp16_state=False):
+    """Config 1 decode. ``fp16_state``: the fp16-state family instead (fp16
+    tokens with decay logits, fp16 pool, phase origins), same shape."""
     import torch
 
     import flashrwkv_amd
@@ -205,15 +209,25 @@ def bench_decode(args):
     ops = flashrwkv_amd._C.ops
     dev = torch.device("cuda:0")
     batch, heads, d = 256, 40, 64
-    n_pools, n_tokens = 4, 8
+    # Enough replicas that the rotation (>= 671 MB) exceeds the 256 MB cache.
+    n_pools, n_tokens = (8, 8) if fp16_state else (4, 8)
+    state_dtype = torch.float16 if fp16_state else torch.float32
+    io_dtype = torch.float16 if fp16_state else torch.bfloat16
 
     gen = torch.Generator(device=dev).manual_seed(20260805)
-    pools = [torch.randn((batch, heads, d, d), generator=gen, device=dev) * 0.1
-             for _ in range(n_pools)]
-    token_sets = [workloads.make_tokens(batch, heads, d, dtype=torch.bfloat16,
+    pools = [(torch.randn((batch, heads, d, d), generator=gen, device=dev) * 0.1)
+             .to(state_dtype) for _ in range(n_pools)]
+    token_sets = [workloads.make_tokens(batch, heads, d, dtype=io_dtype,
                                        seed=20260805 + i, device=dev)
                   for i in range(n_tokens)]
-    outputs = [torch.empty((batch, heads, d), device=dev, dtype=torch.bfloat16)
+    if fp16_state:
+        # Decay logits (the family's only decay form), reference test scale.
+        # k scaled down so that 1000+ in-place steps stay inside fp16 range.
+        for t in token_sets:
+            t["w"] = (torch.randn((batch, heads, d), generator=gen, device=dev) * 3.5).half()
+            t["k"] = (t["k"].float() * 0.05).half()
+    elapsed = torch.arange(batch, device=dev, dtype=torch.int32) * 11
+    outputs = [torch.empty((batch, heads, d), device=dev, dtype=io_dtype)
                for _ in range(n_tokens)]
     cu = torch.arange(batch + 1, device=dev, dtype=torch.int32)
     slots = torch.arange(batch, device=dev, dtype=torch.int32)
@@ -225,10 +239,15 @@ def bench_decode(args):
 
         def step(i, pool=None):
             t = token_sets[i % n_tokens]
-            ops.recurrent_fp32_forward_internal(
-                cu, slots, pools[i % n_pools] if pool is None else pool,
-                t["r"], t["w"], t["k"], t["v"], t["a"], t["b"],
-                outputs[i % n_tokens], 1.0, DECAY_RAW_W, None, ticket, 1)
+            target = pools[i % n_pools] if pool is None else pool
+            if fp16_state:
+                ops.recurrent_fp16_from_decay_logits(
+                    cu, slots, elapsed, target, t["r"], t["w"], t["k"], t["v"], t["a"],
+                    t["b"], outputs[i % n_tokens], 1.0, None, ticket, 1)
+            else:
+                ops.recurrent_fp32_forward_internal(
+                    cu, slots, target, t["r"], t["w"], t["k"], t["v"], t["a"], t["b"],
+                    outputs[i % n_tokens], 1.0, DECAY_RAW_W, None, ticket, 1)
 
         for i in range(8):
             step(i)
@@ -262,15 +281,35 @@ def bench_decode(args):
             torch.cuda.synchronize()
             return start.elapsed_time(end) / args.steps, time.perf_counter() - wall0
 
-        # Cache-cold: step i uses pool replica i % 4 and token set i % 8.
+        # Cache-cold: step i uses pool replica i % n_pools and token set i % 8.
         cold_ms, wall = timed(capture(range(cycle)), [capture([i]) for i in range(cycle)])
         # In-place: one pool, the literal "consecutive steps" of the config.
         inplace_ms, _ = timed(capture(range(cycle), pools[0]),
                               [capture([i], pools[0]) for i in range(cycle)])
 
-    nbytes = decode_bytes_per_step(batch, heads, d)
+    nbytes = decode_bytes_per_step(batch, heads, d, state_bytes=2 if fp16_state else 4)
     achieved = nbytes / (cold_ms * 1e-3) / 1e9
     tok_s = batch / (cold_ms * 1e-3)
+    if fp16_state:
+        kernel = "recurrent_fp32_kernel<64,64,64,F16,kLogits,kFp16>"
+        return {
+            "workload": f"wkv7_decode_fp16_state: B=256, H=40, D=64, T=1 per step, fp16 io, "
+                        f"fp16 state pool in place, decay logits, {n_pools} rotating pool "
+                        "replicas (cache-cold)",
+            "ms_per_step": round(cold_ms, 6),
+            "tokens_per_s": round(tok_s, 1),
+            "roofline": {
+                "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                "traffic": pmc_traffic(kernel) if kernel in PMC_KIB else None,
+                "kernel": kernel, "algorithmic_bytes_per_launch": nbytes,
+            },
+            "inplace_single_pool": {
+                "ms_per_step": round(inplace_ms, 6),
+                "tokens_per_s": round(batch / (inplace_ms * 1e-3), 1),
+                "achieved_GBps": round(nbytes / (inplace_ms * 1e-3) / 1e9, 1),
+            },
+        }
     line = {
         "metric": METRIC,
         "value": round(tok_s, 1),
@@ -699,9 +738,12 @@ def main():
         line = {"metric": METRIC, "copy": bench_copy(args)}
     elif args.workload == "recurrent_long":
         line = {"metric": METRIC, "recurrent_long": bench_recurrent_long(args)}
+    elif args.workload == "decode_fp16":
+        line = {"metric": METRIC, "decode_fp16_state": bench_decode(args, fp16_state=True)}
     else:
         line = bench_decode(args)
         if args.workload == "all":
+            line["decode_fp16_state"] = bench_decode(args, fp16_state=True)
             line["chunked_prefill"] = bench_prefill(args)
             line["chunked_prefill"]["varlen"] = bench_prefill_varlen(args)
             line["training"] = bench_training(args)

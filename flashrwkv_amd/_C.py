@@ -118,7 +118,7 @@ def statetune_backward_internal(sequence_chunk_offsets, chunk_token_starts, chun
 def rl_infctx_chunk_fp32io16_forward(sequence_chunk_offsets, chunk_token_starts,
                                      chunk_token_ends, state, r, decay_logits, k, v, a, b,
                                      strategy=1, scale=1.0, decay_bias=None):
-    """Reference rl_infctx_chunk_fp32io16_forward.cpp:168-245: returns (output, working_state)."""
+    """Reference rl_infctx_chunk_fp32io16_forward.cpp:157-241: returns (output, working_state)."""
     return ops.rl_infctx_chunk_fp32io16_forward(
         sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, state, r, decay_logits,
         k, v, a, b, int(strategy), float(scale), decay_bias)
@@ -127,7 +127,33 @@ def rl_infctx_chunk_fp32io16_forward(sequence_chunk_offsets, chunk_token_starts,
 def rl_infctx_chunk_fp32io16_backward_replay(chunk_token_starts, chunk_token_ends, boundary, r,
                                              decay_logits, k, v, a, b, output, state_dot_a,
                                              scale=1.0, decay_bias=None):
-    """Reference rl_infctx_chunk_fp32io16_backward.cpp:108-140."""
+    """Reference rl_infctx_chunk_fp32io16_backward.cpp:102-135."""
     ops.rl_infctx_chunk_fp32io16_backward_replay(
         chunk_token_starts, chunk_token_ends, boundary, r, decay_logits, k, v, a, b, output,
         state_dot_a, float(scale), decay_bias)
+
+
+def recurrent_fp16_from_decay_logits(query_start_loc, state_indices, elapsed_state_pool, state,
+                                     r, decay_logits, k, v, a, b, output, scale,
+                                     decay_bias=None, validated_metadata=None, max_seqlen=-1):
+    """Reference infer_recurrent_fp16_forward_varlen.cpp:210-270, 289-301."""
+    ops.recurrent_fp16_from_decay_logits(
+        query_start_loc, state_indices, elapsed_state_pool, state, r, decay_logits, k, v, a,
+        b, output, float(scale), decay_bias, validated_metadata, int(max_seqlen))
+
+
+def recurrent_fp16_advance_i32(elapsed_state, amount):
+    """Reference infer_recurrent_fp16_forward_varlen.cpp:129-135."""
+    ops.recurrent_fp16_advance_i32(elapsed_state, int(amount))
+
+
+def recurrent_fp16_advance_i32_varlen(query_start_loc, state_indices, elapsed_state_pool,
+                                      total_tokens, validated_metadata=None):
+    """Reference infer_recurrent_fp16_forward_varlen.cpp:137-191."""
+    ops.recurrent_fp16_advance_i32_varlen(query_start_loc, state_indices, elapsed_state_pool,
+                                          int(total_tokens), validated_metadata)
+
+
+def recurrent_add_vec_forward_varlen(x, vec):
+    """Reference infer_recurrent_fp16_forward_varlen.cpp:193-208."""
+    return ops.recurrent_add_vec_forward_varlen(x, vec)

@@ -15,6 +15,10 @@ except ImportError:
 
 from .tmix.wkv7 import (
     infer_chunk_bf16_forward_varlen,
+    infer_recurrent_add_vec_forward_varlen,
+    infer_recurrent_fp16_advance_i32,
+    infer_recurrent_fp16_advance_i32_varlen,
+    infer_recurrent_fp16_forward_varlen,
     infer_recurrent_fp32io16_forward_varlen,
     prepare_recurrent_metadata,
     pretrain_recurrent_bf16,
@@ -23,6 +27,10 @@ from .tmix.wkv7.statetune import statetune_recurrent_fp32io16
 
 __all__ = [
     "infer_chunk_bf16_forward_varlen",
+    "infer_recurrent_add_vec_forward_varlen",
+    "infer_recurrent_fp16_advance_i32",
+    "infer_recurrent_fp16_advance_i32_varlen",
+    "infer_recurrent_fp16_forward_varlen",
     "infer_recurrent_fp32io16_forward_varlen",
     "prepare_recurrent_metadata",
     "pretrain_recurrent_bf16",

@@ -19,7 +19,8 @@ LIBRARY = Path(__file__).resolve().parent / "libflashrwkv_amd.so"
 DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 DECAY_LOGITS, DECAY_RAW_W = 0, 1
 
-_INT, _I32, _F32, _VP = ctypes.c_int, ctypes.c_int32, ctypes.c_float, ctypes.c_void_p
+_INT, _I32, _I64 = ctypes.c_int, ctypes.c_int32, ctypes.c_int64
+_F32, _VP = ctypes.c_float, ctypes.c_void_p
 
 # name -> argtypes, in the header's parameter order.
 SIGNATURES = {
@@ -34,6 +35,10 @@ SIGNATURES = {
     "frwkv_pretrain_forward": [_INT] * 2 + [_I32] * 4 + [_VP] * 10,
     "frwkv_pretrain_backward": [_INT] * 2 + [_I32] * 4 + [_VP] * 15,
     "frwkv_chunk_replay": [_INT] * 2 + [_I32] * 4 + [_VP] * 12 + [_F32, _VP],
+    "frwkv_recurrent_fp16_forward": [_I32] * 6 + [_VP] * 13 + [_F32, _VP],
+    "frwkv_advance_i32": [_VP, _I64, _I32, _VP],
+    "frwkv_advance_i32_varlen": [_I32] * 2 + [_VP] * 5,
+    "frwkv_add_vec": [_I64, _I32] + [_VP] * 4,
 }
 
 _LIB = None
@@ -156,3 +161,31 @@ def chunk_replay(r, decay, k, v, a, b, *, chunk_token_starts, chunk_token_ends, 
         _p(chunk_token_starts), _p(chunk_token_ends), _p(boundary), _p(r), _p(decay),
         _p(decay_bias), _p(k), _p(v), _p(a), _p(b), _p(output), _p(state_dot_a),
         float(scale), _stream()))
+
+
+def recurrent_fp16_forward(r, decay_logits, k, v, a, b, *, state_pool, elapsed_state_pool,
+                           cu_seqlens, state_indices, metadata_status, output, scale=1.0,
+                           decay_bias=None, max_seqlen=-1):
+    """fp16-state family: fp16 tokens and pool, int32 phase origins (read only)."""
+    n, h, d = r.shape
+    _check(library().frwkv_recurrent_fp16_forward(
+        state_indices.numel(), h, d, n, int(max_seqlen), state_pool.shape[0], _p(cu_seqlens),
+        _p(state_indices), _p(metadata_status), _p(elapsed_state_pool), _p(state_pool), _p(r),
+        _p(decay_logits), _p(decay_bias), _p(k), _p(v), _p(a), _p(b), _p(output),
+        float(scale), _stream()))
+
+
+def advance_i32(elapsed_state, amount):
+    _check(library().frwkv_advance_i32(_p(elapsed_state), elapsed_state.numel(), int(amount),
+                                       _stream()))
+
+
+def advance_i32_varlen(elapsed_state_pool, *, cu_seqlens, state_indices, metadata_status):
+    _check(library().frwkv_advance_i32_varlen(
+        state_indices.numel(), elapsed_state_pool.numel(), _p(cu_seqlens), _p(state_indices),
+        _p(metadata_status), _p(elapsed_state_pool), _stream()))
+
+
+def add_vec(x, vec, output):
+    rows, channels = x.shape
+    _check(library().frwkv_add_vec(rows, channels, _p(x), _p(vec), _p(output), _stream()))

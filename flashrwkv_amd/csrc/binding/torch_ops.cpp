@@ -875,6 +875,169 @@ void rl_infctx_replay(Tensor starts, Tensor ends, Tensor boundary, Tensor r, Ten
       static_cast<float>(scale), current_stream(r)));
 }
 
+// ------------------------------------------------------- fp16 state ---
+
+// Layout checks of the fp16-state op: the rules and messages of the reference's
+// check_fp16_recurrent_layout (infer_recurrent_fp16_forward_varlen.cpp:50-125).
+void check_fp16_layout(const Tensor& cu, const Tensor& slots, const Tensor& elapsed,
+                       const Tensor& state, const Tensor& r, const Tensor& decay,
+                       const Tensor& k, const Tensor& v, const Tensor& a, const Tensor& b,
+                       const Tensor& output, double scale) {
+  const std::pair<const Tensor*, const char*> all[] = {
+      {&cu, "query_start_loc"}, {&slots, "state_indices"},
+      {&elapsed, "elapsed_state_pool"}, {&state, "state"}, {&r, "r"},
+      {&decay, "decay_logits"}, {&k, "k"}, {&v, "v"}, {&a, "a"}, {&b, "b"},
+      {&output, "output"}};
+  for (const auto& item : all) check_device_contiguous(*item.first, item.second);
+  for (const auto& item : all) check_same_device(state, *item.first, item.second);
+  TORCH_CHECK(cu.scalar_type() == at::kInt && slots.scalar_type() == at::kInt &&
+                  elapsed.scalar_type() == at::kInt,
+              "recurrent metadata must be int32");
+  TORCH_CHECK(slots.dim() == 1 && slots.numel() > 0 && cu.dim() == 1 &&
+                  cu.numel() == slots.numel() + 1,
+              "query_start_loc must have shape [B+1] and state_indices shape [B]");
+  TORCH_CHECK(slots.numel() <= 65535, "state_indices must contain at most 65535 sequences");
+  TORCH_CHECK(elapsed.dim() == 1 && state.dim() >= 1 && elapsed.size(0) == state.size(0),
+              "elapsed_state_pool must have shape [state_pool_slots]");
+  TORCH_CHECK(state.dim() == 4 && state.scalar_type() == at::kHalf && state.size(0) > 0 &&
+                  state.size(1) > 0 && state.size(2) == state.size(3),
+              "state must be contiguous float16 [slots,H,D,D]");
+  TORCH_CHECK(state.size(0) <= std::numeric_limits<int32_t>::max(),
+              "state slot count must fit in int32");
+  const int64_t d = state.size(2);
+  TORCH_CHECK(d == 64 || d == 128 || d == 256,
+              "recurrent head size must be 64, 128, or 256, got ", d);
+  TORCH_CHECK(r.dim() == 3 && r.size(0) > 0 && r.size(1) == state.size(1) && r.size(2) == d,
+              "r must have packed shape [total_tokens,H,D] matching state");
+  TORCH_CHECK(r.size(0) <= std::numeric_limits<int32_t>::max(),
+              "token count must fit in int32");
+  TORCH_CHECK(r.sizes() == decay.sizes() && r.sizes() == k.sizes() &&
+                  r.sizes() == v.sizes() && r.sizes() == a.sizes() &&
+                  r.sizes() == b.sizes() && r.sizes() == output.sizes(),
+              "r,decay_logits,k,v,a,b,output shape mismatch");
+  TORCH_CHECK(r.scalar_type() == at::kHalf && decay.scalar_type() == at::kHalf &&
+                  k.scalar_type() == at::kHalf && v.scalar_type() == at::kHalf &&
+                  a.scalar_type() == at::kHalf && b.scalar_type() == at::kHalf &&
+                  output.scalar_type() == at::kHalf,
+              "FP16-state recurrent token tensors must be float16");
+  TORCH_CHECK(std::isfinite(scale), "scale must be finite");
+}
+
+// The reference's recurrent_fp16_from_decay_logits
+// (infer_recurrent_fp16_forward_varlen.cpp:210-270).
+void recurrent_fp16_from_decay_logits(
+    Tensor query_start_loc, Tensor state_indices, Tensor elapsed_state_pool, Tensor state,
+    Tensor r, Tensor decay_logits, Tensor k, Tensor v, Tensor a, Tensor b, Tensor output,
+    double scale, std::optional<Tensor> decay_bias,
+    std::optional<TicketPtr> validated_metadata, int64_t max_seqlen) {
+  check_fp16_layout(query_start_loc, state_indices, elapsed_state_pool, state, r,
+                    decay_logits, k, v, a, b, output, scale);
+  if (decay_bias.has_value()) {
+    check_device_contiguous(*decay_bias, "decay_bias");
+    check_same_device(state, *decay_bias, "decay_bias");
+    const int64_t heads = state.size(1), d = state.size(2);
+    TORCH_CHECK(decay_bias->scalar_type() == at::kHalf &&
+                    ((decay_bias->dim() == 1 && decay_bias->numel() == heads * d) ||
+                     (decay_bias->dim() == 2 && decay_bias->size(0) == heads &&
+                      decay_bias->size(1) == d)),
+                "decay_bias must be float16 with shape [H*D] or [H,D]");
+  }
+  c10::DeviceGuard guard(state.device());
+  Prepared launch;
+  if (validated_metadata.has_value() && validated_metadata->defined()) {
+    (*validated_metadata)
+        ->check_compatible(query_start_loc, state_indices, r.size(0), state.size(0), max_seqlen);
+    launch = (*validated_metadata)->prepared();
+    max_seqlen = (*validated_metadata)->max_seqlen();
+  } else {
+    launch = device_prepare(query_start_loc, state_indices, r.size(0), state.size(0));
+  }
+  check_rc(frwkv_recurrent_fp16_forward(
+      static_cast<int32_t>(state_indices.numel()), static_cast<int32_t>(state.size(1)),
+      static_cast<int32_t>(state.size(2)), static_cast<int32_t>(r.size(0)),
+      static_cast<int32_t>(max_seqlen), static_cast<int32_t>(state.size(0)),
+      launch.cu_snapshot.data_ptr<int32_t>(), launch.slot_snapshot.data_ptr<int32_t>(),
+      launch.status.data_ptr<int32_t>(), elapsed_state_pool.data_ptr<int32_t>(),
+      state.data_ptr(), r.data_ptr(), decay_logits.data_ptr(),
+      decay_bias.has_value() ? decay_bias->data_ptr() : nullptr, k.data_ptr(), v.data_ptr(),
+      a.data_ptr(), b.data_ptr(), output.data_ptr(), static_cast<float>(scale),
+      current_stream(state)));
+}
+
+// The reference's recurrent_fp16_advance_i32 (infer_recurrent_fp16_forward_varlen.cpp:129-135,
+// range check .cu:1218-1219).
+void recurrent_fp16_advance_i32(Tensor elapsed_state, int64_t amount) {
+  check_device_contiguous(elapsed_state, "elapsed state");
+  TORCH_CHECK(elapsed_state.scalar_type() == at::kInt,
+              "elapsed state must be contiguous CUDA int32");
+  TORCH_CHECK(elapsed_state.numel() > 0, "elapsed state must be non-empty");
+  TORCH_CHECK(amount >= std::numeric_limits<int32_t>::min() &&
+                  amount <= std::numeric_limits<int32_t>::max(),
+              "advance_i32 amount out of int range");
+  c10::DeviceGuard guard(elapsed_state.device());
+  check_rc(frwkv_advance_i32(elapsed_state.data_ptr<int32_t>(), elapsed_state.numel(),
+                             static_cast<int32_t>(amount), current_stream(elapsed_state)));
+}
+
+// The reference's recurrent_fp16_advance_i32_varlen
+// (infer_recurrent_fp16_forward_varlen.cpp:137-191).
+void recurrent_fp16_advance_i32_varlen(Tensor query_start_loc, Tensor state_indices,
+                                       Tensor elapsed_state, int64_t total_tokens,
+                                       std::optional<TicketPtr> validated_metadata) {
+  check_device_contiguous(query_start_loc, "query_start_loc");
+  check_device_contiguous(state_indices, "state_indices");
+  check_device_contiguous(elapsed_state, "elapsed_state_pool");
+  check_same_device(elapsed_state, query_start_loc, "query_start_loc");
+  check_same_device(elapsed_state, state_indices, "state_indices");
+  TORCH_CHECK(query_start_loc.scalar_type() == at::kInt &&
+                  state_indices.scalar_type() == at::kInt &&
+                  elapsed_state.scalar_type() == at::kInt,
+              "varlen elapsed metadata must be contiguous CUDA int32");
+  TORCH_CHECK(query_start_loc.dim() == 1 && state_indices.dim() == 1 &&
+                  state_indices.numel() > 0 &&
+                  query_start_loc.numel() == state_indices.numel() + 1,
+              "query_start_loc must have shape [B+1] and state_indices shape [B]");
+  TORCH_CHECK(state_indices.numel() <= 65535,
+              "state_indices must contain at most 65535 sequences");
+  TORCH_CHECK(elapsed_state.dim() == 1 && elapsed_state.size(0) > 0 && total_tokens > 0 &&
+                  total_tokens <= std::numeric_limits<int32_t>::max() &&
+                  elapsed_state.size(0) <= std::numeric_limits<int32_t>::max(),
+              "invalid varlen elapsed state or total_tokens");
+  c10::DeviceGuard guard(elapsed_state.device());
+  Prepared launch;
+  if (validated_metadata.has_value() && validated_metadata->defined()) {
+    (*validated_metadata)
+        ->check_compatible(query_start_loc, state_indices, total_tokens, elapsed_state.size(0),
+                           -1);
+    launch = (*validated_metadata)->prepared();
+  } else {
+    launch = device_prepare(query_start_loc, state_indices, total_tokens, elapsed_state.size(0));
+  }
+  check_rc(frwkv_advance_i32_varlen(
+      static_cast<int32_t>(state_indices.numel()), static_cast<int32_t>(elapsed_state.size(0)),
+      launch.cu_snapshot.data_ptr<int32_t>(), launch.slot_snapshot.data_ptr<int32_t>(),
+      launch.status.data_ptr<int32_t>(), elapsed_state.data_ptr<int32_t>(),
+      current_stream(elapsed_state)));
+}
+
+// The reference's recurrent_add_vec_forward_varlen (infer_recurrent_fp16_forward_varlen.cpp:193-208).
+Tensor recurrent_add_vec_forward_varlen(Tensor x, Tensor vec) {
+  check_device_contiguous(x, "x");
+  check_device_contiguous(vec, "vec");
+  TORCH_CHECK(vec.device() == x.device(), "vec must be on the same device as x");
+  TORCH_CHECK(x.scalar_type() == at::kHalf && vec.scalar_type() == at::kHalf,
+              "x and vec must be float16");
+  TORCH_CHECK(x.dim() == 2 && x.size(0) > 0 && x.size(1) > 0 && x.size(1) % 2 == 0 &&
+                  x.size(1) <= std::numeric_limits<int32_t>::max(),
+              "x must have packed shape [total_tokens,C] with even C");
+  TORCH_CHECK(vec.dim() == 1 && vec.size(0) == x.size(1), "vec must have shape [C]");
+  c10::DeviceGuard guard(x.device());
+  Tensor out = at::empty_like(x);
+  check_rc(frwkv_add_vec(x.size(0), static_cast<int32_t>(x.size(1)), x.data_ptr(),
+                         vec.data_ptr(), out.data_ptr(), current_stream(x)));
+  return out;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(flashrwkv_amd, m) {
@@ -965,6 +1128,24 @@ TORCH_LIBRARY(flashrwkv_amd, m) {
       "Tensor v, Tensor a, Tensor b, Tensor(a!) output, Tensor(b!) state_dot_a, "
       "float scale=1.0, Tensor? decay_bias=None) -> ()",
       &rl_infctx_replay);
+  m.def(
+      "recurrent_fp16_from_decay_logits(Tensor query_start_loc, Tensor state_indices, "
+      "Tensor elapsed_state_pool, Tensor(a!) state, Tensor r, Tensor decay_logits, "
+      "Tensor k, Tensor v, Tensor a, Tensor b, Tensor(b!) output, float scale, "
+      "Tensor? decay_bias=None, "
+      "__torch__.torch.classes.flashrwkv_amd.MetadataTicket? "
+      "validated_metadata=None, int max_seqlen=-1) -> ()",
+      &recurrent_fp16_from_decay_logits);
+  m.def("recurrent_fp16_advance_i32(Tensor(a!) elapsed_state, int amount) -> ()",
+        &recurrent_fp16_advance_i32);
+  m.def(
+      "recurrent_fp16_advance_i32_varlen(Tensor query_start_loc, Tensor state_indices, "
+      "Tensor(a!) elapsed_state_pool, int total_tokens, "
+      "__torch__.torch.classes.flashrwkv_amd.MetadataTicket? "
+      "validated_metadata=None) -> ()",
+      &recurrent_fp16_advance_i32_varlen);
+  m.def("recurrent_add_vec_forward_varlen(Tensor x, Tensor vec) -> Tensor",
+        &recurrent_add_vec_forward_varlen);
 }
 
 // The reference's pretraining operator namespace (pretrain_recurrent_bf16_forward.cpp:50-53).

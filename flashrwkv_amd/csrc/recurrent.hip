@@ -6,6 +6,14 @@
 // out [K,V] and updated in place at state_indices, fail-closed NaN output when
 // the metadata status word is non-zero.
 //
+// The same kernel runs the fp16-state family (reference
+// csrc/sm120/tmix/wkv7/infer_recurrent_fp16_forward_varlen.cu, contract
+// tests/tmix/wkv7/test.py:214-264): the pool holds fp16, the retention enters
+// as delta = fp16(w - 1 + dither(phase)) with phase = elapsed[slot] + h*D +
+// key + token offset, and every token's state S + S*delta + b sa^T + k v^T
+// is rounded to fp16 before the output reads it. Arithmetic between those
+// rounding points is fp32, as in the reference's oracle.
+//
 // MI355X design. The value columns of a state are independent given the token
 // vectors (sa[v], y[v] and S[:,v] only touch column v), so the work unit is a
 // wave owning a slab of CW columns of one (sequence, head) state:
@@ -28,6 +36,62 @@ namespace frwkv {
 namespace {
 
 
+// State pool element type.
+enum class StateKind : int { kFp32 = 0, kFp16 = 1 };
+
+template <StateKind SK>
+struct StateTraits {
+  using storage = float;
+};
+template <>
+struct StateTraits<StateKind::kFp16> {
+  using storage = uint16_t;
+};
+
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// Four consecutive state columns, streamed (each state slab moves once).
+template <StateKind SK>
+__device__ __forceinline__ float4 load_state4(const typename StateTraits<SK>::storage* p) {
+  if constexpr (SK == StateKind::kFp32) {
+    return load_f4_stream(p);
+  } else {
+    const u32x2_t q = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+    return make_float4(f16_to_f32(static_cast<uint16_t>(q.x & 0xffffu)),
+                       f16_to_f32(static_cast<uint16_t>(q.x >> 16)),
+                       f16_to_f32(static_cast<uint16_t>(q.y & 0xffffu)),
+                       f16_to_f32(static_cast<uint16_t>(q.y >> 16)));
+  }
+}
+
+template <StateKind SK>
+__device__ __forceinline__ void store_state4(typename StateTraits<SK>::storage* p, float4 v) {
+  if constexpr (SK == StateKind::kFp32) {
+    store_f4_stream(p, v);
+  } else {
+    // v holds fp16 values already; the conversion is exact.
+    u32x2_t q;
+    q.x = static_cast<uint32_t>(from_f32<F16>(v.x)) |
+          (static_cast<uint32_t>(from_f32<F16>(v.y)) << 16);
+    q.y = static_cast<uint32_t>(from_f32<F16>(v.z)) |
+          (static_cast<uint32_t>(from_f32<F16>(v.w)) << 16);
+    __builtin_nontemporal_store(q, reinterpret_cast<u32x2_t*>(p));
+  }
+}
+
+__device__ __forceinline__ float round_f16(float x) {
+  return static_cast<float>(static_cast<_Float16>(x));
+}
+
+// Phase dither of the fp16-state delta: the signed 32-bit value of
+// phase * 2654435769 (mod 2^32), times 2^-41, so |dither| <= 2^-10.
+constexpr uint32_t kDitherMultiplier = 2654435769u;
+constexpr float kDitherUnit = 4.547473508864641e-13f;  // 2^-41
+
+__device__ __forceinline__ float phase_dither(uint32_t phase) {
+  return kDitherUnit * static_cast<float>(static_cast<int32_t>(kDitherMultiplier * phase));
+}
+
 template <int NG>
 __device__ __forceinline__ float reduce_row_groups(float x) {
   // Lanes with equal column group differ in the high bits of the lane id.
@@ -44,6 +108,7 @@ __device__ __forceinline__ float reduce_row_groups(float x) {
 // chunks, the replay stage). state_dot_a (optional) receives a_t^T S_{t-1};
 // read_only_state keeps the pool unwritten (the replay stage starts from
 // stored boundaries); status may be null (no metadata word to check).
+// elapsed is the fp16-state family's per-slot phase origin.
 struct RecurrentKernelParams {
   int32_t num_heads, num_units;
   int64_t output_elements;
@@ -52,13 +117,14 @@ struct RecurrentKernelParams {
   const int32_t* seg_ends;
   const int32_t* slots;
   const int32_t* status;
-  float* state;
+  const int32_t* elapsed;
+  void* state;
   float* state_dot_a;
   int32_t read_only_state;
   float scale;
 };
 
-template <int D, int CW, int WG, typename T, DecayMode M>
+template <int D, int CW, int WG, typename T, DecayMode M, StateKind SK>
 __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
     RecurrentKernelParams p,
     const typename IoTraits<T>::storage* __restrict__ r_ptr,
@@ -107,11 +173,19 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
     return;
   }
 
-  float* sbase = p.state + ((static_cast<int64_t>(slot) * num_heads + head) * D) * D;
+  using SS = typename StateTraits<SK>::storage;
+  SS* sbase = static_cast<SS*>(p.state) +
+              ((static_cast<int64_t>(slot) * num_heads + head) * D) * D;
   float4 s[kRpl];
 #pragma unroll
   for (int j = 0; j < kRpl; ++j) {
-    s[j] = load_f4_stream(sbase + static_cast<int64_t>(row0 + j) * D + col);
+    s[j] = load_state4<SK>(sbase + static_cast<int64_t>(row0 + j) * D + col);
+  }
+  // fp16 state: phase of key row0 at the first token.
+  uint32_t phase0 = 0;
+  if constexpr (SK == StateKind::kFp16) {
+    phase0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(p.elapsed[slot])) +
+             static_cast<uint32_t>(head * D + row0) - static_cast<uint32_t>(t_begin);
   }
 
   float bias[kRpl];
@@ -192,10 +266,19 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
 #pragma unroll
       for (int j = 0; j < kRpl; ++j) {
         const float w = decay_retention<M>(ww[j] + bias[j]);
-        s[j].x = fmaf(w, s[j].x, fmaf(bb[j], sa.x, kk[j] * vv[0]));
-        s[j].y = fmaf(w, s[j].y, fmaf(bb[j], sa.y, kk[j] * vv[1]));
-        s[j].z = fmaf(w, s[j].z, fmaf(bb[j], sa.z, kk[j] * vv[2]));
-        s[j].w = fmaf(w, s[j].w, fmaf(bb[j], sa.w, kk[j] * vv[3]));
+        if constexpr (SK == StateKind::kFp32) {
+          s[j].x = fmaf(w, s[j].x, fmaf(bb[j], sa.x, kk[j] * vv[0]));
+          s[j].y = fmaf(w, s[j].y, fmaf(bb[j], sa.y, kk[j] * vv[1]));
+          s[j].z = fmaf(w, s[j].z, fmaf(bb[j], sa.z, kk[j] * vv[2]));
+          s[j].w = fmaf(w, s[j].w, fmaf(bb[j], sa.w, kk[j] * vv[3]));
+        } else {
+          const uint32_t phase = phase0 + static_cast<uint32_t>(j + t);
+          const float delta = round_f16(w - 1.0f + phase_dither(phase));
+          s[j].x = round_f16(fmaf(kk[j], vv[0], fmaf(bb[j], sa.x, fmaf(s[j].x, delta, s[j].x))));
+          s[j].y = round_f16(fmaf(kk[j], vv[1], fmaf(bb[j], sa.y, fmaf(s[j].y, delta, s[j].y))));
+          s[j].z = round_f16(fmaf(kk[j], vv[2], fmaf(bb[j], sa.z, fmaf(s[j].z, delta, s[j].z))));
+          s[j].w = round_f16(fmaf(kk[j], vv[3], fmaf(bb[j], sa.w, fmaf(s[j].w, delta, s[j].w))));
+        }
         y.x = fmaf(rr[j], s[j].x, y.x);
         y.y = fmaf(rr[j], s[j].y, y.y);
         y.z = fmaf(rr[j], s[j].z, y.z);
@@ -216,7 +299,7 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
   if (p.read_only_state) return;
 #pragma unroll
   for (int j = 0; j < kRpl; ++j) {
-    store_f4_stream(sbase + static_cast<int64_t>(row0 + j) * D + col, s[j]);
+    store_state4<SK>(sbase + static_cast<int64_t>(row0 + j) * D + col, s[j]);
   }
 }
 
@@ -226,7 +309,7 @@ struct RecurrentArgs {
   const int32_t* cu;
   const int32_t* slots;
   const int32_t* status;
-  float* state;
+  void* state;
   const void *r, *decay, *bias, *k, *v, *a, *b;
   void* out;
   float scale;
@@ -234,9 +317,10 @@ struct RecurrentArgs {
   const int32_t* seg_ends = nullptr;
   float* state_dot_a = nullptr;
   int32_t read_only_state = 0;
+  const int32_t* elapsed = nullptr;
 };
 
-template <int D, int CW, int WG, typename T, DecayMode M>
+template <int D, int CW, int WG, typename T, DecayMode M, StateKind SK>
 int launch_recurrent(const RecurrentArgs& p) {
   using S = typename IoTraits<T>::storage;
   const int units = p.num_sequences * p.num_heads;
@@ -253,11 +337,12 @@ int launch_recurrent(const RecurrentArgs& p) {
   kp.seg_ends = p.seg_ends;
   kp.slots = p.slots;
   kp.status = p.status;
+  kp.elapsed = p.elapsed;
   kp.state = p.state;
   kp.state_dot_a = p.state_dot_a;
   kp.read_only_state = p.read_only_state;
   kp.scale = p.scale;
-  hipLaunchKernelGGL((recurrent_fp32_kernel<D, CW, WG, T, M>), dim3(blocks),
+  hipLaunchKernelGGL((recurrent_fp32_kernel<D, CW, WG, T, M, SK>), dim3(blocks),
                      dim3(WG), 0, p.stream, kp, static_cast<const S*>(p.r),
                      static_cast<const S*>(p.decay), static_cast<const S*>(p.bias),
                      static_cast<const S*>(p.k), static_cast<const S*>(p.v),
@@ -266,20 +351,20 @@ int launch_recurrent(const RecurrentArgs& p) {
   return check_launch("recurrent_fp32_kernel");
 }
 
-template <typename T, DecayMode M>
+template <typename T, DecayMode M, StateKind SK = StateKind::kFp32>
 int dispatch_head_size(const RecurrentArgs& p) {
   switch (p.head_size) {
     case 64:
       // Decode keeps one wave per state (fewest redundant decay evaluations);
       // longer sequences split the state over 4 waves for more parallelism.
       if (p.max_seqlen > 0 && p.max_seqlen <= 2) {
-        return launch_recurrent<64, 64, 64, T, M>(p);
+        return launch_recurrent<64, 64, 64, T, M, SK>(p);
       }
-      return launch_recurrent<64, 16, 256, T, M>(p);
+      return launch_recurrent<64, 16, 256, T, M, SK>(p);
     case 128:
-      return launch_recurrent<128, 16, 256, T, M>(p);
+      return launch_recurrent<128, 16, 256, T, M, SK>(p);
     case 256:
-      return launch_recurrent<256, 16, 256, T, M>(p);
+      return launch_recurrent<256, 16, 256, T, M, SK>(p);
     default:
       return set_error(FRWKV_ERR_UNSUPPORTED,
                        "recurrent head size must be 64, 128, or 256, got %d",
@@ -370,4 +455,37 @@ int frwkv_replay_recurrent(int io_dtype, int decay_mode, int32_t num_chunks, int
       return set_error(FRWKV_ERR_UNSUPPORTED,
                        "replay takes float16 or bfloat16 tokens (io dtype %d)", io_dtype);
   }
+}
+
+// fp16-state family: fp16 tokens, decay logits, fp16 pool, per-slot elapsed
+// phase origins (read, not advanced: frwkv_advance_i32_varlen does that).
+extern "C" int frwkv_recurrent_fp16_forward(
+    int32_t num_sequences, int32_t num_heads, int32_t head_size, int32_t total_tokens,
+    int32_t max_seqlen, int32_t state_pool_size, const int32_t* cu_seqlens,
+    const int32_t* state_indices, const int32_t* metadata_status,
+    const int32_t* elapsed_state_pool, void* state_pool, const void* r,
+    const void* decay_logits, const void* decay_bias, const void* k, const void* v,
+    const void* a, const void* b, void* output, float scale, void* stream) {
+  using namespace frwkv;
+  if (!cu_seqlens || !state_indices || !metadata_status || !elapsed_state_pool ||
+      !state_pool || !r || !decay_logits || !k || !v || !a || !b || !output) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT,
+                     "frwkv_recurrent_fp16_forward: null pointer argument");
+  }
+  if (num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 ||
+      total_tokens <= 0 || state_pool_size <= 0) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT,
+                     "frwkv_recurrent_fp16_forward: sizes must be positive "
+                     "(B=%d, H=%d, N=%d, slots=%d)",
+                     num_sequences, num_heads, total_tokens, state_pool_size);
+  }
+  if (!__builtin_isfinite(scale)) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT, "scale must be finite");
+  }
+  RecurrentArgs p{num_sequences, num_heads, head_size, total_tokens, max_seqlen,
+                  state_pool_size, cu_seqlens, state_indices, metadata_status,
+                  state_pool, r, decay_logits, decay_bias, k, v, a, b, output, scale,
+                  static_cast<hipStream_t>(stream)};
+  p.elapsed = elapsed_state_pool;
+  return dispatch_head_size<F16, DecayMode::kLogits, StateKind::kFp16>(p);
 }

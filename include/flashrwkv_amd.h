@@ -110,6 +110,60 @@ int frwkv_recurrent_forward(int io_dtype, int decay_mode, int32_t num_sequences,
                             void* output, float scale, void* stream);
 
 /*
+ * fp16-state recurrent forward (the Albatross family), pool [slots,H,D,D] of
+ * fp16 updated in place at state_indices.
+ * Replaces recurrent_fp16_from_decay_logits_cuda and its dispatch
+ * (csrc/sm120/tmix/wkv7/infer_recurrent_fp16_forward_varlen.cu:1078-1215,
+ * 1283-1365; binding .cpp:210-270). Tokens, decay_bias and output are fp16;
+ * the decay is given as logits. Per token, with phase = elapsed_state_pool
+ * [slot] + h*D + key + (t - sequence start), dither(p) = 2^-41 *
+ * int32(p * 2654435769 mod 2^32) and delta = fp16(w - 1 + dither):
+ *   sa = S^T a; S = fp16(S + diag(delta) S + b sa^T + k v^T);
+ *   y = fp16(scale S^T r)
+ * with fp32 arithmetic between the roundings. elapsed_state_pool [slots]
+ * int32 is read, not advanced (frwkv_advance_i32_varlen advances it).
+ * head_size in {64, 128, 256}; metadata_status and max_seqlen as for
+ * frwkv_recurrent_forward.
+ */
+int frwkv_recurrent_fp16_forward(int32_t num_sequences, int32_t num_heads,
+                                 int32_t head_size, int32_t total_tokens,
+                                 int32_t max_seqlen, int32_t state_pool_size,
+                                 const int32_t* cu_seqlens, const int32_t* state_indices,
+                                 const int32_t* metadata_status,
+                                 const int32_t* elapsed_state_pool, void* state_pool,
+                                 const void* r, const void* decay_logits,
+                                 const void* decay_bias, const void* k, const void* v,
+                                 const void* a, const void* b, void* output, float scale,
+                                 void* stream);
+
+/*
+ * elapsed_state[i] += amount for i < count (int32, wrapping).
+ * Replaces recurrent_fp16_advance_i32_cuda
+ * (csrc/sm120/tmix/wkv7/infer_recurrent_fp16_forward_varlen.cu:57-64, 1217-1228).
+ */
+int frwkv_advance_i32(int32_t* elapsed_state, int64_t count, int32_t amount, void* stream);
+
+/*
+ * elapsed_state_pool[state_indices[s]] += cu_seqlens[s+1] - cu_seqlens[s] for
+ * every sequence s; nothing when metadata_status[0] != 0 at run time.
+ * Replaces recurrent_fp16_advance_i32_varlen_cuda
+ * (csrc/sm120/tmix/wkv7/infer_recurrent_fp16_forward_varlen.cu:67-81, 1230-1245).
+ */
+int frwkv_advance_i32_varlen(int32_t num_sequences, int32_t state_pool_size,
+                             const int32_t* cu_seqlens, const int32_t* state_indices,
+                             const int32_t* metadata_status, int32_t* elapsed_state_pool,
+                             void* stream);
+
+/*
+ * output[n,c] = fp16(float(x[n,c]) + float(vec[c])) for x [rows,channels]
+ * fp16 (channels even; x, vec, output 4-byte aligned).
+ * Replaces recurrent_add_vec_forward_varlen_cuda
+ * (csrc/sm120/tmix/wkv7/infer_recurrent_fp16_forward_varlen.cu:85-122, 1247-1281).
+ */
+int frwkv_add_vec(int64_t rows, int32_t channels, const void* x, const void* vec,
+                  void* output, void* stream);
+
+/*
  * Chunked forward over packed varlen sequences (prefill), state pool updated
  * in place at state_indices. Exact chunk form of the recurrence on bf16 MFMA
  * with fp32 accumulation and an fp32 state carried between 64-token chunks;

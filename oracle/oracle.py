@@ -28,6 +28,18 @@ How each function is pinned (see ``tests/test_oracle.py``):
 * ``backward``: torch fp64 autograd through an independent per-token torch
   forward (itself checked against ``forward``), and central finite
   differences at D=4.
+* ``fp16_dither``: known answers at phases 0, 1, 2, -1 and 2^31 worked out by
+  hand from the definition (recurrent_decay.cuh:36-41).
+* ``forward_fp16_state``: agreement with the pinned fp32-state ``forward``
+  within fp16 rounding (catches a dropped term, sign or transpose); phase
+  continuity (tokens split over two calls with the phase origin advanced
+  by the first call's length give the same result bitwise); channel
+  mapping c = h*D + key (with a = b = k = 0 the rows evolve independently,
+  so H=2, D=4 must equal H=1, D=8); sensitivity to the phase origin.
+* ``advance_i32`` / ``advance_i32_varlen``: the reference test's known
+  answers (tests/tmix/wkv7/test.py:32-60) and int32 wrap-around.
+* ``add_vec``: exact sums and round-half-to-even ties at 2048 + 1 and
+  2050 + 1 (fp16 spacing 2 there).
 """
 
 from __future__ import annotations
@@ -251,6 +263,91 @@ def forward_einsum(r, w, k, v, a, b, state_pool, cu_seqlens, state_indices,
             y[t] = scale * np.einsum("hk,hkv->hv", r[t], s)
         pool[slots[seq]] = s
     return y, pool
+
+
+# ------------------------------------------------------- fp16 state -----
+#
+# The fp16-state (Albatross) family, restating the reference's contract oracle
+# ``tests/tmix/wkv7/test.py:214-264`` and the dither of
+# ``csrc/sm120/tmix/wkv7/recurrent_decay.cuh:36-46``. Arithmetic between the
+# contract's fp16 rounding points (delta, state after every token, output) is
+# fp64 here; the rounding points themselves are the contract.
+
+DITHER_MULTIPLIER = 2654435769
+DITHER_UNIT = 2.0 ** -41  # 4.547473508864641e-13
+
+
+def fp16_dither(phase) -> np.ndarray:
+    """``float32(int32(phase * 2654435769 mod 2^32)) * 2^-41`` (recurrent_decay.cuh:36-41).
+
+    The int32 -> float32 conversion rounds to 24 bits, as the device does;
+    the scaling by a power of two is exact.
+    """
+    p = np.asarray(phase).astype(np.int64).astype(np.uint64) & np.uint64(0xFFFFFFFF)
+    with np.errstate(over="ignore"):
+        bits = (p * np.uint64(DITHER_MULTIPLIER)) & np.uint64(0xFFFFFFFF)
+    signed = bits.astype(np.int64) - (bits >= np.uint64(1 << 31)).astype(np.int64) * (1 << 32)
+    return signed.astype(np.float32).astype(np.float64) * DITHER_UNIT
+
+
+def fp16_delta(x, phase, bias=None) -> np.ndarray:
+    """``fp16(retention(x + bias) - 1 + dither(phase))`` as float64 (recurrent_decay.cuh:43-46)."""
+    w = retention_from_logits(x, bias)
+    return (w - 1.0 + fp16_dither(phase)).astype(np.float16).astype(np.float64)
+
+
+def forward_fp16_state(r, x, k, v, a, b, state_pool, elapsed_state_pool, cu_seqlens,
+                       state_indices, scale=1.0, bias=None):
+    """fp16-state recurrence over packed sequences (test.py:214-264).
+
+    ``x`` are decay logits; ``state_pool`` ``[slots,H,D,D]`` ([K,V]) and the
+    returned pool are float16; ``elapsed_state_pool`` ``[slots]`` int32 phase
+    origins (read only). Channel ``c = h*D + key`` of token ``t`` of a
+    sequence starting at ``start`` uses phase ``elapsed[slot] + c + t - start``.
+    Returns ``(y float16 [N,H,D], pool float16)``.
+    """
+    r, x, k, v, a, b = (_f64(t) for t in (r, x, k, v, a, b))
+    n, heads, d = r.shape
+    pool = np.asarray(state_pool).astype(np.float16).copy()
+    elapsed = np.asarray(elapsed_state_pool).astype(np.int64)
+    channel = np.arange(heads * d, dtype=np.int64).reshape(heads, d)
+    y = np.zeros((n, heads, d), dtype=np.float16)
+    cu = [int(c) for c in np.asarray(cu_seqlens)]
+    slots = [int(c) for c in np.asarray(state_indices)]
+    for seq, (start, end) in enumerate(zip(cu[:-1], cu[1:])):
+        slot = slots[seq]
+        s = pool[slot].astype(np.float64)
+        for t in range(start, end):
+            delta = fp16_delta(x[t], channel + elapsed[slot] + (t - start), bias)
+            sa = np.einsum("hk,hkv->hv", a[t], s)
+            s = (s + s * delta[:, :, None] + b[t][:, :, None] * sa[:, None, :]
+                 + k[t][:, :, None] * v[t][:, None, :])
+            s = s.astype(np.float16).astype(np.float64)
+            y[t] = (scale * np.einsum("hk,hkv->hv", r[t], s)).astype(np.float16)
+        pool[slot] = s.astype(np.float16)
+    return y, pool
+
+
+def advance_i32(elapsed_state, amount) -> np.ndarray:
+    """``elapsed + amount`` with int32 wrap-around (fp16 .cu:57-64)."""
+    e = np.asarray(elapsed_state).astype(np.int64) + int(amount)
+    return ((e + (1 << 31)) % (1 << 32) - (1 << 31)).astype(np.int32)
+
+
+def advance_i32_varlen(elapsed_state_pool, cu_seqlens, state_indices) -> np.ndarray:
+    """Each selected slot advanced by its sequence length (fp16 .cu:67-81)."""
+    out = np.asarray(elapsed_state_pool).astype(np.int64).copy()
+    cu = np.asarray(cu_seqlens).astype(np.int64)
+    for seq, slot in enumerate(np.asarray(state_indices)):
+        out[int(slot)] += cu[seq + 1] - cu[seq]
+    return ((out + (1 << 31)) % (1 << 32) - (1 << 31)).astype(np.int32)
+
+
+def add_vec(x, vec) -> np.ndarray:
+    """``fp16(float32(x) + float32(vec))`` per row (fp16 .cu:85-122)."""
+    x32 = np.asarray(x).astype(np.float16).astype(np.float32)
+    v32 = np.asarray(vec).astype(np.float16).astype(np.float32)
+    return (x32 + v32[None, :]).astype(np.float16)
 
 
 # ------------------------------------------------------------- metrics -----

@@ -98,3 +98,19 @@ def test_ctypes_binding_reports_errors_without_a_gpu():
     assert rc == 1 and b"null pointer" in lib.frwkv_last_error()
     with pytest.raises(RuntimeError, match="invalid argument"):
         capi._check(rc)
+
+
+def test_fp16_state_entry_points_reject_bad_arguments_without_a_gpu():
+    from flashrwkv_amd import capi
+
+    lib = capi.library()
+    null = ctypes.c_void_p()
+    rc = lib.frwkv_recurrent_fp16_forward(1, 1, 64, 1, 1, 1, *([null] * 13), 1.0, null)
+    assert rc == 1 and b"null pointer" in lib.frwkv_last_error()
+    assert lib.frwkv_advance_i32(null, 0, 5, null) == 1
+    assert b"non-empty" in lib.frwkv_last_error()
+    assert lib.frwkv_advance_i32_varlen(1, 4, null, null, null, null, null) == 1
+    # Odd row length: rejected before any pointer is touched.
+    fake = ctypes.c_void_p(0x1000)
+    assert lib.frwkv_add_vec(3, 7, fake, fake, fake, null) == 1
+    assert b"even C" in lib.frwkv_last_error()

@@ -282,3 +282,101 @@ def test_metrics_are_normwise():
     ref = np.array([1.0, -4.0, 2.0])
     assert oracle.max_rel_error(ref + np.array([0.0, 0.4, 0.0]), ref) == pytest.approx(0.1)
     assert oracle.relative_rmse(ref, ref) == 0.0
+
+
+# ------------------------------------------------------- fp16 state ----
+
+
+def test_fp16_dither_known_answers():
+    """int32(p * 2654435769 mod 2^32), rounded to float32, times 2^-41, worked by
+    hand: p=1 -> -1640531527 (float32 -1640531584), p=2 -> 1013904242
+    (1013904256), p=-1 -> 1640531527, p=2^31 -> -2^31."""
+    phases = np.array([0, 1, 2, -1, 2**31], dtype=np.int64)
+    expected = np.array([0, -1640531584, 1013904256, 1640531584, -2147483648]) * 2.0**-41
+    assert np.array_equal(oracle.fp16_dither(phases), expected)
+    assert np.max(np.abs(oracle.fp16_dither(np.arange(-5000, 5000)))) <= 2.0**-10
+
+
+def _fp16_case(lengths, h, d, *, seed, slots=None, pool_slots=None):
+    rng = np.random.default_rng(seed)
+    n = sum(lengths)
+    r, _, k, v, a, b = _tokens(n, h, d, rng=rng)
+    x = rng.standard_normal((n, h, d)) * 2.0
+    half = [t.astype(np.float16) for t in (r * 0.3, x, k * 0.3, v * 0.3, a, b)]
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    if slots is None:
+        slots = np.arange(len(lengths), dtype=np.int32)
+    slots = np.asarray(slots, dtype=np.int32)
+    pool_slots = pool_slots or int(slots.max()) + 1
+    pool = (rng.standard_normal((pool_slots, h, d, d)) * 0.3).astype(np.float16)
+    elapsed = (np.arange(pool_slots) * 11 + 3).astype(np.int32)
+    bias = (rng.standard_normal((h, d)) * 0.2).astype(np.float16)
+    return half, pool, elapsed, cu, slots, bias
+
+
+def test_fp16_state_tracks_the_fp32_state_recurrence():
+    """Same inputs through the pinned fp32-state forward: close (fp16 rounding
+    and a dither of at most 2^-10 per step), but not identical."""
+    half, pool, elapsed, cu, slots, bias = _fp16_case((5, 17), 2, 8, seed=31, slots=(2, 0))
+    y16, pool16 = oracle.forward_fp16_state(*half, pool, elapsed, cu, slots, scale=0.7,
+                                            bias=bias)
+    r, x, k, v, a, b = (t.astype(np.float64) for t in half)
+    w = oracle.retention_from_logits(x, bias.astype(np.float64))
+    y64, pool64 = oracle.forward_varlen(r, w, k, v, a, b, pool.astype(np.float64), cu, slots,
+                                        scale=0.7)
+    err_y = oracle.max_rel_error(y16, y64)
+    err_s = oracle.max_rel_error(pool16[[2, 0]], pool64[[2, 0]])
+    assert 1e-5 < err_y < 5e-3 and 1e-5 < err_s < 5e-3, (err_y, err_s)
+    assert np.array_equal(pool16[1], pool[1])
+
+
+def test_fp16_state_phase_continues_across_calls():
+    """Split a sequence over two calls, the second from the advanced phase
+    origin and the first call's pool: bitwise the same as one call."""
+    half, pool, elapsed, cu, slots, bias = _fp16_case((23,), 2, 8, seed=32)
+    y, final = oracle.forward_fp16_state(*half, pool, elapsed, cu, slots, bias=bias)
+    m = 9
+    first = [t[:m] for t in half]
+    second = [t[m:] for t in half]
+    y1, mid = oracle.forward_fp16_state(*first, pool, elapsed, [0, m], slots, bias=bias)
+    advanced = oracle.advance_i32_varlen(elapsed, [0, m], slots)
+    y2, end = oracle.forward_fp16_state(*second, mid, advanced, [0, 23 - m], slots, bias=bias)
+    assert np.array_equal(np.concatenate([y1, y2]), y) and np.array_equal(end, final)
+    # The phase origin matters: one step later gives a different state.
+    _, shifted = oracle.forward_fp16_state(*half, pool, elapsed + 1, cu, slots, bias=bias)
+    assert not np.array_equal(shifted, final)
+
+
+def test_fp16_state_channel_is_head_times_d_plus_key():
+    """With a = b = k = 0 every key row evolves alone (S = fp16(S (1 + delta))),
+    so H=2, D=4 equals rows h*4 + key of H=1, D=8."""
+    rng = np.random.default_rng(33)
+    n = 6
+    x8 = (rng.standard_normal((n, 1, 8)) * 2).astype(np.float16)
+    s8 = (rng.standard_normal((1, 1, 8, 8)) * 0.3).astype(np.float16)
+    zeros8 = np.zeros((n, 1, 8), dtype=np.float16)
+    elapsed = np.array([5], dtype=np.int32)
+    cu, slots = np.array([0, n], dtype=np.int32), np.array([0], dtype=np.int32)
+    _, out8 = oracle.forward_fp16_state(zeros8, x8, zeros8, zeros8, zeros8, zeros8, s8,
+                                        elapsed, cu, slots)
+    x4 = x8.reshape(n, 2, 4)
+    s4 = np.ascontiguousarray(s8[:, 0, :, :4].reshape(1, 2, 4, 4))
+    zeros4 = np.zeros((n, 2, 4), dtype=np.float16)
+    _, out4 = oracle.forward_fp16_state(zeros4, x4, zeros4, zeros4, zeros4, zeros4, s4,
+                                        elapsed, cu, slots)
+    assert np.array_equal(out4.reshape(1, 8, 4), out8[:, 0, :, :4])
+    assert not np.array_equal(out8, s8)
+
+
+def test_advance_known_answers_and_wraparound():
+    """Reference tests/tmix/wkv7/test.py:32-60."""
+    assert oracle.advance_i32([2, 7, 11], 5).tolist() == [7, 12, 16]
+    assert oracle.advance_i32_varlen([2, 5, 7, 11], [0, 2, 5], [3, 1]).tolist() == [2, 8, 7, 13]
+    assert oracle.advance_i32([2**31 - 1, -(2**31)], 1).tolist() == [-(2**31), -(2**31) + 1]
+
+
+def test_add_vec_exact_sums_and_ties_to_even():
+    """fp16 spacing is 2 at 2048: 2048 + 1 and 2050 + 1 are ties (to even)."""
+    x = np.array([[2048, 2050, 1.5, -3.0]], dtype=np.float16)
+    vec = np.array([1, 1, 0.25, 3.0], dtype=np.float16)
+    assert oracle.add_vec(x, vec).tolist() == [[2048.0, 2052.0, 1.75, 0.0]]
