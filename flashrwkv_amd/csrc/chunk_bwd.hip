@@ -975,10 +975,8 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
       {
         auto st4 = [&](void* dst, const float (&x)[4]) {
           u32x2 q;
-          q.x = static_cast<uint32_t>(from_f32<T>(x[0])) |
-                (static_cast<uint32_t>(from_f32<T>(x[1])) << 16);
-          q.y = static_cast<uint32_t>(from_f32<T>(x[2])) |
-                (static_cast<uint32_t>(from_f32<T>(x[3])) << 16);
+          q.x = pack2<T>(x[0], x[1]);
+          q.y = pack2<T>(x[2], x[3]);
           __builtin_amdgcn_raw_buffer_store_b64(q, rs(dst), tok_off, so, 0);
         };
         st4(p.dr, grad_r);
@@ -1020,10 +1018,8 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
         }
         {
           u32x2 q;
-          q.x = static_cast<uint32_t>(from_f32<T>(dwv[0])) |
-                (static_cast<uint32_t>(from_f32<T>(dwv[1])) << 16);
-          q.y = static_cast<uint32_t>(from_f32<T>(dwv[2])) |
-                (static_cast<uint32_t>(from_f32<T>(dwv[3])) << 16);
+          q.x = pack2<T>(dwv[0], dwv[1]);
+          q.y = pack2<T>(dwv[2], dwv[3]);
           __builtin_amdgcn_raw_buffer_store_b64(q, rs(p.ddecay), tok_off,
                                                 static_cast<int>(2 * 16 * kb), 0);
         }

@@ -61,7 +61,7 @@ __device__ __forceinline__ float log2_retention(float x) {
   } else {
     lg = __builtin_amdgcn_logf(x);
   }
-  return fminf(fmaxf(lg, kLog2Min), 0.0f);
+  return __builtin_amdgcn_fmed3f(lg, kLog2Min, 0.0f);
 }
 
 // 8 floats -> 8 bf16 at an 8-byte aligned LDS address (two 8-byte writes).

@@ -144,22 +144,23 @@ struct Spans {
 
 // Decodes the thread's rows restricted to tokens [lo, hi) of the chunk,
 // scans the decay and writes the scaled operand tiles At, Rt, Bh, Kh
-// ([t][k]) and the V tile. Ends with a barrier.
+// ([t][k]) and the V tile. Ends with a barrier. kFull: the range is the
+// whole 64-token chunk, so no token needs masking.
 //
 // Per feature, the thread's tokens t0 and t0 + 1 need 2^Gp(t0), 2^G(t0)
 // (= 2^Gp(t0 + 1)), 2^G(t0 + 1), 2^-G(t0), 2^-G(t0 + 1): two exponentials
 // and products with the retentions w = 2^lg (G(t) = Gp(t) + lg(t)).
-template <typename T, DecayMode M>
+template <typename T, DecayMode M, bool kFull>
 __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bias)[8],
                          int lo, int hi) {
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = uniform(tid >> 6);
   const int lane = tid & 63;
   const int tp = lane & 7;   // token pair
   const int kg = lane >> 3;  // feature group
   const int t0 = 16 * wave + 2 * tp;
-  const bool on0 = t0 >= lo && t0 < hi;
-  const bool on1 = t0 + 1 >= lo && t0 + 1 < hi;
+  const bool on0 = kFull || (t0 >= lo && t0 < hi);
+  const bool on1 = kFull || (t0 + 1 >= lo && t0 + 1 < hi);
 
   __syncthreads();  // earlier readers of the tiles are done
 
@@ -172,14 +173,18 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
     unpack8<T>(rows.w[1], x1);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float l0 = log2_retention<M>(x0[e] + bias[e]);
-      const float l1 = log2_retention<M>(x1[e] + bias[e]);
+      if constexpr (M == DecayMode::kLogits) {
+        x0[e] += bias[e];
+        x1[e] += bias[e];
+      }
+      const float l0 = log2_retention<M>(x0[e]);
+      const float l1 = log2_retention<M>(x1[e]);
       lg0[e] = on0 ? l0 : 0.0f;
       lg1[e] = on1 ? l1 : 0.0f;
       if constexpr (M == DecayMode::kRawW) {
         // 2^lg is the input clamped to [2^-20, 1] (log2_retention's clamp).
-        w0[e] = on0 ? fminf(fmaxf(x0[e], 0x1p-20f), 1.0f) : 1.0f;
-        w1[e] = on1 ? fminf(fmaxf(x1[e], 0x1p-20f), 1.0f) : 1.0f;
+        w0[e] = on0 ? __builtin_amdgcn_fmed3f(x0[e], 0x1p-20f, 1.0f) : 1.0f;
+        w1[e] = on1 ? __builtin_amdgcn_fmed3f(x1[e], 0x1p-20f, 1.0f) : 1.0f;
       } else {
         w0[e] = fast_exp2(lg0[e]);
         w1[e] = fast_exp2(lg1[e]);
@@ -203,40 +208,45 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
   }
   __syncthreads();
 
+  // Block totals x_q (q = 0..3, one per wave's 16 tokens); the carry into
+  // this wave is the sum of the blocks before it (a wave-uniform count).
   float gp0[8], g1[8], total[8];
-  bool over_all = false, over_block[4] = {false, false, false, false};
-  {
-    float base[8], tot[8];
+  float xq[4][8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) base[e] = tot[e] = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float4 xa = *reinterpret_cast<const float4*>(&sm.wave_tot[q][8 * kg]);
-      const float4 xb = *reinterpret_cast<const float4*>(&sm.wave_tot[q][8 * kg + 4]);
-      const float x[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        base[e] += (q < wave) ? x[e] : 0.0f;
-        tot[e] += x[e];
-        over_block[q] |= -x[e] > kSpanLimit;
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      total[e] = tot[e];
-      over_all |= -tot[e] > kSpanLimit;
-      gp0[e] = base[e] + incl[e] - lg0[e] - lg1[e];
-      g1[e] = gp0[e] + lg0[e] + lg1[e];
-    }
+  for (int q = 0; q < 4; ++q) {
+    const float4 xa = *reinterpret_cast<const float4*>(&sm.wave_tot[q][8 * kg]);
+    const float4 xb = *reinterpret_cast<const float4*>(&sm.wave_tot[q][8 * kg + 4]);
+    xq[q][0] = xa.x; xq[q][1] = xa.y; xq[q][2] = xa.z; xq[q][3] = xa.w;
+    xq[q][4] = xb.x; xq[q][5] = xb.y; xq[q][6] = xb.z; xq[q][7] = xb.w;
   }
-  // Every wave covers all 64 features, so the ballots agree across waves.
-  Spans spans;
-  spans.whole = __builtin_amdgcn_ballot_w64(over_all) == 0;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) spans.block[q] = __builtin_amdgcn_ballot_w64(over_block[q]) == 0;
+  for (int e = 0; e < 8; ++e) {
+    const float lo2 = xq[0][e] + xq[1][e];
+    const float hi2 = xq[2][e] + xq[3][e];
+    total[e] = lo2 + hi2;
+    float base = 0.0f;
+    if (wave == 1) base = xq[0][e];
+    if (wave == 2) base = lo2;
+    if (wave == 3) base = lo2 + xq[2][e];
+    g1[e] = base + incl[e];
+    gp0[e] = g1[e] - (lg0[e] + lg1[e]);
+  }
+  // A span exceeds the limit when its (non-positive) log2 decay sum is
+  // below -kSpanLimit; min reductions over the thread's 8 features, then a
+  // ballot. Every wave covers all 64 features, so the ballots agree.
+  auto within = [](const float (&x)[8]) {
+    float m = x[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) m = fminf(m, x[e]);
+    return __builtin_amdgcn_ballot_w64(m < -kSpanLimit) == 0;
+  };
+  Spans spans;
+  spans.whole = within(total);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) spans.block[q] = within(xq[q]);
 
   // Scale factors of the thread's two token rows, zero outside [lo, hi).
-  float fa0[8], fa1[8], fr0[8], fr1[8], fd0[8], fd1[8], gcv[8];
+  float fa0[8], fa1[8], fr0[8], fr1[8], fd0[8], fd1[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float up_p = fast_exp2(gp0[e]);  // 2^Gp(t0)
@@ -250,7 +260,6 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
     fr1[e] = on1 ? up1 : 0.0f;
     fd0[e] = on0 ? dn0 : 0.0f;
     fd1[e] = on1 ? dn1 : 0.0f;
-    gcv[e] = fast_exp2(total[e]);
   }
   auto tile_rows = [&](uint16_t* tile, uint4 q0, uint4 q1, const float (&f0)[8],
                        const float (&f1)[8]) {
@@ -276,7 +285,7 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
   }
   if (wave == 0 && tp == 0) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sm.gc[8 * kg + e] = gcv[e];
+    for (int e = 0; e < 8; ++e) sm.gc[8 * kg + e] = fast_exp2(total[e]);
   }
   if (wave < 3 && tp == 7) {
     // Token t0 + 1 = 16 wave + 15 ends a 16-token block.
@@ -299,6 +308,10 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
 // the twelve off-diagonal half-pairs ({Lab, Arb} share Bh_q, {Lak, Ark}
 // share Kh_q; both share At_p and Rt_p).
 __device__ void intra_chunk(ChunkSmem& sm) {
+  // MFMA phases run at raised wave priority: the other workgroup on the CU
+  // is then usually in its VALU-heavy prepare, and the arbiter keeps the
+  // matrix pipe fed from this one.
+  __builtin_amdgcn_s_setprio(1);
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -392,6 +405,7 @@ __device__ void intra_chunk(ChunkSmem& sm) {
     const int q = pair - (p * (p - 1)) / 2;
     group(p, q, (item & 1) == 0, (item & 1) == 1);
   }
+  __builtin_amdgcn_s_setprio(0);
   __syncthreads();
 }
 
@@ -409,6 +423,7 @@ __device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const uint16_t* v
                            __amdgpu_buffer_rsrc_t out_rs, __amdgpu_buffer_rsrc_t sda_rs,
                            bool with_sda, uint32_t row_bytes, float scale, int lo, int hi,
                            __amdgpu_buffer_rsrc_t sub_rs, int nsub) {
+  __builtin_amdgcn_s_setprio(1);  // MFMA phase (see intra_chunk)
   const int tid = threadIdx.x;
   const int w = tid >> 6;
   const int lane = tid & 63;
@@ -566,6 +581,7 @@ __device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const uint16_t* v
 #pragma unroll
     for (int j = 0; j < 4; ++j) S[kb][j] = sn[kb][j] * sm.gc[16 * kb + 4 * g + j];
   }
+  __builtin_amdgcn_s_setprio(0);
 
   // Lane (g, n) stores Y[16p + n][16w + 4g .. 16w + 4g + 3] (8 bytes).
   const uint32_t y_off = static_cast<uint32_t>(n) * row_bytes + 2 * (16 * w + 4 * g);
@@ -574,10 +590,8 @@ __device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const uint16_t* v
     const int t = 16 * pb + n;
     if (t >= lo && t < hi) {
       u32x2 q;
-      q.x = static_cast<uint32_t>(from_f32<T>(scale * y[pb][0])) |
-            (static_cast<uint32_t>(from_f32<T>(scale * y[pb][1])) << 16);
-      q.y = static_cast<uint32_t>(from_f32<T>(scale * y[pb][2])) |
-            (static_cast<uint32_t>(from_f32<T>(scale * y[pb][3])) << 16);
+      q.x = pack2<T>(scale * y[pb][0], scale * y[pb][1]);
+      q.y = pack2<T>(scale * y[pb][2], scale * y[pb][3]);
       __builtin_amdgcn_raw_buffer_store_b64(q, out_rs, y_off,
                                             static_cast<int>(16 * pb * row_bytes), 0);
     }
@@ -785,7 +799,8 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
       bool whole = true, first = true;
       int lo = 0, hi = ntok;
       for (;;) {
-        const Spans cur = prepare<T, M>(sm, rows, bias, lo, hi);
+        const Spans cur = (lo == 0 && hi == kChunk) ? prepare<T, M, true>(sm, rows, bias, lo, hi)
+                                                    : prepare<T, M, false>(sm, rows, bias, lo, hi);
         if (first) {
           first = false;
           spans = cur;

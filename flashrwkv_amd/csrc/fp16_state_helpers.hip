@@ -46,8 +46,7 @@ __device__ __forceinline__ uint32_t add_pair(uint32_t x, uint32_t v) {
                    f16_to_f32(static_cast<uint16_t>(v & 0xffffu));
   const float hi = f16_to_f32(static_cast<uint16_t>(x >> 16)) +
                    f16_to_f32(static_cast<uint16_t>(v >> 16));
-  return static_cast<uint32_t>(from_f32<F16>(lo)) |
-         (static_cast<uint32_t>(from_f32<F16>(hi)) << 16);
+  return pack2<F16>(lo, hi);
 }
 
 // Each lane adds W consecutive elements of one row (W = 8: 16-byte loads,

@@ -71,10 +71,8 @@ __device__ __forceinline__ void store_state4(typename StateTraits<SK>::storage* 
   } else {
     // v holds fp16 values already; the conversion is exact.
     u32x2_t q;
-    q.x = static_cast<uint32_t>(from_f32<F16>(v.x)) |
-          (static_cast<uint32_t>(from_f32<F16>(v.y)) << 16);
-    q.y = static_cast<uint32_t>(from_f32<F16>(v.z)) |
-          (static_cast<uint32_t>(from_f32<F16>(v.w)) << 16);
+    q.x = pack2<F16>(v.x, v.y);
+    q.y = pack2<F16>(v.z, v.w);
     __builtin_nontemporal_store(q, reinterpret_cast<u32x2_t*>(p));
   }
 }

@@ -101,6 +101,24 @@ __device__ __forceinline__ typename IoTraits<T>::storage from_f32(float x) {
   }
 }
 
+// Two floats -> two 16-bit io values packed in one dword (lo in bits 0..15),
+// rounded to nearest even. The vector conversion lets the compiler select one
+// packed conversion (v_cvt_pk_bf16_f32 for bf16) instead of a conversion per
+// value followed by shift/mask/or packing.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  typedef float v2f __attribute__((ext_vector_type(2)));
+  const v2f v = {lo, hi};
+  if constexpr (__is_same(T, Bf16)) {
+    typedef __bf16 v2h __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, v2h));
+  } else {
+    static_assert(__is_same(T, F16), "pack2 packs 16-bit io types");
+    typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, v2h));
+  }
+}
+
 // Loads N contiguous elements (16-byte aligned when N*bytes >= 16) as floats.
 template <typename T, int N>
 __device__ __forceinline__ void load_vec(const typename IoTraits<T>::storage* p,
@@ -194,10 +212,8 @@ __device__ __forceinline__ void store4(typename IoTraits<T>::storage* p, float x
     *reinterpret_cast<float4*>(p) = make_float4(x0, x1, x2, x3);
   } else {
     uint2 q;
-    q.x = static_cast<uint32_t>(from_f32<T>(x0)) |
-          (static_cast<uint32_t>(from_f32<T>(x1)) << 16);
-    q.y = static_cast<uint32_t>(from_f32<T>(x2)) |
-          (static_cast<uint32_t>(from_f32<T>(x3)) << 16);
+    q.x = pack2<T>(x0, x1);
+    q.y = pack2<T>(x2, x3);
     *reinterpret_cast<uint2*>(p) = q;
   }
 }

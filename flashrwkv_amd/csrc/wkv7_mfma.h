@@ -80,19 +80,24 @@ __device__ __forceinline__ float bf16_float(uint16_t bits) {
   return __uint_as_float(static_cast<uint32_t>(bits) << 16);
 }
 
+// Two fp32 -> two round-to-nearest-even bf16 in one dword (lo in bits
+// 0..15). The vector conversion selects one v_cvt_pk_bf16_f32 with both
+// sources; converting the halves one by one costs a conversion per value plus
+// the shift/mask/or to pack them.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(to_bf16_bits(lo)) |
-         (static_cast<uint32_t>(to_bf16_bits(hi)) << 16);
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
-// C-layout accumulator -> bf16 operand registers.
+// C-layout accumulator -> bf16 operand registers (two packed conversions;
+// a single 4-wide vector conversion is split into per-value conversions plus
+// byte permutes when its result feeds an MFMA operand directly).
 __device__ __forceinline__ i16x4 to_operand(f32x4 c) {
-  i16x4 r;
-  r[0] = static_cast<short>(to_bf16_bits(c[0]));
-  r[1] = static_cast<short>(to_bf16_bits(c[1]));
-  r[2] = static_cast<short>(to_bf16_bits(c[2]));
-  r[3] = static_cast<short>(to_bf16_bits(c[3]));
-  return r;
+  const u32x2 q = {pack_bf16x2(c[0], c[1]), pack_bf16x2(c[2], c[3])};
+  return __builtin_bit_cast(i16x4, q);
 }
 
 // Operand read from an LDS tile: 4 consecutive bf16 of row `row` starting at
