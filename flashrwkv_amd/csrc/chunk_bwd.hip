@@ -322,7 +322,12 @@ __device__ bool prepare_bwd(BwdSmem& sm, const BwdRows& rows, const float (&bias
 // ([t][i]), Arb, Ark, Lab, Lak transposed ([i][t]), and T, T^T. Ends with a
 // barrier. A product with A = source rows, B = target rows stores [t][i];
 // with A = target rows, B = source rows it stores [i][t].
-__device__ void intra_bwd(BwdSmem& sm) {
+// issue(i), i = 0..4, is called between the product groups: the caller
+// issues a fifth of the earlier chunk's loads there, so they enter the
+// memory system while the products run instead of stalling the wave on one
+// burst of 30 outstanding loads.
+template <typename Issue>
+__device__ __forceinline__ void intra_bwd(BwdSmem& sm, Issue&& issue) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -382,7 +387,9 @@ __device__ void intra_bwd(BwdSmem& sm) {
   };
 
   f32x4 l_r, l_c;
+  issue(0);
   group(wave, wave, true, true, &l_r, &l_c);
+  issue(1);
   // T = (I - L)^{-1} = (I + L)(I + L^2)(I + L^4)(I + L^8) in both layouts
   // (see the forward kernel): Z = X Y gives Z_C = mfma(X_R, Y_C) and
   // Z_R = mfma(Y_C, X_R).
@@ -416,6 +423,7 @@ __device__ void intra_bwd(BwdSmem& sm) {
     const int pair = item >> 1;
     const int p = pair < 1 ? 1 : (pair < 3 ? 2 : 3);
     const int q = pair - (p * (p - 1)) / 2;
+    issue(2 + r);
     group(p, q, (item & 1) == 0, (item & 1) == 1, nullptr, nullptr);
   }
   __syncthreads();
@@ -496,49 +504,83 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
     te = uniform(min(__builtin_amdgcn_readlane(ends_v, seg - cache_base), p.total_tokens));
   };
 
-  // Inputs of a chunk (see BwdRows). Rows past the chunk's tokens read as
-  // zero through the buffer bounds.
-  auto load_chunk = [&](int seg, BwdRows& rows) {
+  // Inputs of a chunk (see BwdRows), in five pieces (0: w, r; 1: k, a;
+  // 2: b, dY; 3: V and the first half of the checkpoint slice; 4: the rest).
+  // Rows past the chunk's tokens read as zero through the buffer bounds; an
+  // invalid segment (seg < seg_lo) has empty ranges and loads zeros.
+  struct ChunkSrc {
+    int64_t b0;
+    uint32_t nbytes;
+    int64_t ck_index;
+    bool valid;
+  };
+  auto chunk_src = [&](int seg) {
+    ChunkSrc c{0, 0u, 0, false};
+    if (seg < seg_lo) return c;
     int tb, te;
     seg_bounds(seg, tb, te);
     const int nt = uniform(max(min(te - tb, kChunk), 0));
-    const int64_t b0 = (static_cast<int64_t>(tb) * heads + head) * kHead;
-    const uint32_t nbytes = static_cast<uint32_t>(nt) * row_bytes;
+    c.b0 = (static_cast<int64_t>(tb) * heads + head) * kHead;
+    c.nbytes = static_cast<uint32_t>(nt) * row_bytes;
+    c.ck_index = p.ckpt16 ? (static_cast<int64_t>(seq) * heads + head) * (p.dense_t / 16) + 4 * seg
+                          : static_cast<int64_t>(seg) * heads + head;
+    c.valid = true;
+    return c;
+  };
+  auto load_piece = [&](const ChunkSrc& c, BwdRows& rows, int piece) {
     auto brs = [&](const void* x) {
-      return buffer_rsrc(x != nullptr ? static_cast<const S16*>(x) + b0 : nullptr,
-                         x != nullptr ? nbytes : 0u);
+      return buffer_rsrc(x != nullptr ? static_cast<const S16*>(x) + c.b0 : nullptr,
+                         x != nullptr ? c.nbytes : 0u);
     };
     auto ld = [&](__amdgpu_buffer_rsrc_t r, uint32_t off, int so) {
       const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, off, so, 0);
       return make_uint4(x.x, x.y, x.z, x.w);
     };
-    const auto r_rs = brs(p.r), w_rs = brs(p.decay), k_rs = brs(p.k), a_rs = brs(p.a),
-               b_rs = brs(p.b), v_rs = brs(p.v), dy_rs = brs(p.dy);
+    auto rows2 = [&](const void* x, uint4 (&dst)[2]) {
+      const auto r = brs(x);
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int so = s * static_cast<int>(row_bytes);
-      rows.r[s] = ld(r_rs, prep_off, so);
-      rows.w[s] = ld(w_rs, prep_off, so);
-      rows.k[s] = ld(k_rs, prep_off, so);
-      rows.a[s] = ld(a_rs, prep_off, so);
-      rows.b[s] = ld(b_rs, prep_off, so);
-      const int piece = tid + 256 * s;
-      const uint32_t tile_off = static_cast<uint32_t>(piece >> 3) * row_bytes + 16 * (piece & 7);
-      rows.dy[s] = ld(dy_rs, tile_off, 0);
-      rows.v[s] = ld(v_rs, tile_off, 0);
-    }
-    const int64_t ck_index =
-        p.ckpt16 ? (static_cast<int64_t>(seq) * heads + head) * (p.dense_t / 16) + 4 * seg
-                 : static_cast<int64_t>(seg) * heads + head;
-    const auto ck = buffer_rsrc(p.checkpoint + ck_index * kHead * kHead, kHead * kHead * 4);
+      for (int s = 0; s < 2; ++s) dst[s] = ld(r, prep_off, s * static_cast<int>(row_bytes));
+    };
+    auto tile2 = [&](const void* x, uint4 (&dst)[2]) {
+      const auto r = brs(x);
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        rows.s0[kb][j] = __uint_as_float(
-            __builtin_amdgcn_raw_buffer_load_b32(ck, s_off, (16 * kb + j) * kHead * 4, 0));
+      for (int s = 0; s < 2; ++s) {
+        const int tp_piece = tid + 256 * s;
+        dst[s] = ld(r, static_cast<uint32_t>(tp_piece >> 3) * row_bytes + 16 * (tp_piece & 7), 0);
       }
+    };
+    auto ckpt = [&](int kb0) {
+      const auto ck = buffer_rsrc(c.valid ? p.checkpoint + c.ck_index * kHead * kHead : nullptr,
+                                  c.valid ? kHead * kHead * 4 : 0);
+#pragma unroll
+      for (int kb = kb0; kb < kb0 + 2; ++kb) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          rows.s0[kb][j] = __uint_as_float(
+              __builtin_amdgcn_raw_buffer_load_b32(ck, s_off, (16 * kb + j) * kHead * 4, 0));
+        }
+      }
+    };
+    if (piece == 0) {
+      rows2(p.decay, rows.w);
+      rows2(p.r, rows.r);
+    } else if (piece == 1) {
+      rows2(p.k, rows.k);
+      rows2(p.a, rows.a);
+    } else if (piece == 2) {
+      rows2(p.b, rows.b);
+      tile2(p.dy, rows.dy);
+    } else if (piece == 3) {
+      tile2(p.v, rows.v);
+      ckpt(0);
+    } else {
+      ckpt(2);
     }
+  };
+  auto load_chunk = [&](int seg, BwdRows& rows) {
+    const ChunkSrc c = chunk_src(seg);
+#pragma unroll
+    for (int piece = 0; piece < 5; ++piece) load_piece(c, rows, piece);
   };
 
   BwdRows rows;
@@ -573,12 +615,16 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
     f32x4 S0[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) S0[kb] = rows.s0[kb];
-    // The rows are in LDS now: start loading the chunk before this one.
-    if (seg - 1 >= seg_lo) {
-      load_chunk(seg - 1, rows);
-      loaded = seg - 1;
-    }
+    // The rows are in LDS now: the chunk before this one is loaded during
+    // the intra-chunk products (below, or here on the fail-closed path).
+    // Unconditional: before the first segment the ranges are empty (a
+    // skipped load would make the compiler's in-order wait counts too
+    // strict).
+    const ChunkSrc prev = chunk_src(seg - 1);
+    if (prev.valid) loaded = seg - 1;
     if (failed) {
+#pragma unroll
+      for (int piece = 0; piece < 5; ++piece) load_piece(prev, rows, piece);
       // Fail closed: NaN gradients for this chunk, and for every earlier one
       // (the adjoint would be wrong from here on).
       // Rows past the chunk's tokens fall outside the buffer range and are
@@ -596,7 +642,7 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
       }
       continue;
     }
-    intra_bwd(sm);
+    intra_bwd(sm, [&](int piece) { load_piece(prev, rows, piece); });
 
     // ---------------------------------------------------------- columns --
     // V and scale * dY in operand layout: lane (g, n) holds X[16q + 4g + e][16w + n].

@@ -307,7 +307,13 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
 // wave w does all four matrices of its diagonal pair (w, w), then three of
 // the twelve off-diagonal half-pairs ({Lab, Arb} share Bh_q, {Lak, Ark}
 // share Kh_q; both share At_p and Rt_p).
-__device__ void intra_chunk(ChunkSmem& sm) {
+//
+// issue(i), i = 0..5, is called between the product groups: the caller
+// issues one sixth of the next chunk's row loads there, so the loads enter
+// the memory system while the products run instead of stalling the wave on
+// a burst of 12 outstanding 16-byte loads.
+template <typename Issue>
+__device__ __forceinline__ void intra_chunk(ChunkSmem& sm, Issue&& issue) {
   // MFMA phases run at raised wave priority: the other workgroup on the CU
   // is then usually in its VALU-heavy prepare, and the arbiter keeps the
   // matrix pipe fed from this one.
@@ -359,7 +365,9 @@ __device__ void intra_chunk(ChunkSmem& sm) {
   };
 
   // Diagonal pair first; its Lab block feeds the inverse.
+  issue(0);
   group(wave, wave, true, true);
+  issue(1);
   // T_pp = (I - L)^{-1} for the strictly lower 16 x 16 block L = Lab_pp:
   // L^16 = 0, so (I - L)^{-1} = (I + L)(I + L^2)(I + L^4)(I + L^8). All
   // factors are polynomials in L and commute. With X_R the register layout
@@ -394,6 +402,7 @@ __device__ void intra_chunk(ChunkSmem& sm) {
     t = mfma16(p8c, to_operand(t), t);  // T  = T3 + P8 T3
     lds_store_transposed(sm.tinv[wave], kTriStride, g, n, t);
   }
+  issue(2);
 
   // Off-diagonal half-pairs: pair index item / 2 over (1,0) (2,0) (2,1)
   // (3,0) (3,1) (3,2), half item % 2 ({Lab, Arb} or {Lak, Ark}).
@@ -404,6 +413,7 @@ __device__ void intra_chunk(ChunkSmem& sm) {
     const int p = pair < 1 ? 1 : (pair < 3 ? 2 : 3);
     const int q = pair - (p * (p - 1)) / 2;
     group(p, q, (item & 1) == 0, (item & 1) == 1);
+    issue(3 + r);
   }
   __builtin_amdgcn_s_setprio(0);
   __syncthreads();
@@ -712,32 +722,35 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
   // Per-lane byte offset inside a chunk's rows in the prepare layout (token
   // 16w + 2tp [+1], features 8kg..8kg+7).
   const uint32_t prep_off = static_cast<uint32_t>(16 * wave + 2 * tp) * row_bytes + 16 * kg;
-  auto load_rows = [&](ChunkRows& rows, int c0, int ntok) {
+  // Row loads of one chunk in six pieces (piece i: tensor w, a, r, b, k, v
+  // in prepare's order of use), two 16-byte loads per lane each.
+  auto load_piece = [&](ChunkRows& rows, int c0, int ntok, int piece) {
     const int64_t base = (static_cast<int64_t>(c0) * heads + head) * kHead;
     const uint32_t bytes = static_cast<uint32_t>(ntok) * row_bytes;
-    auto rs = [&](const void* x) { return buffer_rsrc(static_cast<const S16c*>(x) + base, bytes); };
-    const auto rr = rs(p.r), rw = rs(p.decay), rk = rs(p.k), ra = rs(p.a), rb = rs(p.b);
+    const void* src = piece == 0 ? p.decay : piece == 1 ? p.a : piece == 2 ? p.r
+                    : piece == 3 ? p.b : piece == 4 ? p.k : p.v;
+    const auto rs = buffer_rsrc(static_cast<const S16c*>(src) + base, bytes);
+    uint4* dst = piece == 0 ? rows.w : piece == 1 ? rows.a : piece == 2 ? rows.r
+               : piece == 3 ? rows.b : piece == 4 ? rows.k : rows.v;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const int so = s * static_cast<int>(row_bytes);
-      auto ld = [&](__amdgpu_buffer_rsrc_t r) {
-        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, prep_off, so, 0);
-        return make_uint4(x.x, x.y, x.z, x.w);
-      };
-      rows.r[s] = ld(rr);
-      rows.w[s] = ld(rw);
-      rows.k[s] = ld(rk);
-      rows.a[s] = ld(ra);
-      rows.b[s] = ld(rb);
+      uint32_t off;
+      int so;
+      if (piece == 5) {
+        const int v_piece = tid + 256 * s;
+        off = static_cast<uint32_t>(v_piece >> 3) * row_bytes + 16 * (v_piece & 7);
+        so = 0;
+      } else {
+        off = prep_off;
+        so = s * static_cast<int>(row_bytes);
+      }
+      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs, off, so, 0);
+      dst[s] = make_uint4(x.x, x.y, x.z, x.w);
     }
-    const auto rv = rs(p.v);
+  };
+  auto load_rows = [&](ChunkRows& rows, int c0, int ntok) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int piece = tid + 256 * s;
-      const uint32_t off = static_cast<uint32_t>(piece >> 3) * row_bytes + 16 * (piece & 7);
-      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
-      rows.v[s] = make_uint4(x.x, x.y, x.z, x.w);
-    }
+    for (int piece = 0; piece < 6; ++piece) load_piece(rows, c0, ntok, piece);
   };
 
   ChunkRows rows;
@@ -809,9 +822,19 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
             hi = min(spans.block[0] ? 16 : 4, ntok);
             continue;
           }
-          if (has_next) load_rows(rows, nc0, min(kChunk, nend - nc0));
         }
-        intra_chunk(sm);
+        // A whole chunk's pass requests the next chunk's rows in pieces
+        // during the products. The request is unconditional: with no next
+        // chunk the range is empty and the loads return zeros (a skipped
+        // load would make the compiler's in-order wait counts too strict).
+        if (whole) {
+          intra_chunk(sm, [&](int piece) {
+            load_piece(rows, has_next ? nc0 : c0, has_next ? min(kChunk, nend - nc0) : 0,
+                       piece);
+          });
+        } else {
+          intra_chunk(sm, [](int) {});
+        }
         {
           const int64_t base = (static_cast<int64_t>(c0) * heads + head) * kHead;
           const auto out_rs = buffer_rsrc(static_cast<S16c*>(p.out) + base,
@@ -830,7 +853,7 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
         const int q = lo >> 4;
         hi = min(lo + (spans.block_ok(q) ? 16 : 4), min(16 * q + 16, ntok));
       }
-      if (!whole && has_next) load_rows(rows, nc0, min(kChunk, nend - nc0));
+      if (!whole) load_rows(rows, has_next ? nc0 : c0, has_next ? min(kChunk, nend - nc0) : 0);
     }
   }
 
