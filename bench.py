@@ -41,18 +41,18 @@ BF16_PEAK_TFLOPS = 2516.6
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, mean KiB per dispatch of each
 # kernel at its bench workload (the traffic summaries under profiles/ give the
 # runs and their commands). Calibration: a 256 MiB device copy (--workload copy) reads
-# FETCH_SIZE 131085.1 KiB and WRITE_SIZE 262144.0 KiB per dispatch, so fetched
-# bytes are FETCH_SIZE * 1024 * (262144 / 131085.1) and written bytes
+# FETCH_SIZE 131085.3 KiB and WRITE_SIZE 262144.0 KiB per dispatch, so fetched
+# bytes are FETCH_SIZE * 1024 * (262144 / 131085.3) and written bytes
 # WRITE_SIZE * 1024.
 _COPY_KIB = 262144.0
-_COPY_FETCH_KIB = 131085.1
+_COPY_FETCH_KIB = 131085.3
 _COPY_WRITE_KIB = 262144.0
 PMC_KIB = {  # kernel -> (FETCH_SIZE, WRITE_SIZE)
-    "recurrent_fp32_kernel<64,64,64,Bf16,kRawW>": (85810.9, 165163.6),
-    "chunk_fwd_kernel<Bf16,kRawW,float>": (790724.0, 270338.2),
-    "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": (790893.0, 1318970.7),
-    "chunk_bwd_kernel<Bf16,kRawW>": (1730522.7, 2159326.8),
-    "recurrent_fp32_kernel<64,64,64,F16,kLogits,kFp16>": (44898.3, 83200.2),
+    "recurrent_fp32_kernel<64,64,64,Bf16,kRawW>": (85812.5, 165181.9),
+    "chunk_fwd_kernel<Bf16,kRawW,float>": (790726.8, 270851.7),
+    "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": (803353.1, 1319761.2),
+    "chunk_bwd_kernel<Bf16,kRawW>": (1988333.6, 2456509.8),
+    "recurrent_fp32_kernel<64,64,64,F16,kLogits,kFp16>": (44896.8, 83200.7),
 }
 
 
@@ -233,6 +233,8 @@ def bench_decode(args, fp16_state=False):
     slots = torch.arange(batch, device=dev, dtype=torch.int32)
 
     stream = torch.cuda.Stream(device=dev)
+    # Inputs were made on the default stream: order the side stream after them.
+    stream.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(stream):
         ticket = prepare_recurrent_metadata(cu, slots, total_tokens=batch,
                                             state_pool_size=batch, max_seqlen=1)
@@ -399,6 +401,25 @@ def cpu_baseline_prefill(t_len, heads_total, seconds):
     }
 
 
+def _kernel_ms(fn, steps, stream, warmup=2):
+    """Mean ms per call of ``fn`` (kernel launches only, no host work in the
+    loop), timed with HIP events on ``stream``, the stream fn launches on."""
+    import torch
+
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            fn()
+        stream.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            fn()
+        end.record(stream)
+        end.synchronize()
+    return start.elapsed_time(end) / steps
+
+
 def bench_prefill(args):
     """chunked prefill, B=16, T=4096, H=32, D=64, bf16 io,
     raw retention u ~ U(-8, 0), fp32 state pool updated in place."""
@@ -420,6 +441,8 @@ def bench_prefill(args):
     cu = torch.arange(0, n_tok + 1, t_len, device=dev, dtype=torch.int32)
     slots = torch.arange(batch, device=dev, dtype=torch.int32)
     stream = torch.cuda.Stream(device=dev)
+    # Inputs were made on the default stream: order the side stream after them.
+    stream.wait_stream(torch.cuda.current_stream(dev))
 
     def step():
         ops.chunk_forward_internal(tok["r"], tok["w"], tok["k"], tok["v"], tok["a"],
@@ -437,17 +460,30 @@ def bench_prefill(args):
         end.record(stream)
         end.synchronize()
     ms = start.elapsed_time(end) / args.prefill_steps
+    # The kernel alone: the op above validates the metadata on every call
+    # (two small kernels); through the C ABI the validated snapshot is reused.
+    from flashrwkv_amd import capi
+    status, cu_snap, slot_snap = capi.metadata_validate(cu, slots, n_tok, batch)
+    out_t = torch.empty_like(tok["v"])
+    kernel_ms = _kernel_ms(lambda: capi.chunk_forward(
+        tok["r"], tok["w"], tok["k"], tok["v"], tok["a"], tok["b"], state_pool=pool,
+        cu_seqlens=cu_snap, state_indices=slot_snap, metadata_status=status, output=out_t,
+        decay_mode=DECAY_RAW_W), args.prefill_steps, stream)
     chunk_heads = batch * heads * (t_len // 64)
     flops = chunk_heads * chunk_flops()
     nbytes = n_tok * heads * 7 * d * 2 + 2 * batch * heads * d * d * 4
-    tflops = flops / (ms * 1e-3) / 1e12
-    gbps = nbytes / (ms * 1e-3) / 1e9
+    tflops = flops / (kernel_ms * 1e-3) / 1e12
+    gbps = nbytes / (kernel_ms * 1e-3) / 1e9
     attainable = min(BF16_PEAK_TFLOPS, flops / nbytes * HBM_PEAK_GBPS / 1e3)
     out = {
         "workload": "wkv7_chunked_prefill_cfg3: B=16, T=4096, H=32, D=64, bf16 io, chunk 64, "
                     "raw retention u~U(-8,0), fp32 state pool",
         "ms_per_step": round(ms, 4),
         "tokens_per_s": round(n_tok / (ms * 1e-3), 1),
+        "kernel_ms": round(kernel_ms, 4),
+        "kernel_tokens_per_s": round(n_tok / (kernel_ms * 1e-3), 1),
+        "timing": "ms_per_step: the op per call (metadata validation + kernel); kernel_ms "
+                  "and the roofline: the kernel alone through the C ABI",
         "steps": args.prefill_steps,
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
                      "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
@@ -492,6 +528,8 @@ def bench_prefill_varlen(args):
     slots = torch.arange(batch, device=dev, dtype=torch.int32)
     pool = torch.zeros((batch, heads, d, d), device=dev)
     stream = torch.cuda.Stream(device=dev)
+    # Inputs were made on the default stream: order the side stream after them.
+    stream.wait_stream(torch.cuda.current_stream(dev))
 
     def step():
         ops.chunk_forward_internal(tok["r"], tok["w"], tok["k"], tok["v"], tok["a"],
@@ -509,17 +547,25 @@ def bench_prefill_varlen(args):
         end.record(stream)
         end.synchronize()
     ms = start.elapsed_time(end) / args.prefill_steps
+    from flashrwkv_amd import capi
+    status, cu_snap, slot_snap = capi.metadata_validate(cu, slots, n_tok, batch)
+    out_t = torch.empty_like(tok["v"])
+    kernel_ms = _kernel_ms(lambda: capi.chunk_forward(
+        tok["r"], tok["w"], tok["k"], tok["v"], tok["a"], tok["b"], state_pool=pool,
+        cu_seqlens=cu_snap, state_indices=slot_snap, metadata_status=status, output=out_t,
+        decay_mode=DECAY_RAW_W), args.prefill_steps, stream)
     flops = heads * sum((length // 64) * chunk_flops() + chunk_flops(length % 64)
                         for length in lengths)
     nbytes = n_tok * heads * 7 * d * 2 + 2 * batch * heads * d * d * 4
-    tflops = flops / (ms * 1e-3) / 1e12
-    gbps = nbytes / (ms * 1e-3) / 1e9
+    tflops = flops / (kernel_ms * 1e-3) / 1e12
+    gbps = nbytes / (kernel_ms * 1e-3) / 1e9
     return {
         "workload": f"wkv7_chunked_prefill_cfg3_varlen: {batch} sequences, lengths "
                     f"U[128,4096] (seeded; N={n_tok}), H=32, D=64, bf16 io, u~U(-8,0), "
                     "fp32 pool",
         "ms_per_step": round(ms, 4),
         "tokens_per_s": round(n_tok / (ms * 1e-3), 1),
+        "kernel_ms": round(kernel_ms, 4),
         "achieved_TFLOPs": round(tflops, 2),
         "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
         "achieved_GBps": round(gbps, 1),
@@ -572,6 +618,27 @@ def bench_training(args):
     end.record()
     end.synchronize()
     ms = start.elapsed_time(end) / args.training_steps
+    # The two kernels alone through the C ABI (the autograd step above also
+    # clones S0, allocates outputs and gradients and splits no chunks here).
+    from flashrwkv_amd import capi
+    stream = torch.cuda.Stream(device=dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    raw = [t.detach() for t in leaves]
+    st_k = s0.detach().clone()
+    y_k = torch.empty_like(raw[3])
+    bnd = torch.empty((batch * (t_len // 64), heads, d, d), device=dev)
+    sda = torch.empty((n_tok, heads, d), device=dev)
+    grads_k = [torch.empty_like(t) for t in raw]
+    ds0_k = torch.empty_like(ds)
+    fwd_ms = _kernel_ms(lambda: capi.statetune_forward(
+        *raw, sequence_chunk_offsets=offsets, chunk_token_starts=starts,
+        chunk_token_ends=ends, state=st_k, output=y_k, boundary=bnd, state_dot_a=sda),
+        args.training_steps, stream)
+    bwd_ms = _kernel_ms(lambda: capi.statetune_backward(
+        *raw, sequence_chunk_offsets=offsets, chunk_token_starts=starts,
+        chunk_token_ends=ends, boundary=bnd, grad_output=dy, grad_final_state=ds,
+        grads=grads_k, grad_initial_state=ds0_k), args.training_steps, stream)
+    kernel_ms = fwd_ms + bwd_ms
     chunk_heads = batch * heads * (t_len // 64)
     flops = 3 * chunk_heads * chunk_flops()
     tok_bytes = n_tok * heads * d * 2
@@ -581,13 +648,16 @@ def bench_training(args):
     # backward: 6 token reads + dY, boundary read, 6 gradient writes, dS_T/dS0.
     nbytes = (6 + 1) * tok_bytes + 2 * boundary_bytes + 2 * state_bytes \
         + 7 * tok_bytes + boundary_bytes + 6 * tok_bytes + 2 * state_bytes
-    tflops = flops / (ms * 1e-3) / 1e12
-    gbps = nbytes / (ms * 1e-3) / 1e9
+    tflops = flops / (kernel_ms * 1e-3) / 1e12
+    gbps = nbytes / (kernel_ms * 1e-3) / 1e9
     out = {
         "workload": "wkv7_training_cfg4: chunked forward + backward (StateTune), B=8, T=4096, "
                     "H=64, D=64, chunk 64, bf16 io, raw retention, fp32 state and boundaries",
         "ms_per_step": round(ms, 4),
         "train_tokens_per_s": round(n_tok / (ms * 1e-3), 1),
+        "kernel_ms": {"forward": round(fwd_ms, 4), "backward": round(bwd_ms, 4)},
+        "timing": "ms_per_step: autograd forward + backward; kernel_ms and the roofline: "
+                  "the two kernels alone through the C ABI",
         "steps": args.training_steps,
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
