@@ -70,7 +70,7 @@ def _parse():
     p.add_argument("--steps", type=int, default=1000)
     p.add_argument("--warmup", type=int, default=50)
     p.add_argument("--workload", default="all",
-                   choices=("all", "decode", "decode_fp16", "prefill", "training",
+                   choices=("all", "decode", "decode_fp16", "decode_fused", "prefill", "training",
                             "recurrent_long", "copy"),
                    help="all: decode headline line plus the prefill, training and "
                         "long-sequence legs")
@@ -398,6 +398,114 @@ def cpu_baseline_prefill(t_len, heads_total, seconds):
         "sample": f"{reps} x (1 sequence x {sample_heads} heads x T={t_len}) through the fp64 "
                   f"C oracle, OpenMP over heads, {elapsed:.1f} s; token-heads/s divided by "
                   f"H={heads_total} (heads are independent)",
+    }
+
+
+def bench_decode_fused(args):
+    """The TMix chain around decode at config 1's shape (B=256, H=40, D=64, one
+    token per step, fp16 io, fp32 pool, decay logits, 4 rotating pool
+    replicas): the fused kernel (producer + WKV7 step + consumer) against the
+    same chain as three kernels (kk_a_gate, the recurrent op, lnx_rkvres_xg).
+    Both run from HIP graphs of 8 steps with a prepared ticket."""
+    import torch
+
+    import flashrwkv_amd
+    from flashrwkv_amd.tmix.wkv7 import DECAY_LOGITS, prepare_recurrent_metadata
+
+    ops = flashrwkv_amd._C.ops
+    dev = torch.device("cuda:0")
+    batch, heads, d = 256, 40, 64
+    c = heads * d
+    n_pools, n_tokens = 4, 8
+    gen = torch.Generator(device=dev).manual_seed(20260811)
+    f16 = torch.float16
+
+    def randn(*shape, s=1.0):
+        return torch.randn(shape, generator=gen, device=dev) * s
+
+    pools = [randn(batch, heads, d, d, s=0.1) for _ in range(n_pools)]
+    tokens = [{"r": randn(batch, heads, d).to(f16), "w": randn(batch, heads, d, s=2.0).to(f16),
+               "k": randn(batch, heads, d).to(f16), "v": randn(batch, heads, d).to(f16),
+               "a12": randn(batch, heads, d).to(f16),
+               "g": torch.sigmoid(randn(batch, heads, d)).to(f16)} for _ in range(n_tokens)]
+    vec = {"k_k": (1.0 + randn(c, s=0.3)).to(f16), "a0": randn(c, s=0.5).to(f16),
+           "k_a": torch.rand(c, generator=gen, device=dev).to(f16),
+           "r_k": randn(c, s=0.5).to(f16), "ln_w": (1.0 + randn(c, s=0.2)).to(f16),
+           "ln_b": randn(c, s=0.1).to(f16)}
+    cu = torch.arange(batch + 1, device=dev, dtype=torch.int32)
+    slots = torch.arange(batch, device=dev, dtype=torch.int32)
+    stream = torch.cuda.Stream(device=dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(stream):
+        ticket = prepare_recurrent_metadata(cu, slots, total_tokens=batch,
+                                            state_pool_size=batch, max_seqlen=1)
+
+        def fused(i):
+            t = tokens[i % n_tokens]
+            ops.recurrent_tmix_fused_forward(
+                cu, slots, pools[i % n_pools], t["r"], t["w"], t["k"], t["v"], t["a12"], t["g"],
+                vec["k_k"], vec["a0"], vec["k_a"], vec["r_k"], vec["ln_w"], vec["ln_b"], 1.0,
+                DECAY_LOGITS, None, ticket)
+
+        y_bufs = [torch.empty((batch, heads, d), device=dev, dtype=f16) for _ in range(n_tokens)]
+
+        def chain(i):
+            t = tokens[i % n_tokens]
+            flat = lambda x: x.reshape(batch, c)
+            new_k, neg_kk, kka = ops.tmix_kk_a_gate_forward_varlen(
+                flat(t["k"]), vec["k_k"], vec["a0"], flat(t["a12"]), vec["k_a"], 64, batch, 1)
+            y = y_bufs[i % n_tokens]
+            ops.recurrent_fp32_from_decay_logits(
+                cu, slots, pools[i % n_pools], t["r"], t["w"], new_k.reshape(batch, heads, d),
+                t["v"], neg_kk.reshape(batch, heads, d), kka.reshape(batch, heads, d), y, 1.0,
+                None, ticket, 1)
+            ops.tmix_lnx_rkvres_xg_forward_varlen(
+                flat(y), flat(t["r"]), new_k, flat(t["v"]), vec["r_k"], vec["ln_w"],
+                vec["ln_b"], flat(t["g"]), 64, batch, 1)
+
+        def graph_ms(step):
+            for i in range(8):
+                step(i)
+            stream.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for i in range(8):
+                    step(i)
+            reps = max(1, args.steps // 8)
+            for _ in range(max(1, args.warmup // 8)):
+                g.replay()
+            stream.synchronize()
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for _ in range(reps):
+                g.replay()
+            end.record(stream)
+            end.synchronize()
+            return start.elapsed_time(end) / (8 * reps)
+
+        fused_ms = graph_ms(fused)
+        chain_ms = graph_ms(chain)
+    units = batch * heads
+    fused_bytes = units * (2 * d * d * 4 + 7 * d * 2)
+    # kk_a_gate: read k, a12, write 3; WKV: 6 reads + y; lnx: 5 reads + out.
+    chain_bytes = units * (2 * d * d * 4 + (5 + 7 + 6) * d * 2)
+    gbps = fused_bytes / (fused_ms * 1e-3) / 1e9
+    return {
+        "workload": "tmix_chain_decode: kk_a_gate -> WKV7 step -> lnx_rkvres_xg at B=256, "
+                    "H=40, D=64, T=1 per step, fp16 io, fp32 state pool, decay logits, "
+                    f"{n_pools} rotating pool replicas",
+        "fused": {"ms_per_step": round(fused_ms, 6),
+                  "tokens_per_s": round(batch / (fused_ms * 1e-3), 1),
+                  "kernel": "recurrent_tmix_fused_kernel<F16,kLogits>",
+                  "roofline": {"bound": "hbm", "achieved": round(gbps, 1),
+                               "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                               "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                               "algorithmic_bytes_per_launch": fused_bytes}},
+        "three_kernel_chain": {"ms_per_step": round(chain_ms, 6),
+                               "tokens_per_s": round(batch / (chain_ms * 1e-3), 1),
+                               "algorithmic_bytes_per_step": chain_bytes},
+        "speedup": round(chain_ms / fused_ms, 3),
     }
 
 
@@ -810,10 +918,13 @@ def main():
         line = {"metric": METRIC, "recurrent_long": bench_recurrent_long(args)}
     elif args.workload == "decode_fp16":
         line = {"metric": METRIC, "decode_fp16_state": bench_decode(args, fp16_state=True)}
+    elif args.workload == "decode_fused":
+        line = {"metric": METRIC, "decode_tmix_fused": bench_decode_fused(args)}
     else:
         line = bench_decode(args)
         if args.workload == "all":
             line["decode_fp16_state"] = bench_decode(args, fp16_state=True)
+            line["decode_tmix_fused"] = bench_decode_fused(args)
             line["chunked_prefill"] = bench_prefill(args)
             line["chunked_prefill"]["varlen"] = bench_prefill_varlen(args)
             line["training"] = bench_training(args)

@@ -157,3 +157,18 @@ def recurrent_fp16_advance_i32_varlen(query_start_loc, state_indices, elapsed_st
 def recurrent_add_vec_forward_varlen(x, vec):
     """Reference infer_recurrent_fp16_forward_varlen.cpp:193-208."""
     return ops.recurrent_add_vec_forward_varlen(x, vec)
+
+
+def tmix_kk_a_gate_forward_varlen(k, k_k, a0, a12, k_a, head_size=64, batch_size=1,
+                                  max_seqlen=1):
+    """Reference kk_a_gate/infer_fp16_forward_varlen.cpp:41-85: returns (new_k, neg_kk, kka)."""
+    return ops.tmix_kk_a_gate_forward_varlen(k, k_k, a0, a12, k_a, int(head_size),
+                                             int(batch_size), int(max_seqlen))
+
+
+def tmix_lnx_rkvres_xg_forward_varlen(x, r, k, v, r_k, weight, bias, g, head_size=64,
+                                      batch_size=1, max_seqlen=1):
+    """Reference lnx_rkvres_xg/infer_fp16_forward_varlen.cpp:40-98."""
+    return ops.tmix_lnx_rkvres_xg_forward_varlen(x, r, k, v, r_k, weight, bias, g,
+                                                 int(head_size), int(batch_size),
+                                                 int(max_seqlen))

@@ -39,6 +39,9 @@ SIGNATURES = {
     "frwkv_advance_i32": [_VP, _I64, _I32, _VP],
     "frwkv_advance_i32_varlen": [_I32] * 2 + [_VP] * 5,
     "frwkv_add_vec": [_I64, _I32] + [_VP] * 4,
+    "frwkv_kk_a_gate": [_INT, _I64, _I32, _I32] + [_VP] * 9,
+    "frwkv_lnx_rkvres_xg": [_INT, _I64, _I32, _I32] + [_VP] * 10,
+    "frwkv_recurrent_tmix_fused_forward": [_INT] * 2 + [_I32] * 5 + [_VP] * 18 + [_F32, _VP],
 }
 
 _LIB = None
@@ -189,3 +192,32 @@ def advance_i32_varlen(elapsed_state_pool, *, cu_seqlens, state_indices, metadat
 def add_vec(x, vec, output):
     rows, channels = x.shape
     _check(library().frwkv_add_vec(rows, channels, _p(x), _p(vec), _p(output), _stream()))
+
+
+def kk_a_gate(k, k_k, a0, a12, k_a, *, new_k, neg_kk, kka, head_size=64):
+    """TMix producer on packed ``[N, C]`` rows (C = H * head_size)."""
+    n, c = k.shape
+    _check(library().frwkv_kk_a_gate(
+        DTYPE[k.dtype], n, c // head_size, head_size, _p(k), _p(k_k), _p(a0), _p(a12),
+        _p(k_a), _p(new_k), _p(neg_kk), _p(kka), _stream()))
+
+
+def lnx_rkvres_xg(x, r, k, v, r_k, weight, bias, g, *, output, head_size=64):
+    """TMix consumer on packed ``[N, C]`` rows (C = H * head_size)."""
+    n, c = x.shape
+    _check(library().frwkv_lnx_rkvres_xg(
+        DTYPE[x.dtype], n, c // head_size, head_size, _p(x), _p(r), _p(k), _p(v), _p(r_k),
+        _p(weight), _p(bias), _p(g), _p(output), _stream()))
+
+
+def recurrent_tmix_fused_forward(r, decay, k, v, a12, g, k_k, a0, k_a, r_k, ln_weight,
+                                 ln_bias, *, state_pool, cu_seqlens, state_indices,
+                                 metadata_status, output, scale=1.0, decay_mode=DECAY_LOGITS,
+                                 decay_bias=None):
+    """Fused kk_a_gate -> WKV7 -> lnx_rkvres_xg (head size 64, fp32 pool)."""
+    n, h, d = r.shape
+    _check(library().frwkv_recurrent_tmix_fused_forward(
+        DTYPE[r.dtype], decay_mode, state_indices.numel(), h, d, n, state_pool.shape[0],
+        _p(cu_seqlens), _p(state_indices), _p(metadata_status), _p(state_pool), _p(r),
+        _p(decay), _p(decay_bias), _p(k), _p(v), _p(a12), _p(g), _p(k_k), _p(a0), _p(k_a),
+        _p(r_k), _p(ln_weight), _p(ln_bias), _p(output), float(scale), _stream()))

@@ -1040,6 +1040,136 @@ Tensor recurrent_add_vec_forward_varlen(Tensor x, Tensor vec) {
 
 }  // namespace
 
+// ------------------------------------------- TMix producer and consumer ---
+
+void check_half(const Tensor& t, const Tensor& ref, const char* name) {
+  check_device_contiguous(t, name);
+  TORCH_CHECK(t.device() == ref.device(), name, " must be on the same device as ",
+              &ref == &t ? "itself" : "the first input");
+  TORCH_CHECK(t.scalar_type() == at::kHalf, name, " must be float16");
+}
+
+void check_gate_common(const Tensor& x, const char* name, int64_t head_size,
+                       int64_t batch_size, int64_t max_seqlen) {
+  TORCH_CHECK(head_size == 64 || head_size == 128 || head_size == 256,
+              "head_size must be one of 64, 128, or 256");
+  TORCH_CHECK(x.dim() == 2 && x.size(0) > 0 && x.size(1) > 0 && x.size(1) % head_size == 0,
+              name, " must have packed shape [total_tokens,H*head_size]");
+  TORCH_CHECK(batch_size > 0, "batch_size must be positive");
+  TORCH_CHECK(max_seqlen > 0, "max_seqlen must be positive");
+}
+
+// Reference tmix_kk_a_gate_forward_varlen (kk_a_gate/infer_fp16_forward_varlen.cpp:41-75).
+std::tuple<Tensor, Tensor, Tensor> tmix_kk_a_gate_forward_varlen(
+    Tensor k, Tensor k_k, Tensor a0, Tensor a12, Tensor k_a, int64_t head_size,
+    int64_t batch_size, int64_t max_seqlen) {
+  check_half(k, k, "k");
+  check_gate_common(k, "k", head_size, batch_size, max_seqlen);
+  const int64_t channels = k.size(1);
+  const std::pair<const Tensor*, const char*> vectors[] = {
+      {&k_k, "k_k"}, {&a0, "a0"}, {&k_a, "k_a"}};
+  for (const auto& item : vectors) {
+    check_half(*item.first, k, item.second);
+    TORCH_CHECK(item.first->dim() == 1 && item.first->size(0) == channels, item.second,
+                " must have shape [C]");
+  }
+  check_half(a12, k, "a12");
+  TORCH_CHECK(a12.sizes() == k.sizes(), "a12 must match k's packed shape");
+  c10::DeviceGuard guard(k.device());
+  Tensor new_k = at::empty_like(k), neg_kk = at::empty_like(k), kka = at::empty_like(k);
+  check_rc(frwkv_kk_a_gate(FRWKV_DTYPE_F16, k.size(0),
+                           static_cast<int32_t>(channels / head_size),
+                           static_cast<int32_t>(head_size), k.data_ptr(), k_k.data_ptr(),
+                           a0.data_ptr(), a12.data_ptr(), k_a.data_ptr(), new_k.data_ptr(),
+                           neg_kk.data_ptr(), kka.data_ptr(), current_stream(k)));
+  return {new_k, neg_kk, kka};
+}
+
+// Reference tmix_lnx_rkvres_xg_forward_varlen (lnx_rkvres_xg/infer_fp16_forward_varlen.cpp:40-89).
+Tensor tmix_lnx_rkvres_xg_forward_varlen(Tensor x, Tensor r, Tensor k, Tensor v, Tensor r_k,
+                                         Tensor weight, Tensor bias, Tensor g,
+                                         int64_t head_size, int64_t batch_size,
+                                         int64_t max_seqlen) {
+  check_half(x, x, "x");
+  check_gate_common(x, "x", head_size, batch_size, max_seqlen);
+  const int64_t channels = x.size(1);
+  const std::pair<const Tensor*, const char*> tokens[] = {
+      {&r, "r"}, {&k, "k"}, {&v, "v"}, {&g, "g"}};
+  for (const auto& item : tokens) {
+    check_half(*item.first, x, item.second);
+    TORCH_CHECK(item.first->sizes() == x.sizes(), item.second, " must match x's packed shape");
+  }
+  const std::pair<const Tensor*, const char*> vectors[] = {
+      {&r_k, "r_k"}, {&weight, "weight"}, {&bias, "bias"}};
+  for (const auto& item : vectors) {
+    check_half(*item.first, x, item.second);
+    TORCH_CHECK(item.first->dim() == 1 && item.first->size(0) == channels, item.second,
+                " must have shape [C]");
+  }
+  c10::DeviceGuard guard(x.device());
+  Tensor out = at::empty_like(x);
+  check_rc(frwkv_lnx_rkvres_xg(FRWKV_DTYPE_F16, x.size(0),
+                               static_cast<int32_t>(channels / head_size),
+                               static_cast<int32_t>(head_size), x.data_ptr(), r.data_ptr(),
+                               k.data_ptr(), v.data_ptr(), r_k.data_ptr(), weight.data_ptr(),
+                               bias.data_ptr(), g.data_ptr(), out.data_ptr(),
+                               current_stream(x)));
+  return out;
+}
+
+// Fused chain (no reference counterpart): kk_a_gate -> WKV7 step -> lnx_rkvres_xg.
+// Token tensors [N,H,64] fp16/bf16, vectors [H*64] of the same dtype, fp32
+// pool [slots,H,64,64] updated in place; returns the consumer's output.
+Tensor recurrent_tmix_fused_forward(Tensor query_start_loc, Tensor state_indices,
+                                    Tensor state, Tensor r, Tensor decay, Tensor k, Tensor v,
+                                    Tensor a12, Tensor g, Tensor k_k, Tensor a0, Tensor k_a,
+                                    Tensor r_k, Tensor ln_weight, Tensor ln_bias, double scale,
+                                    int64_t decay_mode, std::optional<Tensor> decay_bias,
+                                    std::optional<TicketPtr> validated_metadata) {
+  TORCH_CHECK(decay_mode == FRWKV_DECAY_LOGITS || decay_mode == FRWKV_DECAY_RAW_W,
+              "decay_mode must be 0 (logits) or 1 (raw retention)");
+  Tensor output = at::empty_like(v);
+  // The layout checks of the recurrent op, with a12 and g in the a and b places.
+  check_recurrent_layout(query_start_loc, state_indices, state, r, decay, k, v, a12, g, output,
+                         scale, /*allow_fp32_tokens=*/false);
+  TORCH_CHECK(state.size(2) == 64, "the fused TMix chain supports head size 64, got ",
+              state.size(2));
+  const int64_t channels = state.size(1) * 64;
+  const std::pair<const Tensor*, const char*> vectors[] = {
+      {&k_k, "k_k"}, {&a0, "a0"}, {&k_a, "k_a"},
+      {&r_k, "r_k"}, {&ln_weight, "ln_weight"}, {&ln_bias, "ln_bias"}};
+  for (const auto& item : vectors) {
+    check_device_contiguous(*item.first, item.second);
+    check_same_device(state, *item.first, item.second);
+    TORCH_CHECK(item.first->scalar_type() == r.scalar_type(), item.second,
+                " must match the token tensor dtype");
+    TORCH_CHECK(item.first->numel() == channels, item.second, " must have shape [H*D]");
+  }
+  check_decay_bias(decay_bias, state, r);
+  TORCH_CHECK(!(decay_bias.has_value() && decay_mode == FRWKV_DECAY_RAW_W),
+              "decay_bias is only defined for decay logits");
+  c10::DeviceGuard guard(state.device());
+  Prepared launch;
+  if (validated_metadata.has_value() && validated_metadata->defined()) {
+    (*validated_metadata)->check_compatible(query_start_loc, state_indices, r.size(0),
+                                            state.size(0), -1);
+    launch = (*validated_metadata)->prepared();
+  } else {
+    launch = device_prepare(query_start_loc, state_indices, r.size(0), state.size(0));
+  }
+  check_rc(frwkv_recurrent_tmix_fused_forward(
+      io_code(r.scalar_type()), static_cast<int>(decay_mode),
+      static_cast<int32_t>(state_indices.numel()), static_cast<int32_t>(state.size(1)), 64,
+      static_cast<int32_t>(r.size(0)), static_cast<int32_t>(state.size(0)),
+      launch.cu_snapshot.data_ptr<int32_t>(), launch.slot_snapshot.data_ptr<int32_t>(),
+      launch.status.data_ptr<int32_t>(), state.data_ptr<float>(), r.data_ptr(),
+      decay.data_ptr(), decay_bias.has_value() ? decay_bias->data_ptr() : nullptr, k.data_ptr(),
+      v.data_ptr(), a12.data_ptr(), g.data_ptr(), k_k.data_ptr(), a0.data_ptr(), k_a.data_ptr(),
+      r_k.data_ptr(), ln_weight.data_ptr(), ln_bias.data_ptr(), output.data_ptr(),
+      static_cast<float>(scale), current_stream(state)));
+  return output;
+}
+
 TORCH_LIBRARY(flashrwkv_amd, m) {
   m.class_<MetadataTicket>("MetadataTicket")
       .def("max_seqlen", [](const TicketPtr& t) { return t->max_seqlen(); })
@@ -1146,6 +1276,22 @@ TORCH_LIBRARY(flashrwkv_amd, m) {
       &recurrent_fp16_advance_i32_varlen);
   m.def("recurrent_add_vec_forward_varlen(Tensor x, Tensor vec) -> Tensor",
         &recurrent_add_vec_forward_varlen);
+  m.def(
+      "tmix_kk_a_gate_forward_varlen(Tensor k, Tensor k_k, Tensor a0, Tensor a12, Tensor k_a, "
+      "int head_size=64, int batch_size=1, int max_seqlen=1) -> (Tensor, Tensor, Tensor)",
+      &tmix_kk_a_gate_forward_varlen);
+  m.def(
+      "tmix_lnx_rkvres_xg_forward_varlen(Tensor x, Tensor r, Tensor k, Tensor v, Tensor r_k, "
+      "Tensor weight, Tensor bias, Tensor g, int head_size=64, int batch_size=1, "
+      "int max_seqlen=1) -> Tensor",
+      &tmix_lnx_rkvres_xg_forward_varlen);
+  m.def(
+      "recurrent_tmix_fused_forward(Tensor query_start_loc, Tensor state_indices, "
+      "Tensor(a!) state, Tensor r, Tensor decay, Tensor k, Tensor v, Tensor a12, Tensor g, "
+      "Tensor k_k, Tensor a0, Tensor k_a, Tensor r_k, Tensor ln_weight, Tensor ln_bias, "
+      "float scale=1.0, int decay_mode=0, Tensor? decay_bias=None, "
+      "__torch__.torch.classes.flashrwkv_amd.MetadataTicket? validated_metadata=None) -> Tensor",
+      &recurrent_tmix_fused_forward);
 }
 
 // The reference's pretraining operator namespace (pretrain_recurrent_bf16_forward.cpp:50-53).

@@ -383,6 +383,226 @@ int dispatch_decay(const RecurrentArgs& p, int decay_mode) {
   return set_error(FRWKV_ERR_INVALID_ARGUMENT, "unknown decay mode %d", decay_mode);
 }
 
+// Fused TMix chain for decode and short sequences (head size 64, fp32 pool,
+// one wave per (sequence, head) state; lane layout as recurrent_fp32_kernel
+// <64, 64, 64>: lane (rg, cg) holds key rows 16rg..16rg+15 of value columns
+// 4cg..4cg+3). Per token it runs, without writing the intermediates:
+//   producer (reference kk_a_gate): u = k k_k, kk = u / max(|u|, 1e-12),
+//     gate = sigmoid(a0 + a12), k' = k (gate k_a + 1 - k_a);
+//   WKV7 step with k', a = -kk, b = kk gate (S += b (a^T S), the RWKV-7
+//     update as BASELINE's configs state it), y = scale S^T r;
+//   consumer (reference lnx_rkvres_xg): out = ((y - mean) rstd ln_w + ln_b
+//     + rkv v) g with rstd = 1 / sqrt(var + 64e-5), rkv = sum r k' r_k.
+// Norms over key features reduce across the four row groups (xor 16, 32),
+// norms over value columns across the 16 column-group lanes (xor 1..8).
+struct FusedTmixParams {
+  const void* a12;
+  const void* g;
+  const void* k_k;
+  const void* a0;
+  const void* k_a;
+  const void* r_k;
+  const void* ln_weight;
+  const void* ln_bias;
+};
+
+__device__ __forceinline__ float sigmoid_fast(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-kLog2E * x));
+}
+
+__device__ __forceinline__ float reduce_col_groups(float x) {
+#pragma unroll
+  for (int offset = 1; offset < 16; offset <<= 1) x += __shfl_xor(x, offset, 64);
+  return x;
+}
+
+template <typename T, DecayMode M>
+__global__ __launch_bounds__(64, 2) void recurrent_tmix_fused_kernel(
+    RecurrentKernelParams p, FusedTmixParams f,
+    const typename IoTraits<T>::storage* __restrict__ r_ptr,
+    const typename IoTraits<T>::storage* __restrict__ decay_ptr,
+    const typename IoTraits<T>::storage* __restrict__ bias_ptr,
+    const typename IoTraits<T>::storage* __restrict__ k_ptr,
+    const typename IoTraits<T>::storage* __restrict__ v_ptr,
+    typename IoTraits<T>::storage* __restrict__ out_ptr) {
+  using S = typename IoTraits<T>::storage;
+  constexpr int D = 64;
+  constexpr int kRpl = 16;
+  const int32_t num_heads = p.num_heads;
+  if (p.status != nullptr && p.status[0] != 0) {
+    fill_nan<T>(out_ptr, p.output_elements);
+    return;
+  }
+  const int lane = threadIdx.x & 63;
+  const int unit = blockIdx.x;
+  if (unit >= p.num_units) return;
+  const int seq = unit / num_heads;
+  const int head = unit % num_heads;
+  const int cg = lane % 16;
+  const int rg = lane / 16;
+  const int row0 = rg * kRpl;
+  const int col = 4 * cg;
+  const int32_t t_begin = __builtin_amdgcn_readfirstlane(p.cu_seqlens[seq]);
+  const int32_t t_end = __builtin_amdgcn_readfirstlane(p.cu_seqlens[seq + 1]);
+  const int32_t slot = __builtin_amdgcn_readfirstlane(p.slots[seq]);
+  if (t_begin < 0 || t_end > p.total_tokens || t_begin >= t_end || slot < 0 ||
+      slot >= p.state_pool_size) {
+    return;
+  }
+  float* sbase = static_cast<float*>(p.state) +
+                 ((static_cast<int64_t>(slot) * num_heads + head) * D) * D;
+  float4 s[kRpl];
+#pragma unroll
+  for (int j = 0; j < kRpl; ++j) {
+    s[j] = load_state4<StateKind::kFp32>(sbase + static_cast<int64_t>(row0 + j) * D + col);
+  }
+  // Per-head vectors: the lane's 16 key rows of k_k, a0, k_a, r_k (kept raw,
+  // decoded per token) and its 4 value columns of the norm weight and bias.
+  const int64_t hrow = static_cast<int64_t>(head) * D;
+  RawRow<T, kRpl> kkp_raw, a0_raw, ka_raw, rk_raw;
+  load_raw<T, kRpl>(static_cast<const S*>(f.k_k) + hrow + row0, kkp_raw);
+  load_raw<T, kRpl>(static_cast<const S*>(f.a0) + hrow + row0, a0_raw);
+  load_raw<T, kRpl>(static_cast<const S*>(f.k_a) + hrow + row0, ka_raw);
+  load_raw<T, kRpl>(static_cast<const S*>(f.r_k) + hrow + row0, rk_raw);
+  float lnw[4], lnb[4];
+  load_vec<T, 4>(static_cast<const S*>(f.ln_weight) + hrow + col, lnw);
+  load_vec<T, 4>(static_cast<const S*>(f.ln_bias) + hrow + col, lnb);
+  float bias[kRpl];
+  if (bias_ptr != nullptr) {
+    load_vec<T, kRpl>(bias_ptr + hrow + row0, bias);
+  } else {
+#pragma unroll
+    for (int j = 0; j < kRpl; ++j) bias[j] = 0.0f;
+  }
+
+  // Element j of a raw row (rows stay packed; decoding on use keeps the
+  // register count, and so the number of waves per SIMD, close to the plain
+  // decode kernel's).
+  auto at = [](const auto& raw, int j) {
+    const uint32_t w = raw.w[j >> 1];
+    return to_f32<T>(static_cast<uint16_t>((j & 1) ? (w >> 16) : (w & 0xffffu)));
+  };
+  for (int32_t t = t_begin; t < t_end; ++t) {
+    const int64_t base = (static_cast<int64_t>(t) * num_heads + head) * D;
+    RawRow<T, kRpl> a12_raw, w_raw, k_raw, r_raw;
+    load_raw<T, kRpl>(static_cast<const S*>(f.a12) + base + row0, a12_raw);
+    load_raw<T, kRpl>(decay_ptr + base + row0, w_raw);
+    load_raw<T, kRpl>(k_ptr + base + row0, k_raw);
+    load_raw<T, kRpl>(r_ptr + base + row0, r_raw);
+    float vv[4], gg[4];
+    load_vec<T, 4>(v_ptr + base + col, vv);
+    load_vec<T, 4>(static_cast<const S*>(f.g) + base + col, gg);
+
+    // Producer: the norm of u = k k_k over the head's 64 key features.
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRpl; ++j) {
+      const float u = at(k_raw, j) * at(kkp_raw, j);
+      ss = fmaf(u, u, ss);
+    }
+    const float inv =
+        __builtin_amdgcn_rcpf(fmaxf(__builtin_sqrtf(reduce_row_groups<4>(ss)), 1.0e-12f));
+    // WKV7 step. sa = S^T a with a = -kk; then, row by row, the rest of the
+    // producer (gate, b = kk gate, k' = k (gate k_a + 1 - k_a)), the update,
+    // y = S^T r and the residual dot rkv = sum r k' r_k. Each producer value
+    // is computed once, where it is used.
+    float4 sa = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < kRpl; ++j) {
+      const float a_j = -(at(k_raw, j) * at(kkp_raw, j) * inv);
+      sa.x = fmaf(a_j, s[j].x, sa.x);
+      sa.y = fmaf(a_j, s[j].y, sa.y);
+      sa.z = fmaf(a_j, s[j].z, sa.z);
+      sa.w = fmaf(a_j, s[j].w, sa.w);
+    }
+    sa.x = reduce_row_groups<4>(sa.x);
+    sa.y = reduce_row_groups<4>(sa.y);
+    sa.z = reduce_row_groups<4>(sa.z);
+    sa.w = reduce_row_groups<4>(sa.w);
+    float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+    float rkv = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRpl; ++j) {
+      const float kraw = at(k_raw, j);
+      const float kkn = kraw * at(kkp_raw, j) * inv;
+      const float gate = sigmoid_fast(at(a0_raw, j) + at(a12_raw, j));
+      const float ka = at(ka_raw, j);
+      const float b_j = kkn * gate;
+      const float k_j = kraw * fmaf(gate, ka, 1.0f - ka);
+      const float w = decay_retention<M>(at(w_raw, j) + bias[j]);
+      const float rj = at(r_raw, j);
+      rkv = fmaf(rj * k_j, at(rk_raw, j), rkv);
+      s[j].x = fmaf(w, s[j].x, fmaf(b_j, sa.x, k_j * vv[0]));
+      s[j].y = fmaf(w, s[j].y, fmaf(b_j, sa.y, k_j * vv[1]));
+      s[j].z = fmaf(w, s[j].z, fmaf(b_j, sa.z, k_j * vv[2]));
+      s[j].w = fmaf(w, s[j].w, fmaf(b_j, sa.w, k_j * vv[3]));
+      y.x = fmaf(rj, s[j].x, y.x);
+      y.y = fmaf(rj, s[j].y, y.y);
+      y.z = fmaf(rj, s[j].z, y.z);
+      y.w = fmaf(rj, s[j].w, y.w);
+    }
+    rkv = reduce_row_groups<4>(rkv);
+    const float x[4] = {p.scale * reduce_row_groups<4>(y.x), p.scale * reduce_row_groups<4>(y.y),
+                        p.scale * reduce_row_groups<4>(y.z), p.scale * reduce_row_groups<4>(y.w)};
+
+    // Consumer: per-head norm of the output, residual and gate.
+    const float mean = reduce_col_groups(x[0] + x[1] + x[2] + x[3]) * (1.0f / D);
+    float dev[4], sq = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      dev[c] = x[c] - mean;
+      sq = fmaf(dev[c], dev[c], sq);
+    }
+    const float rstd = __builtin_amdgcn_rsqf(reduce_col_groups(sq) * (1.0f / D) + 64.0e-5f);
+    float o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      o[c] = fmaf(dev[c] * rstd, lnw[c], fmaf(rkv, vv[c], lnb[c])) * gg[c];
+    }
+    if (rg == 0) store4<T>(out_ptr + base + col, o[0], o[1], o[2], o[3]);
+  }
+
+#pragma unroll
+  for (int j = 0; j < kRpl; ++j) {
+    store_state4<StateKind::kFp32>(sbase + static_cast<int64_t>(row0 + j) * D + col, s[j]);
+  }
+}
+
+template <typename T, DecayMode M>
+int launch_tmix_fused(const RecurrentArgs& a, const FusedTmixParams& f) {
+  using S = typename IoTraits<T>::storage;
+  RecurrentKernelParams kp{};
+  kp.num_heads = a.num_heads;
+  kp.num_units = a.num_sequences * a.num_heads;
+  kp.output_elements = static_cast<int64_t>(a.total_tokens) * a.num_heads * 64;
+  kp.total_tokens = a.total_tokens;
+  kp.state_pool_size = a.state_pool_size;
+  kp.cu_seqlens = a.cu;
+  kp.slots = a.slots;
+  kp.status = a.status;
+  kp.state = a.state;
+  kp.scale = a.scale;
+  hipLaunchKernelGGL((recurrent_tmix_fused_kernel<T, M>), dim3(kp.num_units), dim3(64), 0,
+                     a.stream, kp, f, static_cast<const S*>(a.r),
+                     static_cast<const S*>(a.decay), static_cast<const S*>(a.bias),
+                     static_cast<const S*>(a.k), static_cast<const S*>(a.v),
+                     static_cast<S*>(a.out));
+  return check_launch("recurrent_tmix_fused_kernel");
+}
+
+template <typename T>
+int dispatch_tmix_fused(const RecurrentArgs& a, const FusedTmixParams& f, int decay_mode) {
+  if (decay_mode == FRWKV_DECAY_LOGITS) return launch_tmix_fused<T, DecayMode::kLogits>(a, f);
+  if (decay_mode == FRWKV_DECAY_RAW_W) {
+    if (a.bias != nullptr) {
+      return set_error(FRWKV_ERR_INVALID_ARGUMENT,
+                       "decay_bias is only defined for the logits decay mode");
+    }
+    return launch_tmix_fused<T, DecayMode::kRawW>(a, f);
+  }
+  return set_error(FRWKV_ERR_INVALID_ARGUMENT, "unknown decay mode %d", decay_mode);
+}
+
 }  // namespace
 }  // namespace frwkv
 
@@ -486,4 +706,53 @@ extern "C" int frwkv_recurrent_fp16_forward(
                   static_cast<hipStream_t>(stream)};
   p.elapsed = elapsed_state_pool;
   return dispatch_head_size<F16, DecayMode::kLogits, StateKind::kFp16>(p);
+}
+
+// Fused TMix chain (producer + WKV7 step + consumer) on the fp32 pool, head
+// size 64; see recurrent_tmix_fused_kernel.
+extern "C" int frwkv_recurrent_tmix_fused_forward(
+    int io_dtype, int decay_mode, int32_t num_sequences, int32_t num_heads,
+    int32_t head_size, int32_t total_tokens, int32_t state_pool_size,
+    const int32_t* cu_seqlens, const int32_t* state_indices,
+    const int32_t* metadata_status, float* state_pool, const void* r, const void* decay,
+    const void* decay_bias, const void* k, const void* v, const void* a12, const void* g,
+    const void* k_k, const void* a0, const void* k_a, const void* r_k,
+    const void* ln_weight, const void* ln_bias, void* output, float scale, void* stream) {
+  using namespace frwkv;
+  if (!cu_seqlens || !state_indices || !metadata_status || !state_pool || !r || !decay ||
+      !k || !v || !a12 || !g || !k_k || !a0 || !k_a || !r_k || !ln_weight || !ln_bias ||
+      !output) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT,
+                     "frwkv_recurrent_tmix_fused_forward: null pointer argument");
+  }
+  if (head_size != 64) {
+    return set_error(FRWKV_ERR_UNSUPPORTED,
+                     "frwkv_recurrent_tmix_fused_forward: head size 64 only, got %d",
+                     head_size);
+  }
+  if (num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 || total_tokens <= 0 ||
+      state_pool_size <= 0) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT,
+                     "frwkv_recurrent_tmix_fused_forward: sizes must be positive "
+                     "(B=%d, H=%d, N=%d, slots=%d)",
+                     num_sequences, num_heads, total_tokens, state_pool_size);
+  }
+  if (!__builtin_isfinite(scale)) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT, "scale must be finite");
+  }
+  RecurrentArgs p{num_sequences, num_heads, head_size, total_tokens, /*max_seqlen=*/-1,
+                  state_pool_size, cu_seqlens, state_indices, metadata_status,
+                  state_pool, r, decay, decay_bias, k, v, /*a=*/nullptr, /*b=*/nullptr,
+                  output, scale, static_cast<hipStream_t>(stream)};
+  const FusedTmixParams f{a12, g, k_k, a0, k_a, r_k, ln_weight, ln_bias};
+  switch (io_dtype) {
+    case FRWKV_DTYPE_BF16:
+      return dispatch_tmix_fused<Bf16>(p, f, decay_mode);
+    case FRWKV_DTYPE_F16:
+      return dispatch_tmix_fused<F16>(p, f, decay_mode);
+    default:
+      return set_error(FRWKV_ERR_UNSUPPORTED,
+                       "the fused TMix chain takes float16 or bfloat16 tokens (io dtype %d)",
+                       io_dtype);
+  }
 }

@@ -295,6 +295,61 @@ int frwkv_chunk_replay(int io_dtype, int decay_mode, int32_t num_chunks, int32_t
                        const void* b, void* output, float* state_dot_a, float scale,
                        void* stream);
 
+/*
+ * TMix producer of the WKV7 inputs, per (token, head) row of head_size
+ * features of packed k, a12 [total_tokens, H*head_size] with per-channel
+ * k_k, a0, k_a [H*head_size]:
+ *   u = k k_k, kk = u / max(|u|_row, 1e-12), gate = sigmoid(a0 + a12),
+ *   new_k = k (gate k_a + 1 - k_a), neg_kk = -kk, kka = kk gate.
+ * io_dtype F16 or BF16 (the reference op is float16 only); head_size 64,
+ * 128 or 256; every buffer 16-byte aligned.
+ * Replaces tmix_kk_a_gate_forward_varlen
+ * (csrc/sm120/tmix/kk_a_gate/infer_fp16_forward_varlen.cu:52-160 and its .cpp).
+ */
+int frwkv_kk_a_gate(int io_dtype, int64_t total_tokens, int32_t num_heads,
+                    int32_t head_size, const void* k, const void* k_k, const void* a0,
+                    const void* a12, const void* k_a, void* new_k, void* neg_kk, void* kka,
+                    void* stream);
+
+/*
+ * TMix consumer of the WKV7 output x, per (token, head) row of packed
+ * x, r, k, v, g [total_tokens, H*head_size] with per-channel r_k, weight,
+ * bias [H*head_size]:
+ *   out = ((x - mean) / sqrt(var + 64e-5) weight + bias + rkv v) g,
+ * mean and biased var over the row, rkv = sum_d r k r_k.
+ * io_dtype F16 or BF16 (the reference op is float16 only); head_size 64,
+ * 128 or 256; every buffer 16-byte aligned.
+ * Replaces tmix_lnx_rkvres_xg_forward_varlen
+ * (csrc/sm120/tmix/lnx_rkvres_xg/infer_fp16_forward_varlen.cu:56-200 and its .cpp).
+ */
+int frwkv_lnx_rkvres_xg(int io_dtype, int64_t total_tokens, int32_t num_heads,
+                        int32_t head_size, const void* x, const void* r, const void* k,
+                        const void* v, const void* r_k, const void* weight, const void* bias,
+                        const void* g, void* output, void* stream);
+
+/*
+ * The TMix chain kk_a_gate -> WKV7 recurrent step -> lnx_rkvres_xg in one
+ * kernel, for decode and short sequences (fp32 state pool, head_size 64),
+ * with no intermediate written to memory and none rounded to 16 bits:
+ * the producer gives k' = new_k, a = -kk, b = kk gate (the RWKV-7 update
+ * S = diag(w) S + b (a^T S) + k' v^T); y = scale S^T r feeds the consumer
+ * with r, k', v. Token tensors r, decay, k, v, a12, g are [total_tokens,H,64]
+ * (io dtype), vectors k_k, a0, k_a, r_k, ln_weight, ln_bias [H*64]; output
+ * [total_tokens,H,64] is the consumer's result. Metadata, pool and
+ * fail-closed behaviour as frwkv_recurrent_forward.
+ * No counterpart in the reference, which runs the three stages as separate
+ * ops (composed in tests/tmix/wkv7/test.py:310-414); for decode callers that
+ * want the producer's three and the consumer's five [N,C] tensors off HBM.
+ */
+int frwkv_recurrent_tmix_fused_forward(
+    int io_dtype, int decay_mode, int32_t num_sequences, int32_t num_heads,
+    int32_t head_size, int32_t total_tokens, int32_t state_pool_size,
+    const int32_t* cu_seqlens, const int32_t* state_indices, const int32_t* metadata_status,
+    float* state_pool, const void* r, const void* decay, const void* decay_bias,
+    const void* k, const void* v, const void* a12, const void* g, const void* k_k,
+    const void* a0, const void* k_a, const void* r_k, const void* ln_weight,
+    const void* ln_bias, void* output, float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -40,6 +40,16 @@ How each function is pinned (see ``tests/test_oracle.py``):
   answers (tests/tmix/wkv7/test.py:32-60) and int32 wrap-around.
 * ``add_vec``: exact sums and round-half-to-even ties at 2048 + 1 and
   2050 + 1 (fp16 spacing 2 there).
+* ``kk_a_gate``: the reference test's known answer (k = k_k = k_a = 1,
+  a0 = a12 = 0, head 64: new_k = 0.5, neg_kk = -0.125, kka = 0.0625,
+  tests/tmix/kk_a_gate/test.py:26-47), unit norm of kk per head, the k_a = 0
+  and k_a = 1 limits (new_k = k, resp. k gate) and scale invariance of kk.
+* ``lnx_rkvres_xg``: constant rows (var = 0: out = (bias + rkv v) g), a
+  hand-worked two-value row, rkv by brute-force loops, per-head
+  independence (heads of one row do not mix).
+* ``tmix_fused``: composition of the three pinned stages; checked against
+  the same stages called one after another, and against a per-token loop
+  that applies the RWKV-7 update with a = -kk, b = kk gate directly.
 """
 
 from __future__ import annotations
@@ -348,6 +358,68 @@ def add_vec(x, vec) -> np.ndarray:
     x32 = np.asarray(x).astype(np.float16).astype(np.float32)
     v32 = np.asarray(vec).astype(np.float16).astype(np.float32)
     return (x32 + v32[None, :]).astype(np.float16)
+
+
+# --------------------------------------------- TMix producer / consumer -----
+
+
+def kk_a_gate(k, k_k, a0, a12, k_a, head_size=64):
+    """The key / a-gate producer (reference kk_a_gate .cu:128-160 and
+    tests/tmix/kk_a_gate/test.py:58-66), fp64 on packed ``[N, C]`` rows:
+    ``u = k k_k``, ``kk = u / max(|u|_head, 1e-12)``, ``gate = sigmoid(a0 + a12)``;
+    returns ``(new_k, neg_kk, kka) = (k (gate k_a + 1 - k_a), -kk, kk gate)``."""
+    k, a12 = _f64(k), _f64(a12)
+    n, c = k.shape
+    h = c // head_size
+    kr = k.reshape(n, h, head_size)
+    u = kr * _f64(k_k).reshape(1, h, head_size)
+    norm = np.sqrt(np.sum(u * u, axis=-1, keepdims=True))
+    kk = u / np.maximum(norm, 1.0e-12)
+    gate = 1.0 / (1.0 + np.exp(-(_f64(a0).reshape(1, h, head_size)
+                                 + a12.reshape(n, h, head_size))))
+    ka = _f64(k_a).reshape(1, h, head_size)
+    new_k = kr * (gate * ka + 1.0 - ka)
+    return (new_k.reshape(n, c), (-kk).reshape(n, c), (kk * gate).reshape(n, c))
+
+
+def lnx_rkvres_xg(x, r, k, v, r_k, weight, bias, g, head_size=64, eps=64.0e-5):
+    """The WKV7 output consumer (reference lnx_rkvres_xg .cu:56-131 and
+    tests/tmix/lnx_rkvres_xg/test.py:52-64), fp64 on packed ``[N, C]`` rows:
+    per head, ``((x - mean) / sqrt(var + eps) weight + bias + rkv v) g`` with the
+    biased variance and ``rkv = sum_d r k r_k``."""
+    x, r, k, v, g = (_f64(t) for t in (x, r, k, v, g))
+    n, c = x.shape
+    h = c // head_size
+    shp = (n, h, head_size)
+    xr = x.reshape(shp)
+    mean = xr.mean(-1, keepdims=True)
+    var = ((xr - mean) ** 2).mean(-1, keepdims=True)
+    rkv = np.sum(r.reshape(shp) * k.reshape(shp) * _f64(r_k).reshape(1, h, head_size),
+                 axis=-1, keepdims=True)
+    out = ((xr - mean) / np.sqrt(var + eps) * _f64(weight).reshape(1, h, head_size)
+           + _f64(bias).reshape(1, h, head_size) + rkv * v.reshape(shp)) * g.reshape(shp)
+    return out.reshape(n, c)
+
+
+def tmix_fused(r, w, k, v, a12, g, k_k, a0, k_a, r_k, ln_weight, ln_bias, state_pool,
+               cu_seqlens, state_indices, scale=1.0):
+    """The fused chain, with no rounding between its stages: the producer
+    (:func:`kk_a_gate`) gives the WKV7 inputs k = new_k, a = -kk and
+    b = kk gate (the RWKV-7 update S += (kk gate)((-kk)^T S), as BASELINE's
+    configs state it), then :func:`forward_varlen` with retention ``w``, then
+    the consumer (:func:`lnx_rkvres_xg`) with the producer's new_k. Token
+    tensors ``[N, H, D]``, vectors ``[H*D]``; returns ``(out [N,H,D], pool)``."""
+    r, w, k, v, a12, g = (_f64(t) for t in (r, w, k, v, a12, g))
+    n, h, d = r.shape
+    flat = lambda t: t.reshape(n, h * d)
+    new_k, neg_kk, kka = kk_a_gate(flat(k), k_k, a0, flat(a12), k_a, head_size=d)
+    shp = (n, h, d)
+    y, pool = forward_varlen(r, w, new_k.reshape(shp), v, neg_kk.reshape(shp),
+                             kka.reshape(shp), state_pool, cu_seqlens, state_indices,
+                             scale=scale)
+    out = lnx_rkvres_xg(flat(y), flat(r), new_k, flat(v), r_k, ln_weight, ln_bias, flat(g),
+                        head_size=d)
+    return out.reshape(shp), pool
 
 
 # ------------------------------------------------------------- metrics -----

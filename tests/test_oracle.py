@@ -380,3 +380,119 @@ def test_add_vec_exact_sums_and_ties_to_even():
     x = np.array([[2048, 2050, 1.5, -3.0]], dtype=np.float16)
     vec = np.array([1, 1, 0.25, 3.0], dtype=np.float16)
     assert oracle.add_vec(x, vec).tolist() == [[2048.0, 2052.0, 1.75, 0.0]]
+
+
+# ------------------------------------------- TMix producer / consumer -----
+
+
+def test_kk_a_gate_reference_known_answer():
+    # tests/tmix/kk_a_gate/test.py:26-47: k = k_k = k_a = 1, a0 = a12 = 0,
+    # C = 4096, head 64 -> new_k 0.5, neg_kk -0.125 (= -1/sqrt(64)), kka 0.0625.
+    n, c = 3, 4096
+    new_k, neg_kk, kka = oracle.kk_a_gate(np.ones((n, c)), np.ones(c), np.zeros(c),
+                                          np.zeros((n, c)), np.ones(c))
+    np.testing.assert_allclose(new_k, 0.5, rtol=0, atol=1e-15)
+    np.testing.assert_allclose(neg_kk, -0.125, rtol=0, atol=1e-15)
+    np.testing.assert_allclose(kka, 0.0625, rtol=0, atol=1e-15)
+
+
+@pytest.mark.parametrize("head_size", (64, 128, 256))
+def test_kk_a_gate_unit_norm_limits_and_scale_invariance(head_size):
+    rng = np.random.default_rng(5)
+    n, h = 4, 2
+    c = h * head_size
+    k = rng.standard_normal((n, c))
+    k_k = rng.standard_normal(c)
+    a0 = rng.standard_normal(c)
+    a12 = rng.standard_normal((n, c))
+    new_k, neg_kk, kka = oracle.kk_a_gate(k, k_k, a0, a12, np.zeros(c), head_size)
+    # unit norm of kk per (token, head), and kka / kk = sigmoid(a0 + a12)
+    norms = np.linalg.norm(neg_kk.reshape(n, h, head_size), axis=-1)
+    np.testing.assert_allclose(norms, 1.0, rtol=1e-13)
+    gate = 1.0 / (1.0 + np.exp(-(a0[None, :] + a12)))
+    np.testing.assert_allclose(kka, -neg_kk * gate, rtol=1e-13)
+    # k_a = 0: new_k = k; k_a = 1: new_k = k * gate
+    np.testing.assert_allclose(new_k, k, rtol=1e-15)
+    new_k1, _, _ = oracle.kk_a_gate(k, k_k, a0, a12, np.ones(c), head_size)
+    np.testing.assert_allclose(new_k1, k * gate, rtol=1e-13)
+    # kk does not depend on the key's scale per head
+    _, neg2, _ = oracle.kk_a_gate(3.5 * k, k_k, a0, a12, np.zeros(c), head_size)
+    np.testing.assert_allclose(neg2, neg_kk, rtol=1e-13)
+    # a zero key gives kk = 0 (the 1e-12 floor), not NaN
+    _, neg0, _ = oracle.kk_a_gate(np.zeros((n, c)), k_k, a0, a12, np.zeros(c), head_size)
+    assert np.all(neg0 == 0.0)
+
+
+def test_lnx_rkvres_xg_constant_rows_hand_worked_row_and_heads():
+    rng = np.random.default_rng(6)
+    d, h, n = 64, 2, 3
+    c = h * d
+    r, k, v, g = (rng.standard_normal((n, c)) for _ in range(4))
+    r_k, weight, bias = (rng.standard_normal(c) for _ in range(3))
+    # rkv by explicit loops
+    rkv = np.zeros((n, h))
+    for t in range(n):
+        for hh in range(h):
+            for j in range(d):
+                idx = hh * d + j
+                rkv[t, hh] += r[t, idx] * k[t, idx] * r_k[idx]
+    # constant x per head: var = 0, the normalised term vanishes
+    x = np.repeat(rng.standard_normal((n, h)), d, axis=1)
+    out = oracle.lnx_rkvres_xg(x, r, k, v, r_k, weight, bias, g).reshape(n, h, d)
+    want = (bias.reshape(1, h, d) + rkv[:, :, None] * v.reshape(n, h, d)) * g.reshape(n, h, d)
+    np.testing.assert_allclose(out, want, rtol=1e-12, atol=1e-12)
+    # hand-worked row: x = +-1 alternating, weight 1, bias 0, r = 0, g = 1:
+    # mean 0, var 1, out = x / sqrt(1 + 64e-5)
+    x1 = np.tile([1.0, -1.0], c // 2)[None, :]
+    out1 = oracle.lnx_rkvres_xg(x1, np.zeros((1, c)), k[:1], v[:1], r_k, np.ones(c),
+                                np.zeros(c), np.ones((1, c)))
+    np.testing.assert_allclose(out1, x1 / math.sqrt(1.0 + 64.0e-5), rtol=1e-14)
+    # heads do not mix: changing head 1's x leaves head 0's output unchanged
+    x2 = rng.standard_normal((n, c))
+    o_a = oracle.lnx_rkvres_xg(x2, r, k, v, r_k, weight, bias, g)
+    x3 = x2.copy()
+    x3[:, d:] *= 7.0
+    o_b = oracle.lnx_rkvres_xg(x3, r, k, v, r_k, weight, bias, g)
+    np.testing.assert_array_equal(o_a[:, :d], o_b[:, :d])
+
+
+def test_tmix_fused_is_the_rwkv7_update_with_a_minus_kk_and_b_kk_gate():
+    rng = np.random.default_rng(7)
+    h, d = 2, 8
+    lengths = [3, 1, 4]
+    n = sum(lengths)
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    slots = np.array([2, 0, 1], dtype=np.int32)
+    r, k, v, a12, g = (rng.standard_normal((n, h, d)) for _ in range(5))
+    w = rng.uniform(0.4, 0.99, size=(n, h, d))
+    k_k, a0, k_a, r_k, lnw, lnb = (rng.standard_normal(h * d) for _ in range(6))
+    pool = rng.standard_normal((3, h, d, d)) * 0.3
+    out, pool_out = oracle.tmix_fused(r, w, k, v, a12, g, k_k, a0, k_a, r_k, lnw, lnb,
+                                      pool, cu, slots, scale=0.7)
+    # per-token loop written from the RWKV-7 definition: kk = normalize(k k_k),
+    # S = diag(w) S + (kk gate)((-kk)^T S) + k' v^T, y = scale S^T r, then
+    # the per-head norm / residual / gate.
+    ref_out = np.zeros((n, h, d))
+    ref_pool = pool.copy()
+    for s_i, (t0, t1) in enumerate(zip(cu[:-1], cu[1:])):
+        st = ref_pool[slots[s_i]].copy()
+        for t in range(t0, t1):
+            for hh in range(h):
+                sl = slice(hh * d, (hh + 1) * d)
+                u = k[t, hh] * k_k[sl]
+                kk = u / max(np.linalg.norm(u), 1e-12)
+                gate = 1.0 / (1.0 + np.exp(-(a0[sl] + a12[t, hh])))
+                kn = k[t, hh] * (gate * k_a[sl] + 1.0 - k_a[sl])
+                S = st[hh]
+                sa = (-kk) @ S
+                S = w[t, hh][:, None] * S + np.outer(kk * gate, sa) + np.outer(kn, v[t, hh])
+                st[hh] = S
+                y = 0.7 * (r[t, hh] @ S)
+                mu = y.mean()
+                var = ((y - mu) ** 2).mean()
+                rkv = np.sum(r[t, hh] * kn * r_k[sl])
+                ref_out[t, hh] = ((y - mu) / math.sqrt(var + 64e-5) * lnw[sl] + lnb[sl]
+                                  + rkv * v[t, hh]) * g[t, hh]
+        ref_pool[slots[s_i]] = st
+    np.testing.assert_allclose(out, ref_out, rtol=1e-10, atol=1e-10)
+    np.testing.assert_allclose(pool_out, ref_pool, rtol=1e-10, atol=1e-10)
