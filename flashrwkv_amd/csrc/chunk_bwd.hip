@@ -203,7 +203,7 @@ template <typename T, DecayMode M>
 __device__ bool prepare_bwd(BwdSmem& sm, const BwdRows& rows, const float (&bias)[8],
                             int ntok, float scale) {
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = uniform(tid >> 6);
   const int lane = tid & 63;
   const int tp = lane & 7;
   const int kg = lane >> 3;
@@ -329,7 +329,7 @@ __device__ bool prepare_bwd(BwdSmem& sm, const BwdRows& rows, const float (&bias
 template <typename Issue>
 __device__ __forceinline__ void intra_bwd(BwdSmem& sm, Issue&& issue) {
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = uniform(tid >> 6);
   const int lane = tid & 63;
   const int g = lane >> 4;
   const int n = lane & 15;
@@ -435,7 +435,7 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
   using S16 = typename IoTraits<T>::storage;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = uniform(tid >> 6);
   const int lane = tid & 63;
   const int g = lane >> 4;
   const int n = lane & 15;
@@ -1039,17 +1039,29 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
         float dwv[4];
+        // Block carries of the lane's 4 consecutive features, 16-byte reads.
+        const int kf0 = 16 * kb + 4 * g;
+        float4 later4 = make_float4(0.f, 0.f, 0.f, 0.f), all3_4 = later4, dgam4 = later4;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float4 c1 = *reinterpret_cast<const float4*>(&sm.carry[q][kf0]);
+          const float4 c3 = *reinterpret_cast<const float4*>(&sm.carry3[q][kf0]);
+          const float4 dg = *reinterpret_cast<const float4*>(&sm.dgamma[q][kf0]);
+          if (q > pb) {
+            later4.x += c1.x; later4.y += c1.y; later4.z += c1.z; later4.w += c1.w;
+          }
+          all3_4.x += c3.x; all3_4.y += c3.y; all3_4.z += c3.z; all3_4.w += c3.w;
+          dgam4.x += dg.x; dgam4.y += dg.y; dgam4.z += dg.z; dgam4.w += dg.w;
+        }
+        const float4 gc4 = *reinterpret_cast<const float4*>(&sm.gc[kf0]);
+        const float later_v[4] = {later4.x, later4.y, later4.z, later4.w};
+        const float all3_v[4] = {all3_4.x, all3_4.y, all3_4.z, all3_4.w};
+        const float dgam_v[4] = {dgam4.x, dgam4.y, dgam4.z, dgam4.w};
+        const float gc_v[4] = {gc4.x, gc4.y, gc4.z, gc4.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int kf = 16 * kb + 4 * g + j;
-          float later = 0.0f, all3 = 0.0f, dgam = 0.0f;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            later += q > pb ? sm.carry[q][kf] : 0.0f;
-            all3 += sm.carry3[q][kf];
-            dgam += sm.dgamma[q][kf];
-          }
-          const float dlg = suf[kb][j] + later - e2v[kb][j] + all3 + dgam * sm.gc[kf];
+          const float dlg =
+              suf[kb][j] + later_v[j] - e2v[kb][j] + all3_v[j] + dgam_v[j] * gc_v[j];
           const float xin = dec_in[kb][j];
           float d;
           if constexpr (M == DecayMode::kLogits) {
