@@ -361,7 +361,7 @@ void recurrent_fp32_forward_internal(
 
 void check_chunk_tokens(const Tensor& r, const Tensor& decay, const Tensor& k,
                         const Tensor& v, const Tensor& a, const Tensor& b,
-                        bool bf16_only) {
+                        bool bf16_only, bool any_head_size = false) {
   const std::pair<const Tensor*, const char*> all[] = {
       {&r, "r"}, {&decay, "decay_logits"}, {&k, "k"}, {&v, "v"}, {&a, "a"}, {&b, "b"}};
   for (const auto& item : all) {
@@ -380,8 +380,14 @@ void check_chunk_tokens(const Tensor& r, const Tensor& decay, const Tensor& k,
   }
   TORCH_CHECK(r.scalar_type() == at::kBFloat16 || r.scalar_type() == at::kHalf,
               "token tensors must be float16 or bfloat16");
-  TORCH_CHECK(r.dim() == 3 && r.size(0) > 0 && r.size(1) > 0 && r.size(2) == 64,
-              "chunk token tensors must have shape [total_tokens,H,64]");
+  if (any_head_size) {
+    TORCH_CHECK(r.dim() == 3 && r.size(0) > 0 && r.size(1) > 0 &&
+                    (r.size(2) == 64 || r.size(2) == 128 || r.size(2) == 256),
+                "token tensors must have shape [total_tokens,H,D], D in {64,128,256}");
+  } else {
+    TORCH_CHECK(r.dim() == 3 && r.size(0) > 0 && r.size(1) > 0 && r.size(2) == 64,
+                "chunk token tensors must have shape [total_tokens,H,64]");
+  }
   TORCH_CHECK(r.size(0) <= std::numeric_limits<int32_t>::max(),
               "token count must fit in int32");
 }
@@ -494,9 +500,11 @@ void statetune_forward_impl(const Tensor& offsets, const Tensor& starts, const T
   TORCH_CHECK(state.dim() == 4 && state.size(0) > 0 && state.size(1) > 0 &&
                   state.size(2) == state.size(3),
               "state must have shape [B,H,D,D]");
-  TORCH_CHECK(state.size(2) == 64, "state head size must be 64 for the MI355X chunked kernels");
-  check_chunk_tokens(r, decay, k, v, a, b, /*bf16_only=*/false);
-  TORCH_CHECK(r.size(1) == state.size(1), "token tensors must have shape [total_tokens,H,D]");
+  const int64_t d = state.size(2);
+  TORCH_CHECK(d == 64 || d == 128 || d == 256, "state head size must be 64, 128, or 256");
+  check_chunk_tokens(r, decay, k, v, a, b, /*bf16_only=*/false, /*any_head_size=*/true);
+  TORCH_CHECK(r.size(1) == state.size(1) && r.size(2) == d,
+              "token tensors must have shape [total_tokens,H,D]");
   for (const auto* t : {&r, &decay, &k, &v, &a, &b}) check_same_device(state, *t, "token");
   check_statetune_metadata(offsets, starts, ends, state);
   check_device_contiguous(output, "output");
@@ -506,14 +514,14 @@ void statetune_forward_impl(const Tensor& offsets, const Tensor& starts, const T
               "output must match r");
   TORCH_CHECK(boundary.scalar_type() == at::kFloat && boundary.dim() == 4 &&
                   boundary.size(0) == starts.numel() && boundary.size(1) == state.size(1) &&
-                  boundary.size(2) == 64 && boundary.size(3) == 64,
+                  boundary.size(2) == d && boundary.size(3) == d,
               "boundary must have shape [chunks,H,D,D] float32");
   TORCH_CHECK(state_dot_a.scalar_type() == at::kFloat && state_dot_a.sizes() == r.sizes(),
               "state_dot_a must have shape [total_tokens,H,D] float32");
   c10::DeviceGuard guard(state.device());
   check_rc(frwkv_statetune_forward(
       io_code(r.scalar_type()), decay_mode, static_cast<int32_t>(state.size(0)),
-      static_cast<int32_t>(state.size(1)), 64, static_cast<int32_t>(r.size(0)),
+      static_cast<int32_t>(state.size(1)), static_cast<int32_t>(d), static_cast<int32_t>(r.size(0)),
       static_cast<int32_t>(starts.numel()), offsets.data_ptr<int32_t>(),
       starts.data_ptr<int32_t>(), ends.data_ptr<int32_t>(), state.data_ptr<float>(),
       r.data_ptr(), decay.data_ptr(), nullptr, k.data_ptr(), v.data_ptr(), a.data_ptr(),
@@ -557,13 +565,14 @@ void statetune_backward_impl(const Tensor& offsets, const Tensor& starts, const 
                              std::optional<Tensor> grad_initial_state, int64_t num_sequences,
                              double scale, int decay_mode) {
   TORCH_CHECK(std::isfinite(scale), "scale must be finite");
-  check_chunk_tokens(r, decay, k, v, a, b, /*bf16_only=*/false);
-  const int64_t heads = r.size(1);
+  check_chunk_tokens(r, decay, k, v, a, b, /*bf16_only=*/false, /*any_head_size=*/true);
+  const int64_t heads = r.size(1), d = r.size(2);
+  TORCH_CHECK(d == 64 || d == 128 || d == 256, "token head size must be 64, 128, or 256");
   check_device_contiguous(boundary, "boundary");
   TORCH_CHECK(boundary.scalar_type() == at::kFloat && boundary.dim() == 4 &&
                   boundary.size(0) == starts.numel() && boundary.size(1) == heads &&
-                  boundary.size(2) == 64 && boundary.size(3) == 64,
-              "boundary must have shape [chunks,H,64,64] float32");
+                  boundary.size(2) == d && boundary.size(3) == d,
+              "boundary must have shape [chunks,H,D,D] float32");
   for (const auto* t : {&offsets, &starts, &ends}) {
     check_device_contiguous(*t, "chunk metadata");
     TORCH_CHECK(t->scalar_type() == at::kInt && t->dim() == 1, "chunk metadata must be int32 1-D");
@@ -583,9 +592,9 @@ void statetune_backward_impl(const Tensor& offsets, const Tensor& starts, const 
     check_device_contiguous(*grad_final_state, "grad_final_state");
     TORCH_CHECK(grad_final_state->scalar_type() == at::kFloat &&
                     grad_final_state->dim() == 4 && grad_final_state->size(0) == num_sequences &&
-                    grad_final_state->size(1) == heads && grad_final_state->size(2) == 64 &&
-                    grad_final_state->size(3) == 64,
-                "grad_final_state must have shape [B,H,64,64] float32");
+                    grad_final_state->size(1) == heads && grad_final_state->size(2) == d &&
+                    grad_final_state->size(3) == d,
+                "grad_final_state must have shape [B,H,D,D] float32");
   }
   auto token_grad = [&](std::optional<Tensor>& t, const char* name) {
     if (!t.has_value() || !t->defined()) t = at::empty_like(r);
@@ -601,18 +610,18 @@ void statetune_backward_impl(const Tensor& offsets, const Tensor& starts, const 
   void* ga = token_grad(grad_a, "grad_a");
   void* gb = token_grad(grad_b, "grad_b");
   if (!grad_initial_state.has_value() || !grad_initial_state->defined()) {
-    grad_initial_state = at::empty({num_sequences, heads, 64, 64}, state_opts);
+    grad_initial_state = at::empty({num_sequences, heads, d, d}, state_opts);
   }
   check_device_contiguous(*grad_initial_state, "grad_initial_state");
   TORCH_CHECK(grad_initial_state->scalar_type() == at::kFloat &&
-                  grad_initial_state->numel() == num_sequences * heads * 64 * 64,
-              "grad_initial_state must have shape [B,H,64,64] float32");
+                  grad_initial_state->numel() == num_sequences * heads * d * d,
+              "grad_initial_state must have shape [B,H,D,D] float32");
   c10::DeviceGuard guard(r.device());
   const bool has_dy = grad_output.has_value() && grad_output->defined();
   const bool has_ds = grad_final_state.has_value() && grad_final_state->defined();
   check_rc(frwkv_statetune_backward(
       io_code(r.scalar_type()), decay_mode, static_cast<int32_t>(num_sequences),
-      static_cast<int32_t>(heads), 64, static_cast<int32_t>(r.size(0)),
+      static_cast<int32_t>(heads), static_cast<int32_t>(d), static_cast<int32_t>(r.size(0)),
       static_cast<int32_t>(starts.numel()), offsets.data_ptr<int32_t>(),
       starts.data_ptr<int32_t>(), ends.data_ptr<int32_t>(), boundary.data_ptr<float>(),
       r.data_ptr(), decay.data_ptr(), nullptr, k.data_ptr(), v.data_ptr(), a.data_ptr(),
@@ -655,7 +664,8 @@ void statetune_backward_internal(
 // csrc/sm90/tmix/wkv7/pretrain_recurrent_bf16_forward.cpp:20-53. Dense
 // [B,T,H,D] tokens with clampw decay logits, S0 = 0, no final state; s is the
 // state every 16 tokens [B,H,T/16,D,D] fp32 and sa is a^T S_{t-1} [B,T,H,D]
-// fp32. Head size 64 on the MI355X chunked kernels.
+// fp32. Head size 64 runs the chunked MFMA kernels, 128 and 256 the
+// per-token training kernels.
 
 void check_clampw_tokens(const std::vector<std::pair<const Tensor*, const char*>>& all,
                          int64_t head_size) {
@@ -664,8 +674,6 @@ void check_clampw_tokens(const std::vector<std::pair<const Tensor*, const char*>
   const Tensor& r = *all[0].first;
   TORCH_CHECK(r.dim() == 4 && r.size(3) == head_size,
               "input head dimension must equal head_size");
-  TORCH_CHECK(head_size == 64, "head_size ", head_size,
-              " is not supported by the MI355X chunked kernels (64 only)");
   for (const auto& item : all) {
     check_device_contiguous(*item.first, item.second);
     TORCH_CHECK(item.first->device() == r.device(), item.second,

@@ -27,3 +27,33 @@ int frwkv_replay_recurrent(int io_dtype, int decay_mode, int32_t num_chunks, int
                            const void* decay_bias, const void* k, const void* v,
                            const void* a, const void* b, void* output, float* state_dot_a,
                            float scale, void* stream);
+
+// Per-token training kernels (train_recurrent.hip) for head sizes 128 and
+// 256, called by frwkv_statetune_{forward,backward} and
+// frwkv_pretrain_{forward,backward}. Chunks come either from segment arrays
+// (seg_offsets/seg_starts/seg_ends of num_chunks chunks, dense_t = 0) or, with dense_t > 0, from
+// a dense [B, dense_t] layout in 16-token chunks with the pretraining
+// checkpoint layout [B,H,T/16,D,D]. state (forward) is S0 in / S_T out, or
+// null for a zero start and no final state. The backward needs chunks of at
+// most 16 tokens; a longer or out-of-range chunk makes its unit's gradients
+// NaN.
+int frwkv_train_recurrent_forward(int io_dtype, int decay_mode, int32_t num_sequences,
+                                  int32_t num_heads, int32_t head_size, int32_t total_tokens,
+                                  const int32_t* seg_offsets, const int32_t* seg_starts,
+                                  const int32_t* seg_ends, int32_t num_chunks, int32_t dense_t,
+                                  float* state,
+                                  const void* r, const void* decay, const void* decay_bias,
+                                  const void* k, const void* v, const void* a, const void* b,
+                                  void* output, float* boundary, float* state_dot_a,
+                                  float scale, void* stream);
+int frwkv_train_recurrent_backward(int io_dtype, int decay_mode, int32_t num_sequences,
+                                   int32_t num_heads, int32_t head_size, int32_t total_tokens,
+                                   const int32_t* seg_offsets, const int32_t* seg_starts,
+                                   const int32_t* seg_ends, int32_t num_chunks,
+                                   int32_t dense_t, const float* boundary, const void* r, const void* decay,
+                                   const void* decay_bias, const void* k, const void* v,
+                                   const void* a, const void* b, const void* grad_output,
+                                   const float* grad_final_state, void* grad_r,
+                                   void* grad_decay, void* grad_k, void* grad_v, void* grad_a,
+                                   void* grad_b, float* grad_initial_state, float scale,
+                                   void* stream);

@@ -1137,16 +1137,24 @@ extern "C" int frwkv_statetune_backward(
     return set_error(FRWKV_ERR_INVALID_ARGUMENT,
                      "frwkv_statetune_backward: null pointer argument");
   }
-  if (head_size != 64) {
-    return set_error(FRWKV_ERR_UNSUPPORTED, "chunked kernels support head size 64, got %d",
-                     head_size);
-  }
   if (num_sequences <= 0 || num_heads <= 0 || total_tokens <= 0 || num_chunks <= 0) {
     return set_error(FRWKV_ERR_INVALID_ARGUMENT,
                      "frwkv_statetune_backward: sizes must be positive");
   }
   if (!__builtin_isfinite(scale)) {
     return set_error(FRWKV_ERR_INVALID_ARGUMENT, "scale must be finite");
+  }
+  if (head_size == 128 || head_size == 256) {
+    return frwkv_train_recurrent_backward(
+        io_dtype, decay_mode, num_sequences, num_heads, head_size, total_tokens,
+        sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, num_chunks, /*dense_t=*/0,
+        boundary,
+        r, decay, decay_bias, k, v, a, b, grad_output, grad_final_state, grad_r, grad_decay,
+        grad_k, grad_v, grad_a, grad_b, grad_initial_state, scale, stream);
+  }
+  if (head_size != 64) {
+    return set_error(FRWKV_ERR_UNSUPPORTED, "head size must be 64, 128, or 256, got %d",
+                     head_size);
   }
   ChunkBwdParams p{};
   p.num_heads = num_heads;
@@ -1199,10 +1207,6 @@ extern "C" int frwkv_pretrain_backward(int io_dtype, int decay_mode, int32_t bat
     return set_error(FRWKV_ERR_INVALID_ARGUMENT,
                      "frwkv_pretrain_backward: null pointer argument");
   }
-  if (head_size != 64) {
-    return set_error(FRWKV_ERR_UNSUPPORTED, "chunked kernels support head size 64, got %d",
-                     head_size);
-  }
   if (batch <= 0 || tokens <= 0 || num_heads <= 0 || tokens % 16 != 0) {
     return set_error(FRWKV_ERR_INVALID_ARGUMENT,
                      "frwkv_pretrain_backward: B, H > 0 and T a positive multiple of 16 "
@@ -1210,6 +1214,17 @@ extern "C" int frwkv_pretrain_backward(int io_dtype, int decay_mode, int32_t bat
   }
   if (static_cast<int64_t>(batch) * tokens > INT32_MAX) {
     return set_error(FRWKV_ERR_INVALID_ARGUMENT, "frwkv_pretrain_backward: B * T too large");
+  }
+  if (head_size == 128 || head_size == 256) {
+    return frwkv_train_recurrent_backward(
+        io_dtype, decay_mode, batch, num_heads, head_size, batch * tokens, nullptr, nullptr,
+        nullptr, 0, tokens, boundary, r, decay, /*decay_bias=*/nullptr, k, v, a, b, grad_output,
+        /*grad_final_state=*/nullptr, grad_r, grad_decay, grad_k, grad_v, grad_a, grad_b,
+        /*grad_initial_state=*/nullptr, 1.0f, stream);
+  }
+  if (head_size != 64) {
+    return set_error(FRWKV_ERR_UNSUPPORTED, "head size must be 64, 128, or 256, got %d",
+                     head_size);
   }
   ChunkBwdParams p{};
   p.num_heads = num_heads;

@@ -988,16 +988,24 @@ extern "C" int frwkv_statetune_forward(
   }
   int rc = check_token_pointers(r, decay, k, v, a, b, output);
   if (rc != FRWKV_OK) return rc;
-  if (head_size != 64) {
-    return set_error(FRWKV_ERR_UNSUPPORTED, "chunked kernels support head size 64, got %d",
-                     head_size);
-  }
   if (num_sequences <= 0 || num_heads <= 0 || total_tokens <= 0 || num_chunks <= 0) {
     return set_error(FRWKV_ERR_INVALID_ARGUMENT,
                      "frwkv_statetune_forward: sizes must be positive");
   }
   if (!__builtin_isfinite(scale)) {
     return set_error(FRWKV_ERR_INVALID_ARGUMENT, "scale must be finite");
+  }
+  if (head_size == 128 || head_size == 256) {
+    return frwkv_train_recurrent_forward(io_dtype, decay_mode, num_sequences, num_heads,
+                                         head_size, total_tokens, sequence_chunk_offsets,
+                                         chunk_token_starts, chunk_token_ends, num_chunks,
+                                         /*dense_t=*/0,
+                                         state, r, decay, decay_bias, k, v, a, b, output,
+                                         boundary, state_dot_a, scale, stream);
+  }
+  if (head_size != 64) {
+    return set_error(FRWKV_ERR_UNSUPPORTED, "head size must be 64, 128, or 256, got %d",
+                     head_size);
   }
   ChunkFwdParams p{};
   p.num_heads = num_heads;
@@ -1036,10 +1044,6 @@ extern "C" int frwkv_pretrain_forward(int io_dtype, int decay_mode, int32_t batc
   }
   int rc = check_token_pointers(r, decay, k, v, a, b, output);
   if (rc != FRWKV_OK) return rc;
-  if (head_size != 64) {
-    return set_error(FRWKV_ERR_UNSUPPORTED, "chunked kernels support head size 64, got %d",
-                     head_size);
-  }
   if (batch <= 0 || tokens <= 0 || num_heads <= 0 || tokens % 16 != 0) {
     return set_error(FRWKV_ERR_INVALID_ARGUMENT,
                      "frwkv_pretrain_forward: B, H > 0 and T a positive multiple of 16 "
@@ -1047,6 +1051,16 @@ extern "C" int frwkv_pretrain_forward(int io_dtype, int decay_mode, int32_t batc
   }
   if (static_cast<int64_t>(batch) * tokens > INT32_MAX) {
     return set_error(FRWKV_ERR_INVALID_ARGUMENT, "frwkv_pretrain_forward: B * T too large");
+  }
+  if (head_size == 128 || head_size == 256) {
+    return frwkv_train_recurrent_forward(io_dtype, decay_mode, batch, num_heads, head_size,
+                                         batch * tokens, nullptr, nullptr, nullptr, 0, tokens,
+                                         /*state=*/nullptr, r, decay, /*decay_bias=*/nullptr, k,
+                                         v, a, b, output, boundary, state_dot_a, 1.0f, stream);
+  }
+  if (head_size != 64) {
+    return set_error(FRWKV_ERR_UNSUPPORTED, "head size must be 64, 128, or 256, got %d",
+                     head_size);
   }
   ChunkFwdParams p{};
   p.num_heads = num_heads;

@@ -5,8 +5,9 @@
 ``flashrwkv2/tmix/wkv7/pretrain.py:14-129``): dense bf16 ``[B,T,C]`` tokens
 with decay logits ``w`` (retention ``exp(-e^{-1/2} sigmoid(w))``), zero initial
 state, output ``[B,T,C]``. The forward and backward run through
-``torch.ops.rwkv7_clampw_v3`` on the chunked bf16-MFMA kernels; the backward
-recomputes each 64-token chunk from the saved boundary states.
+``torch.ops.rwkv7_clampw_v3``: head size 64 on the chunked bf16-MFMA kernels,
+128 and 256 on the per-token fp32 training kernels. Either backward recomputes
+its chunks from the saved boundary states (every 16 tokens).
 """
 
 from __future__ import annotations

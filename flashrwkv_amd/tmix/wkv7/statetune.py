@@ -2,14 +2,15 @@
 
 ``statetune_recurrent_fp32io16`` keeps the reference's signature, validation
 (error types and messages) and outputs ``(y, S_T, boundary, state_dot_a)``
-(reference ``flashrwkv2/tmix/wkv7/statetune.py:11-236``). Forward and
-backward run the chunked bf16-MFMA kernels; the backward recomputes every
-chunk from the stored boundary states instead of dividing by the decay.
+(reference ``flashrwkv2/tmix/wkv7/statetune.py:11-236``). Head size 64 runs
+the chunked bf16-MFMA kernels, 128 and 256 the per-token fp32 training
+kernels; either backward recomputes every chunk from the stored boundary
+states instead of dividing by the decay.
 
-The kernels work on chunks of at most 64 tokens. Caller chunks that are
-longer are split internally (one device-to-host copy of the chunk metadata
-per forward); the boundary output still holds the state at each caller chunk
-start.
+The backward kernels work on chunks of at most 64 tokens (head size 64) or 16
+tokens (128, 256). Caller chunks that are longer are split internally (one
+device-to-host copy of the chunk metadata per forward); the boundary output
+still holds the state at each caller chunk start.
 """
 
 from __future__ import annotations
@@ -20,7 +21,10 @@ import torch
 
 from . import DECAY_LOGITS, DECAY_RAW_W, _extension
 
-_KERNEL_CHUNK = 64
+
+def _kernel_chunk(head_size: int) -> int:
+    """Longest chunk the backward kernels take for this head size."""
+    return 64 if head_size == 64 else 16
 
 
 def _check_cuda_contiguous(tensor: torch.Tensor, name: str) -> None:
@@ -51,7 +55,7 @@ def _check_metadata(sequence_chunk_offsets, chunk_token_starts, chunk_token_ends
 
 
 def _check_token_inputs(state, r, decay_logits, k, v, a, b) -> None:
-    """Reference ``statetune.py:41-76``; this build's chunked kernels need D = 64."""
+    """Reference ``statetune.py:41-76``."""
     _check_cuda_contiguous(state, "state")
     if state.dtype != torch.float32:
         raise TypeError("state must be float32")
@@ -59,8 +63,6 @@ def _check_token_inputs(state, r, decay_logits, k, v, a, b) -> None:
         raise ValueError("state must have shape [B,H,D,D]")
     if state.shape[2] != state.shape[3] or state.shape[2] not in (64, 128, 256):
         raise ValueError("state head size must be 64, 128, or 256")
-    if state.shape[2] != 64:
-        raise ValueError("state head size must be 64 for the MI355X chunked kernels")
     tensors = {"r": r, "decay_logits": decay_logits, "k": k, "v": v, "a": a, "b": b}
     for name, tensor in tensors.items():
         _check_cuda_contiguous(tensor, name)
@@ -74,8 +76,8 @@ def _check_token_inputs(state, r, decay_logits, k, v, a, b) -> None:
         raise ValueError("token tensors must have shape [total_tokens,H,D]")
 
 
-def _kernel_chunks(sequence_chunk_offsets, chunk_token_starts, chunk_token_ends):
-    """Kernel chunk metadata (chunks of at most 64 tokens).
+def _kernel_chunks(sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, limit):
+    """Kernel chunk metadata (chunks of at most ``limit`` tokens).
 
     Returns ``(offsets, starts, ends, first)`` where ``first[c]`` is the
     kernel chunk that starts caller chunk ``c``, or ``None`` when every
@@ -83,7 +85,7 @@ def _kernel_chunks(sequence_chunk_offsets, chunk_token_starts, chunk_token_ends)
     """
     starts = chunk_token_starts.cpu()
     ends = chunk_token_ends.cpu()
-    if int((ends - starts).max()) <= _KERNEL_CHUNK:
+    if int((ends - starts).max()) <= limit:
         return None
     offsets = sequence_chunk_offsets.cpu().tolist()
     starts, ends = starts.tolist(), ends.tolist()
@@ -95,9 +97,9 @@ def _kernel_chunks(sequence_chunk_offsets, chunk_token_starts, chunk_token_ends)
             if e <= s:
                 k_start.append(s)
                 k_end.append(s)
-            for t in range(s, e, _KERNEL_CHUNK):
+            for t in range(s, e, limit):
                 k_start.append(t)
-                k_end.append(min(t + _KERNEL_CHUNK, e))
+                k_end.append(min(t + limit, e))
         k_off.append(len(k_start))
     dev = sequence_chunk_offsets.device
 
@@ -116,16 +118,17 @@ class _StateTune(torch.autograd.Function):
         state = initial_state.detach().contiguous().clone()
         output = torch.empty_like(v)
         n_chunks = chunk_token_starts.numel()
-        heads = state.shape[1]
+        heads, d = state.shape[1], state.shape[2]
         state_dot_a = torch.empty_like(r, dtype=torch.float32)
-        split = _kernel_chunks(sequence_chunk_offsets, chunk_token_starts, chunk_token_ends)
+        split = _kernel_chunks(sequence_chunk_offsets, chunk_token_starts, chunk_token_ends,
+                               _kernel_chunk(d))
         if split is None:
             meta = (sequence_chunk_offsets, chunk_token_starts, chunk_token_ends)
-            checkpoint = torch.empty((n_chunks, heads, 64, 64), device=state.device,
+            checkpoint = torch.empty((n_chunks, heads, d, d), device=state.device,
                                      dtype=torch.float32)
         else:
             meta = split[:3]
-            checkpoint = torch.empty((split[1].numel(), heads, 64, 64), device=state.device,
+            checkpoint = torch.empty((split[1].numel(), heads, d, d), device=state.device,
                                      dtype=torch.float32)
         _extension().statetune_forward_internal(
             *meta, state, r, decay, k, v, a, b, output, checkpoint, state_dot_a,
@@ -142,7 +145,7 @@ class _StateTune(torch.autograd.Function):
         offsets, starts, ends, r, decay, k, v, a, b, checkpoint = ctx.saved_tensors
         grads = [torch.empty_like(t) for t in (r, decay, k, v, a, b)]
         batch = offsets.numel() - 1
-        grad_state = torch.empty((batch, r.shape[1], 64, 64), device=r.device,
+        grad_state = torch.empty((batch, r.shape[1], r.shape[2], r.shape[2]), device=r.device,
                                  dtype=torch.float32)
         dy = None if grad_output is None else grad_output.contiguous()
         ds = None if grad_final_state is None else grad_final_state.contiguous().float()

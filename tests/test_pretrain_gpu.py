@@ -40,10 +40,10 @@ def test_public_contract_matches_clampw_v3():
         assert hasattr(torch.ops.rwkv7_clampw_v3, "backward")
 
 
-def _case(batch, tokens, heads, *, scale=0.05, seed=20260806):
-    """Reference test.py:31-46: six N(0, 1) * scale bf16 tensors [B,T,H*64]."""
+def _case(batch, tokens, heads, *, scale=0.05, seed=20260806, d=64):
+    """Reference test.py:31-46: six N(0, 1) * scale bf16 tensors [B,T,H*D]."""
     g = torch.Generator().manual_seed(seed + batch + tokens + heads)
-    shape = (batch, tokens, heads * 64)
+    shape = (batch, tokens, heads * d)
     return [(torch.randn(shape, generator=g) * scale).to(torch.bfloat16) for _ in range(6)]
 
 
@@ -58,13 +58,13 @@ def _check(name, actual, expected, tol=TOL):
     assert np.isfinite(err) and err <= tol, f"{name}: {err:.3e} > {tol}"
 
 
-def _oracle(values, dy, batch, tokens, heads):
+def _oracle(values, dy, batch, tokens, heads, d=64):
     """fp64 forward (16-token segments) and adjoint of the clampw recurrence."""
-    packed = [_np(t).reshape(batch * tokens, heads, 64) for t in values]
+    packed = [_np(t).reshape(batch * tokens, heads, d) for t in values]
     x = packed[1]
     w = oracle.retention_from_logits(x)
     args = [packed[0], w, *packed[2:]]
-    s0 = np.zeros((batch, heads, 64, 64))
+    s0 = np.zeros((batch, heads, d, d))
     slots = np.arange(batch, dtype=np.int32)
     meta16 = oracle.chunk_metadata([tokens] * batch, 16)
     y, _, bnd, sda = oracle.forward(*args, s0, seg_offsets=meta16[0], seg_starts=meta16[1],
@@ -75,7 +75,7 @@ def _oracle(values, dy, batch, tokens, heads):
         meta = oracle.chunk_metadata([tokens] * batch, 64)
         grads = oracle.backward(*args, s0, seg_offsets=meta[0], seg_starts=meta[1],
                                 seg_ends=meta[2], state_slots=slots,
-                                dy=_np(dy).reshape(batch * tokens, heads, 64))
+                                dy=_np(dy).reshape(batch * tokens, heads, d))
         grads["dw"] = grads["dw"] * w * oracle.retention_log_derivative(x)
     return y, bnd, sda, grads
 
@@ -168,6 +168,61 @@ def test_invalid_input_contract_is_rejected():
         pretrain_recurrent_bf16(valid[0].transpose(1, 2), *valid[1:])
     with pytest.raises(ValueError, match="contiguous CUDA"):
         pretrain_recurrent_bf16(*[t.cpu() for t in valid])
-    # Head sizes the reference supports but these kernels do not: a clear error.
-    with pytest.raises(RuntimeError, match="head_size 128"):
-        pretrain_recurrent_bf16(*[t.repeat(1, 1, 2).contiguous() for t in valid], head_size=128)
+    # The input's last dimension must be a multiple of head_size.
+    with pytest.raises(ValueError, match="C must be divisible"):
+        pretrain_recurrent_bf16(*valid, head_size=128)
+
+
+# ---------------------------------------------------------------- head sizes 128 and 256 ----
+# The per-token fp32 training kernels. Same oracle and tolerance; bf16 inputs,
+# fp32 state, bf16 outputs and gradients.
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("head_size", (128, 256))
+@pytest.mark.parametrize("batch,tokens,heads", [(1, 16, 1), (2, 48, 2)])
+def test_generalized_forward_backward_matches_recurrence(head_size, batch, tokens, heads):
+    """Reference test.py:131-145 (head sizes 128 and 256), against the fp64
+    forward and adjoint."""
+    values = _case(batch, tokens, heads, scale=0.3, seed=29, d=head_size)
+    leaves = [t.cuda().requires_grad_(True) for t in values]
+    out = pretrain_recurrent_bf16(*leaves, head_size=head_size)
+    g = torch.Generator().manual_seed(31)
+    dy = torch.randn(out.shape, generator=g).to(torch.bfloat16)
+    out.backward(dy.cuda())
+    torch.cuda.synchronize()
+    y_ref, _, _, grads = _oracle(values, dy, batch, tokens, heads, d=head_size)
+    _check("y", out.reshape(batch * tokens, heads, head_size), y_ref)
+    for name, leaf in zip(NAMES, leaves):
+        assert torch.isfinite(leaf.grad.float()).all()
+        _check(f"d{name}", leaf.grad.reshape(batch * tokens, heads, head_size),
+               grads["d" + name])
+    # Forward bitwise determinism (reference test.py:104).
+    again = pretrain_recurrent_bf16(*[t.detach() for t in leaves], head_size=head_size)
+    assert torch.equal(out.detach(), again)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("head_size", (128, 256))
+def test_op_boundary_and_state_dot_a_large_heads(head_size):
+    """The op's s (state before every 16th token) and sa at head sizes 128/256,
+    and the C ABI backward with the gradients of every input."""
+    batch, tokens, heads = 2, 64, 1
+    values = _case(batch, tokens, heads, scale=0.3, seed=37, d=head_size)
+    dev = [t.cuda().view(batch, tokens, heads, head_size) for t in values]
+    y = torch.empty_like(dev[3])
+    s = torch.empty((batch, heads, tokens // 16, head_size, head_size), device="cuda")
+    sa = torch.empty((batch, tokens, heads, head_size), device="cuda")
+    torch.ops.rwkv7_clampw_v3.forward(*dev, y, s, sa, head_size)
+    g = torch.Generator().manual_seed(41)
+    dy = torch.randn(y.shape, generator=g).to(torch.bfloat16)
+    grads = [torch.empty_like(t) for t in dev]
+    capi.pretrain_backward(*dev, grad_output=dy.cuda(), boundary=s, grads=grads)
+    torch.cuda.synchronize()
+    y_ref, bnd_ref, sda_ref, ref = _oracle(values, dy.view(batch, tokens, heads * head_size),
+                                           batch, tokens, heads, d=head_size)
+    _check("y", y.reshape(-1, heads, head_size), y_ref)
+    _check("s", s.permute(0, 2, 1, 3, 4).reshape(-1, heads, head_size, head_size), bnd_ref)
+    _check("sa", sa.reshape(-1, heads, head_size), sda_ref)
+    for name, grad in zip(NAMES, grads):
+        _check(f"d{name}", grad.reshape(-1, heads, head_size), ref["d" + name])

@@ -1,4 +1,5 @@
-"""GPU parity of the StateTune training path (chunked forward + backward).
+"""GPU parity of the StateTune training path (forward + backward; head size 64
+on the chunked MFMA kernels, 128 and 256 on the per-token fp32 kernels).
 
 Expected values: the fp64 oracle forward (boundary and state_dot_a
 definitions of /root/reference/tests/tmix/wkv7/statetune/test.py:39-88) and
@@ -50,11 +51,11 @@ def _check(name, actual, expected, tol=TOL):
 
 def _run(case, meta, *, scale, ds_std=0.01, seed=5, decay_mode=DECAY_RAW_W, public=False):
     offsets, starts, ends = (torch.from_numpy(x).to(DEV) for x in meta[:3])
-    n_tok, heads, _ = case["r"].shape
+    n_tok, heads, d = case["r"].shape
     batch = offsets.numel() - 1
     g = torch.Generator().manual_seed(seed)
-    dy = torch.randn((n_tok, heads, 64), generator=g).to(case["r"].dtype)
-    ds = torch.randn((batch, heads, 64, 64), generator=g) * ds_std
+    dy = torch.randn((n_tok, heads, d), generator=g).to(case["r"].dtype)
+    ds = torch.randn((batch, heads, d, d), generator=g) * ds_std
     s0 = case["state_pool"][:batch].clone().to(DEV).requires_grad_(True)
     toks = [case[nm].to(DEV).requires_grad_(True) for nm in NAMES]
     if public:
@@ -168,3 +169,53 @@ def test_initial_state_not_mutated_and_boundary_not_differentiable():
     torch.cuda.synchronize()
     assert torch.equal(s0, before)
     assert not bnd.requires_grad and not sda.requires_grad
+
+
+# ---------------------------------------------------------------- head sizes 128 and 256 ----
+
+
+@pytest.mark.parametrize("head_size", (128, 256))
+@pytest.mark.parametrize("lengths,chunk", [((40, 7), 16), ((70,), 64), ((33, 16, 1), 5)])
+def test_large_heads_forward_and_gradients(head_size, lengths, chunk):
+    """Head sizes 128 and 256 (per-token kernels): caller chunks of 16 tokens
+    or fewer run as they are, longer ones are split into 16-token kernel
+    chunks (the boundary output still holds each caller chunk's start)."""
+    meta = oracle.chunk_metadata(lengths, chunk)
+    case = workloads.make_case(lengths=lengths, heads=2, head_size=head_size,
+                               dtype=torch.bfloat16, seed=90 + chunk, state_std=0.1)
+    out, grads, dy, ds = _run(case, meta, scale=0.5)
+    ref_out, ref_grads = _oracle(case, meta, _np(case["w"]), scale=0.5, dy=dy, ds=ds,
+                                 batch=len(lengths))
+    _compare(out, grads, ref_out, ref_grads)
+
+
+@pytest.mark.parametrize("head_size", (128, 256))
+def test_large_heads_public_logits_fp16(head_size):
+    """The public (decay logits) entry at head sizes 128/256 with fp16 tokens."""
+    lengths = (21, 12)
+    meta = oracle.chunk_metadata(lengths, 8)
+    g = torch.Generator().manual_seed(101)
+    n = sum(lengths)
+    case = {nm: (torch.randn((n, 1, head_size), generator=g) * 0.2).to(torch.float16)
+            for nm in NAMES}
+    case["w"] = (torch.randn((n, 1, head_size), generator=g) * 2.0).to(torch.float16)
+    case["state_pool"] = torch.randn((2, 1, head_size, head_size), generator=g) * 0.05
+    out, grads, dy, ds = _run(case, meta, scale=0.75, public=True)
+    x = _np(case["w"])
+    w = oracle.retention_from_logits(x)
+    ref_out, ref_grads = _oracle(case, meta, w, scale=0.75, dy=dy, ds=ds, batch=2)
+    _compare(out, grads, ref_out, ref_grads, dw_factor=w * oracle.retention_log_derivative(x))
+
+
+def test_large_heads_backward_deterministic():
+    """Head size 256 splits each (sequence, head) over four workgroups whose
+    per-key sums are added in a fixed order: repeated backward passes are
+    bitwise equal."""
+    lengths = (35,)
+    meta = oracle.chunk_metadata(lengths, 16)
+    case = workloads.make_case(lengths=lengths, heads=1, head_size=256, dtype=torch.bfloat16,
+                               seed=7, state_std=0.1)
+    _, g1, _, _ = _run(case, meta, scale=1.0)
+    _, g2, _, _ = _run(case, meta, scale=1.0)
+    for nm in (*NAMES, "s0"):
+        assert torch.equal(g1[nm], g2[nm]), nm
