@@ -71,13 +71,20 @@ def _parse():
     p.add_argument("--warmup", type=int, default=50)
     p.add_argument("--workload", default="all",
                    choices=("all", "decode", "decode_fp16", "decode_fused", "prefill", "training",
-                            "recurrent_long", "copy"),
+                            "recurrent_long", "copy", "matrix"),
                    help="all: decode headline line plus the prefill, training and "
-                        "long-sequence legs")
+                        "long-sequence legs; matrix: the reference operator benchmark's "
+                        "case matrix with its correctness gate")
     p.add_argument("--prefill-steps", type=int, default=20)
     p.add_argument("--training-steps", type=int, default=10)
     p.add_argument("--cpu-seconds", type=float, default=8.0,
                    help="bound on the CPU-baseline sample (0 disables it)")
+    p.add_argument("--matrix-dtype", default="bfloat16", choices=("bfloat16", "float16"))
+    p.add_argument("--matrix-stress", action="store_true", help="add the stress cases")
+    p.add_argument("--matrix-warmup", type=int, default=5)
+    p.add_argument("--matrix-samples", type=int, default=30)
+    p.add_argument("--matrix-sample-iters", type=int, default=4)
+    p.add_argument("--matrix-seed", type=int, default=20260804)
     return p.parse_args()
 
 
@@ -888,6 +895,205 @@ def bench_recurrent_long(args):
     }
 
 
+# The reference operator benchmark's case matrix (benchmarks/tmix/wkv7/bench.py:132-172):
+# 21 (B, T) cases, operator shapes h32/h40/h64 at D=64, and the stress cases.
+MATRIX_BT = ((1, 1), (1, 2), (1, 4), (1, 8), (1, 16), (1, 32), (1, 64), (1, 128), (1, 256),
+             (2, 1), (4, 1), (8, 1), (16, 1), (32, 1), (64, 1), (128, 1), (256, 1),
+             (2, 2), (4, 4), (8, 8), (16, 16))
+MATRIX_SHAPES = {"h32d64": 32, "h40d64": 40, "h64d64": 64}
+MATRIX_STRESS = {
+    "stress_decode_b320_t1": (1,) * 320,
+    "stress_decode_b2048_t1": (1,) * 2048,
+    "stress_equal_b320_t16": (16,) * 320,
+    "stress_ragged_b320_t1_to_t16": tuple(range(1, 17)) * 20,
+    "stress_ragged_long_b32": (1, 4, 8, 16, 32, 64, 96, 128) * 4,
+    "stress_ragged_skew_b32": (128,) + (1,) * 31,
+}
+# fp32io16_recurrent relative-RMSE limits (reference tests/fixtures/tolerances-v1.json:8-11).
+MATRIX_RMSE_LIMIT = 0.002
+
+
+def percentile(values, q):
+    """Linear-interpolated percentile of ``values`` at ``q`` in [0, 1]
+    (the reference bench's statistic, bench.py:581-592)."""
+    if not values or not 0.0 <= q <= 1.0:
+        raise ValueError("percentile needs samples and q in [0, 1]")
+    ordered = sorted(values)
+    pos = (len(ordered) - 1) * q
+    lo, hi = int(pos // 1), int(-(-pos // 1))
+    return ordered[lo] + (ordered[hi] - ordered[lo]) * (pos - lo)
+
+
+def relative_rmse(actual, expected):
+    """rmse(actual - expected) / max(rmse(expected), 1e-6), in fp32."""
+    diff = actual.float() - expected.float()
+    base = expected.float().square().mean().sqrt().clamp_min(1e-6)
+    return float((diff.square().mean().sqrt() / base).item())
+
+
+def fp32_gate_reference(r, x, k, v, a, b, pool, cu, slots, bias=None, scale=1.0):
+    """fp32 torch restatement of the decay-logits recurrence for the matrix
+    gate, on the tokens' device: one step per token position, batched over the
+    sequences still running (elementwise products and sums, no batched GEMM).
+    Returns (output fp32 [N,H,D], updated copy of the pool)."""
+    import torch
+
+    lengths = (cu[1:] - cu[:-1]).tolist()
+    starts = cu[:-1].long()
+    slot_idx = slots.long()
+    state = pool.float().index_select(0, slot_idx).clone()
+    out = torch.empty(r.shape, device=r.device, dtype=torch.float32)
+    h, d = r.shape[1], r.shape[2]
+    bias_f = None if bias is None else bias.float().reshape(h, d)
+    len_t = torch.tensor(lengths, device=r.device)
+    for t in range(max(lengths)):
+        act = torch.nonzero(len_t > t).flatten()
+        tok = starts.index_select(0, act) + t
+        xs = x.index_select(0, tok).float()
+        if bias_f is not None:
+            xs = xs + bias_f
+        w = torch.exp(-0.6065306597126334 * torch.sigmoid(xs))
+        s = state.index_select(0, act)
+        sa = (a.index_select(0, tok).float().unsqueeze(-1) * s).sum(dim=2)
+        s = (w.unsqueeze(-1) * s + b.index_select(0, tok).float().unsqueeze(-1) * sa.unsqueeze(2)
+             + k.index_select(0, tok).float().unsqueeze(-1) * v.index_select(0, tok).float()
+             .unsqueeze(2))
+        state.index_copy_(0, act, s)
+        out.index_copy_(0, tok, scale * (r.index_select(0, tok).float().unsqueeze(-1) * s)
+                        .sum(dim=2))
+    new_pool = pool.float().clone()
+    new_pool.index_copy_(0, slot_idx, state)
+    return out, new_pool
+
+
+def bench_matrix(args):
+    """The reference operator benchmark (benchmarks/tmix/wkv7/bench.py) on this
+    build: for every case of the (B, T) matrix (plus the stress cases with
+    --matrix-stress) and operator shape, the reference's input recipe
+    (bench.py:309-371: r*0.15, decay logits*4.0, k/v/a/b*0.08, a pool of B+4
+    slots ~ N(0, 0.02), state_indices reversed, seed + case index), its
+    correctness gate (bench.py:374-501: relative RMSE of output and written
+    state <= 0.002 against an fp32 recurrence, untouched slots bitwise equal,
+    a second launch bitwise equal, finite values) and its timing (bench.py:
+    542-578: warm-up, then samples of consecutive in-place launches, each
+    sample from a reset pool, timed with events; p10/p50/p90 and tok_s_p50).
+    Launches go through recurrent_fp32_from_decay_logits with a validated
+    ticket, as the reference's timed boundary does. Each row adds the HBM
+    rate of the algorithmic bytes at p50."""
+    import torch
+
+    import flashrwkv_amd
+
+    if flashrwkv_amd._C is None:
+        raise SystemExit("flashrwkv_amd native library is not built")
+    ops = flashrwkv_amd._C.ops
+    dev = torch.device("cuda:0")
+    dtype = {"bfloat16": torch.bfloat16, "float16": torch.float16}[args.matrix_dtype]
+    cases = [(f"{bsz}x{t}", (t,) * bsz) for bsz, t in MATRIX_BT]
+    if args.matrix_stress:
+        cases += list(MATRIX_STRESS.items())
+    rows = []
+    for shape_name, heads in MATRIX_SHAPES.items():
+        d = 64
+        for index, (label, lengths) in enumerate(cases):
+            bsz, n_tok = len(lengths), sum(lengths)
+            gen = torch.Generator(device=dev).manual_seed(args.matrix_seed + index)
+
+            def rnd(scale):
+                return (torch.randn((n_tok, heads, d), device=dev, generator=gen) * scale).to(
+                    dtype)
+
+            r, x, k, v, a, b = rnd(0.15), rnd(4.0), rnd(0.08), rnd(0.08), rnd(0.08), rnd(0.08)
+            offsets = [0]
+            for length in lengths:
+                offsets.append(offsets[-1] + length)
+            cu = torch.tensor(offsets, device=dev, dtype=torch.int32)
+            slots = torch.arange(bsz - 1, -1, -1, device=dev, dtype=torch.int32)
+            pool = torch.randn((bsz + 4, heads, d, d), device=dev, generator=gen) * 0.02
+            ticket = flashrwkv_amd.prepare_recurrent_metadata(
+                cu, slots, total_tokens=n_tok, state_pool_size=bsz + 4)
+            # Correctness gate.
+            y_ref, pool_ref = fp32_gate_reference(r, x, k, v, a, b, pool, cu, slots)
+            outs = []
+            for _ in range(2):
+                st = pool.clone()
+                y = flashrwkv_amd.infer_recurrent_fp32io16_forward_varlen(
+                    r, x, k, v, a, b, state_pool=st, cu_seqlens=cu, state_indices=slots,
+                    validated_metadata=ticket)
+                outs.append((y, st))
+            torch.cuda.synchronize()
+            (y, st), (y2, st2) = outs
+            act = slots.long()
+            unused = torch.tensor([i for i in range(bsz + 4) if i not in set(act.tolist())],
+                                  device=dev, dtype=torch.long)
+            gate = {
+                "output_relative_rmse": relative_rmse(y, y_ref),
+                "state_relative_rmse": relative_rmse(st.index_select(0, act),
+                                                     pool_ref.index_select(0, act)),
+                "untouched_slots": bool(torch.equal(st.index_select(0, unused),
+                                                    pool.index_select(0, unused))),
+                "deterministic": bool(torch.equal(y, y2) and torch.equal(st, st2)),
+                "finite": bool(torch.isfinite(y.float()).all()
+                               and torch.isfinite(st.index_select(0, act)).all()),
+            }
+            gate["passed"] = bool(gate["finite"] and gate["untouched_slots"]
+                                  and gate["deterministic"]
+                                  and gate["output_relative_rmse"] <= MATRIX_RMSE_LIMIT
+                                  and gate["state_relative_rmse"] <= MATRIX_RMSE_LIMIT)
+            row = {"operator_shape": shape_name, "case": label, "B": bsz,
+                   "T": lengths[0] if len(set(lengths)) == 1 else None,
+                   "total_tokens": n_tok, "dtype": args.matrix_dtype, "correctness": gate}
+            if gate["passed"]:
+                out = torch.empty_like(v)
+                state = pool.clone()
+
+                def launch():
+                    ops.recurrent_fp32_from_decay_logits(cu, slots, state, r, x, k, v, a, b,
+                                                         out, 1.0, None, ticket, -1)
+
+                for _ in range(args.matrix_warmup):
+                    state.copy_(pool)
+                    for _ in range(args.matrix_sample_iters):
+                        launch()
+                torch.cuda.synchronize()
+                samples = []
+                for _ in range(args.matrix_samples):
+                    state.copy_(pool)
+                    e0 = torch.cuda.Event(enable_timing=True)
+                    e1 = torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    for _ in range(args.matrix_sample_iters):
+                        launch()
+                    e1.record()
+                    e1.synchronize()
+                    samples.append(e0.elapsed_time(e1) / args.matrix_sample_iters)
+                p50 = percentile(samples, 0.5)
+                nbytes = bsz * heads * 2 * d * d * 4 + n_tok * heads * 7 * d * 2
+                row["timing"] = {
+                    "p10_ms": round(percentile(samples, 0.1), 6), "p50_ms": round(p50, 6),
+                    "p90_ms": round(percentile(samples, 0.9), 6),
+                    "tok_s_p50": round(n_tok * 1000.0 / p50, 3),
+                    "hbm_GBps_p50": round(nbytes / (p50 * 1e-3) / 1e9, 1),
+                    "algorithmic_bytes": nbytes,
+                }
+                print(f"RESULT operator_shape={shape_name} case={label} dtype={args.matrix_dtype} "
+                      f"correctness=passed p10_ms={row['timing']['p10_ms']:.6f} "
+                      f"p50_ms={p50:.6f} p90_ms={row['timing']['p90_ms']:.6f} "
+                      f"tok_s_p50={row['timing']['tok_s_p50']:.3f}", file=sys.stderr,
+                      flush=True)
+            else:
+                row["failure"] = "correctness gate failed"
+                print(f"RESULT operator_shape={shape_name} case={label} correctness=failed",
+                      file=sys.stderr, flush=True)
+            rows.append(row)
+    return {"workload": "reference operator benchmark matrix (recurrent_fp32_from_decay_logits)",
+            "warmup": args.matrix_warmup, "samples": args.matrix_samples,
+            "sample_iters": args.matrix_sample_iters, "seed": args.matrix_seed,
+            "rmse_limit": MATRIX_RMSE_LIMIT, "all_passed": all(r["correctness"]["passed"]
+                                                                 for r in rows),
+            "rows": rows}
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -920,6 +1126,8 @@ def main():
         line = {"metric": METRIC, "decode_fp16_state": bench_decode(args, fp16_state=True)}
     elif args.workload == "decode_fused":
         line = {"metric": METRIC, "decode_tmix_fused": bench_decode_fused(args)}
+    elif args.workload == "matrix":
+        line = {"metric": METRIC, "matrix": bench_matrix(args)}
     else:
         line = bench_decode(args)
         if args.workload == "all":
