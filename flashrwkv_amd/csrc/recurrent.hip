@@ -17,13 +17,17 @@
 // MI355X design. The value columns of a state are independent given the token
 // vectors (sa[v], y[v] and S[:,v] only touch column v), so the work unit is a
 // wave owning a slab of CW columns of one (sequence, head) state:
-//   * lane l holds a 4-column group (cg = l % (CW/4)) for RPL consecutive key
-//     rows (rg = l / (CW/4)), i.e. RPL float4 registers; the wave's loads and
-//     stores of a state slab are 16-byte per lane and fully coalesced;
+//   * lane l holds a 4-column group cg for RPL consecutive key rows of row
+//     group rg (NG = 64/(CW/4) row groups), i.e. RPL float4 registers; the
+//     wave's loads and stores of a state slab are 16-byte per lane;
 //   * token vectors of the lane's RPL rows are contiguous and read directly
 //     from global memory (lanes sharing rows share the cache line);
 //   * S^T a and S^T r reduce first in-lane over RPL rows, then across the
-//     NG = 64/(CW/4) row groups with xor shuffles;
+//     row groups. Multi-token shapes (CW = 16) put rg in the low lane bits
+//     (rg = l % NG), so that sum is a butterfly of DPP lane permutations
+//     inside a 16-lane row with no LDS-crossbar exchange on the token-to-token
+//     dependency chain (1.7x faster on long sequences); the decode shape
+//     (CW = 64) keeps rg in the high bits (rg = l / 16) for whole-row loads;
 //   * waves never synchronise with each other, so the kernel has no barrier.
 // Decode (T=1) is HBM-bound: per (sequence, head) it moves the 16 KiB state in
 // and out plus 7 token rows; everything is issued up front. State traffic is
@@ -90,14 +94,55 @@ __device__ __forceinline__ float phase_dither(uint32_t phase) {
   return kDitherUnit * static_cast<float>(static_cast<int32_t>(kDitherMultiplier * phase));
 }
 
+// Sum over the NG row groups of recurrent_fp32_kernel's lane layout, where
+// the row group is the low log2(NG) bits of the lane id: a butterfly of DPP
+// permutations inside a 16-lane row (xor 1 and xor 2 by quad_perm, xor 7 by
+// row_half_mirror, xor 15 by row_mirror; the masks span the 4 low bits). Each
+// step adds a lane pair symmetrically, so every lane of a group ends with the
+// same bits, and no step leaves the row (no LDS-crossbar exchange).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_read(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kCtrl, 0xF, 0xF, true));
+}
+
 template <int NG>
 __device__ __forceinline__ float reduce_row_groups(float x) {
-  // Lanes with equal column group differ in the high bits of the lane id.
-  constexpr int kCg = 64 / NG;
-#pragma unroll
-  for (int offset = kCg; offset < 64; offset <<= 1) {
-    x += __shfl_xor(x, offset, 64);
+  static_assert(NG == 4 || NG == 16, "row groups fill a quad or a DPP row");
+  x += dpp_read<0xB1>(x);  // quad_perm [1,0,3,2]
+  x += dpp_read<0x4E>(x);  // quad_perm [2,3,0,1]
+  if constexpr (NG == 16) {
+    x += dpp_read<0x141>(x);  // row_half_mirror
+    x += dpp_read<0x140>(x);  // row_mirror
   }
+  return x;
+}
+
+// The decode shape (one wave per state, CW = 64) keeps its row groups in the
+// high lane bits instead: lanes 16 rg .. 16 rg + 15 then read whole 256-byte
+// state rows per load instruction (measured 57 us against 68 us per config-1
+// step with the low-bit layout), and its single token has no dependency chain
+// to shorten.
+template <int CW>
+struct RowLayout {
+  static constexpr bool kLow = CW != 64;  // row group in the low lane bits
+};
+
+template <int NG, bool kLow>
+__device__ __forceinline__ float sum_row_groups(float x) {
+  if constexpr (kLow) {
+    return reduce_row_groups<NG>(x);
+  } else {
+#pragma unroll
+    for (int offset = 64 / NG; offset < 64; offset <<= 1) x += __shfl_xor(x, offset, 64);
+    return x;
+  }
+}
+
+// Sum over 4 row groups held in the high lane bits (xor 16, xor 32): the
+// fused TMix kernel's layout.
+__device__ __forceinline__ float reduce_row_groups_high(float x) {
+  x += __shfl_xor(x, 16, 64);
+  x += __shfl_xor(x, 32, 64);
   return x;
 }
 
@@ -153,8 +198,9 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
   const int slab = wave % kWavesPerUnit;
   const int seq = unit / num_heads;
   const int head = unit % num_heads;
-  const int cg = lane % kCg;
-  const int rg = lane / kCg;
+  constexpr bool kLowRows = RowLayout<CW>::kLow;
+  const int rg = kLowRows ? lane % kNg : lane / kCg;
+  const int cg = kLowRows ? lane / kNg : lane % kCg;
   const int row0 = rg * kRpl;
   const int col = slab * CW + 4 * cg;
 
@@ -251,10 +297,10 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
         sa.z = fmaf(aa[j], s[j].z, sa.z);
         sa.w = fmaf(aa[j], s[j].w, sa.w);
       }
-      sa.x = reduce_row_groups<kNg>(sa.x);
-      sa.y = reduce_row_groups<kNg>(sa.y);
-      sa.z = reduce_row_groups<kNg>(sa.z);
-      sa.w = reduce_row_groups<kNg>(sa.w);
+      sa.x = sum_row_groups<kNg, kLowRows>(sa.x);
+      sa.y = sum_row_groups<kNg, kLowRows>(sa.y);
+      sa.z = sum_row_groups<kNg, kLowRows>(sa.z);
+      sa.w = sum_row_groups<kNg, kLowRows>(sa.w);
       if (p.state_dot_a != nullptr && rg == 0) {
         *reinterpret_cast<float4*>(
             p.state_dot_a + (static_cast<int64_t>(t) * num_heads + head) * D + col) = sa;
@@ -282,10 +328,10 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
         y.z = fmaf(rr[j], s[j].z, y.z);
         y.w = fmaf(rr[j], s[j].w, y.w);
       }
-      y.x = reduce_row_groups<kNg>(y.x);
-      y.y = reduce_row_groups<kNg>(y.y);
-      y.z = reduce_row_groups<kNg>(y.z);
-      y.w = reduce_row_groups<kNg>(y.w);
+      y.x = sum_row_groups<kNg, kLowRows>(y.x);
+      y.y = sum_row_groups<kNg, kLowRows>(y.y);
+      y.z = sum_row_groups<kNg, kLowRows>(y.z);
+      y.w = sum_row_groups<kNg, kLowRows>(y.w);
       if (rg == 0) {
         const int64_t base = (static_cast<int64_t>(t) * num_heads + head) * D;
         store4<T>(out_ptr + base + col, scale * y.x, scale * y.y, scale * y.z,
@@ -384,9 +430,8 @@ int dispatch_decay(const RecurrentArgs& p, int decay_mode) {
 }
 
 // Fused TMix chain for decode and short sequences (head size 64, fp32 pool,
-// one wave per (sequence, head) state; lane layout as recurrent_fp32_kernel
-// <64, 64, 64>: lane (rg, cg) holds key rows 16rg..16rg+15 of value columns
-// 4cg..4cg+3). Per token it runs, without writing the intermediates:
+// one wave per (sequence, head) state; lane (rg, cg) = (lane / 16, lane % 16)
+// holds key rows 16rg..16rg+15 of value columns 4cg..4cg+3). Per token it runs, without writing the intermediates:
 //   producer (reference kk_a_gate): u = k k_k, kk = u / max(|u|, 1e-12),
 //     gate = sigmoid(a0 + a12), k' = k (gate k_a + 1 - k_a);
 //   WKV7 step with k', a = -kk, b = kk gate (S += b (a^T S), the RWKV-7
@@ -501,7 +546,7 @@ __global__ __launch_bounds__(64, 2) void recurrent_tmix_fused_kernel(
       ss = fmaf(u, u, ss);
     }
     const float inv =
-        __builtin_amdgcn_rcpf(fmaxf(__builtin_sqrtf(reduce_row_groups<4>(ss)), 1.0e-12f));
+        __builtin_amdgcn_rcpf(fmaxf(__builtin_sqrtf(reduce_row_groups_high(ss)), 1.0e-12f));
     // WKV7 step. sa = S^T a with a = -kk; then, row by row, the rest of the
     // producer (gate, b = kk gate, k' = k (gate k_a + 1 - k_a)), the update,
     // y = S^T r and the residual dot rkv = sum r k' r_k. Each producer value
@@ -515,10 +560,10 @@ __global__ __launch_bounds__(64, 2) void recurrent_tmix_fused_kernel(
       sa.z = fmaf(a_j, s[j].z, sa.z);
       sa.w = fmaf(a_j, s[j].w, sa.w);
     }
-    sa.x = reduce_row_groups<4>(sa.x);
-    sa.y = reduce_row_groups<4>(sa.y);
-    sa.z = reduce_row_groups<4>(sa.z);
-    sa.w = reduce_row_groups<4>(sa.w);
+    sa.x = reduce_row_groups_high(sa.x);
+    sa.y = reduce_row_groups_high(sa.y);
+    sa.z = reduce_row_groups_high(sa.z);
+    sa.w = reduce_row_groups_high(sa.w);
     float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
     float rkv = 0.0f;
 #pragma unroll
@@ -541,9 +586,9 @@ __global__ __launch_bounds__(64, 2) void recurrent_tmix_fused_kernel(
       y.z = fmaf(rj, s[j].z, y.z);
       y.w = fmaf(rj, s[j].w, y.w);
     }
-    rkv = reduce_row_groups<4>(rkv);
-    const float x[4] = {p.scale * reduce_row_groups<4>(y.x), p.scale * reduce_row_groups<4>(y.y),
-                        p.scale * reduce_row_groups<4>(y.z), p.scale * reduce_row_groups<4>(y.w)};
+    rkv = reduce_row_groups_high(rkv);
+    const float x[4] = {p.scale * reduce_row_groups_high(y.x), p.scale * reduce_row_groups_high(y.y),
+                        p.scale * reduce_row_groups_high(y.z), p.scale * reduce_row_groups_high(y.w)};
 
     // Consumer: per-head norm of the output, residual and gate.
     const float mean = reduce_col_groups(x[0] + x[1] + x[2] + x[3]) * (1.0f / D);
