@@ -71,7 +71,7 @@ def _parse():
     p.add_argument("--warmup", type=int, default=50)
     p.add_argument("--workload", default="all",
                    choices=("all", "decode", "decode_fp16", "decode_fused", "prefill", "training",
-                            "recurrent_long", "copy", "matrix"),
+                            "recurrent_long", "copy", "matrix", "training_large"),
                    help="all: decode headline line plus the prefill, training and "
                         "long-sequence legs; matrix: the reference operator benchmark's "
                         "case matrix with its correctness gate")
@@ -828,6 +828,64 @@ def cpu_baseline_training(t_len, heads_total, seconds):
     }
 
 
+def bench_training_large(args):
+    """StateTune at head sizes 128 and 256 (the per-token fp32 training
+    kernels): B=8, T=4096, C=H*D=4096, bf16 io, raw retention, S0 ~ N(0, 0.1),
+    dY ~ N(0, 1), dS_T ~ N(0, 0.01), caller chunks of 64 tokens (split into
+    16-token kernel chunks by the wrapper). One step = autograd forward +
+    backward. No BASELINE config uses these head sizes; this leg records their
+    cost beside config 4's D=64 step."""
+    import torch
+
+    import flashrwkv_amd
+    from flashrwkv_amd import workloads
+    from flashrwkv_amd.tmix.wkv7.statetune import statetune_recurrent_internal
+
+    if flashrwkv_amd._C is None:
+        raise SystemExit("flashrwkv_amd native library is not built")
+    dev = torch.device("cuda:0")
+    out = {}
+    for d in (128, 256):
+        batch, t_len, heads = 8, 4096, 4096 // d
+        n_tok = batch * t_len
+        tok = workloads.make_tokens(n_tok, heads, d, dtype=torch.bfloat16, seed=20260812 + d,
+                                    device=dev)
+        leaves = [tok[n].requires_grad_(True) for n in ("r", "w", "k", "v", "a", "b")]
+        gen = torch.Generator(device=dev).manual_seed(20260813 + d)
+        s0 = (torch.randn((batch, heads, d, d), generator=gen, device=dev) * 0.1
+              ).requires_grad_(True)
+        dy = torch.randn((n_tok, heads, d), generator=gen, device=dev).to(torch.bfloat16)
+        ds = torch.randn((batch, heads, d, d), generator=gen, device=dev) * 0.01
+        offsets = torch.arange(0, batch + 1, device=dev, dtype=torch.int32) * (t_len // 64)
+        starts = torch.arange(0, n_tok, 64, device=dev, dtype=torch.int32)
+        ends = starts + 64
+
+        def step():
+            for t in (*leaves, s0):
+                t.grad = None
+            y, st, _, _ = statetune_recurrent_internal(s0, offsets, starts, ends, *leaves)
+            torch.autograd.backward([y, st], [dy, ds])
+
+        step()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        steps = max(1, args.training_steps // 5)
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        e1.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        out[f"d{d}"] = {"workload": f"StateTune B=8, T=4096, H={heads}, D={d}, bf16, raw "
+                                    f"retention, 64-token caller chunks",
+                        "steps": steps, "ms_per_step": round(ms, 3),
+                        "train_tokens_per_s": round(n_tok / (ms * 1e-3), 1)}
+        del tok, leaves, s0, dy, ds
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_copy(args):
     """A plain device copy of known size: the calibration run for the
     FETCH_SIZE / WRITE_SIZE counters (bytes per dispatch vs counter KiB)."""
@@ -1128,6 +1186,8 @@ def main():
         line = {"metric": METRIC, "decode_tmix_fused": bench_decode_fused(args)}
     elif args.workload == "matrix":
         line = {"metric": METRIC, "matrix": bench_matrix(args)}
+    elif args.workload == "training_large":
+        line = {"metric": METRIC, "training_large_heads": bench_training_large(args)}
     else:
         line = bench_decode(args)
         if args.workload == "all":

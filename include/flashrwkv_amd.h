@@ -198,7 +198,9 @@ int frwkv_chunk_forward(int io_dtype, int decay_mode, int pool_dtype,
  * chunk start; state_dot_a [total_tokens,H,D] fp32 receives a_t^T S_{t-1}.
  * Replaces statetune_recurrent_fp32io16_forward_cuda
  * (csrc/sm90/tmix/wkv7/statetune_recurrent_fp32io16_forward.cu:32-224;
- * binding statetune_recurrent_fp32io16_forward.cpp:26-56). head_size 64.
+ * binding statetune_recurrent_fp32io16_forward.cpp:26-56). head_size 64
+ * runs the chunked MFMA kernel; 128 and 256 run the per-token fp32 kernel
+ * (any chunk length).
  */
 int frwkv_statetune_forward(int io_dtype, int decay_mode, int32_t num_sequences,
                             int32_t num_heads, int32_t head_size,
@@ -225,7 +227,12 @@ int frwkv_statetune_forward(int io_dtype, int decay_mode, int32_t num_sequences,
  * single-reference limit, makes its sequence's gradients NaN.
  * Replaces statetune_recurrent_fp32io16_backward_cuda
  * (csrc/sm90/tmix/wkv7/statetune_recurrent_fp32io16_backward.cu:49-676;
- * binding statetune_recurrent_fp32io16_backward.cpp:34-82). head_size 64.
+ * binding statetune_recurrent_fp32io16_backward.cpp:34-82). head_size 64
+ * runs the chunked MFMA kernel. head_size 128 and 256 run the per-token fp32
+ * kernel, whose chunks must span at most 16 tokens (a longer one makes its
+ * sequence's gradients NaN); at 256 the call takes 80 B per element of
+ * [total_tokens,H,D] of fp32 gradient slices from hipMallocAsync on stream
+ * and frees them on the same stream before it returns.
  */
 int frwkv_statetune_backward(int io_dtype, int decay_mode, int32_t num_sequences,
                              int32_t num_heads, int32_t head_size,
@@ -248,7 +255,8 @@ int frwkv_statetune_backward(int io_dtype, int decay_mode, int32_t num_sequences
  * sequence s at row s*T + t), S0 = 0, no final state. boundary
  * [B,H,T/16,D,D] fp32 receives the state every 16 tokens (entry i: the state
  * before token 16 i); state_dot_a [B,T,H,D] fp32 receives a_t^T S_{t-1}.
- * T must be a multiple of 16; head_size 64.
+ * T must be a multiple of 16; head_size 64, 128 or 256 (64 on the chunked
+ * MFMA kernel, 128 and 256 on the per-token fp32 kernel).
  * Replaces rwkv7_clampw_v3::forward / cuda_forward_v3
  * (csrc/sm90/tmix/wkv7/pretrain_recurrent_bf16_forward.cpp:20-26, 50-53;
  * kernel pretrain_recurrent_bf16_forward.cu).
@@ -260,10 +268,11 @@ int frwkv_pretrain_forward(int io_dtype, int decay_mode, int32_t batch, int32_t 
                            float* state_dot_a, void* stream);
 
 /*
- * Pretraining backward: recomputes every 64-token chunk from the boundary
- * written by frwkv_pretrain_forward (every 4th entry) and writes the six
- * token gradients (grad_decay is dL/d(decay input)). grad_output may not be
- * NULL. Replaces rwkv7_clampw_v3::backward / cuda_backward_v3
+ * Pretraining backward: recomputes every chunk from the boundary written by
+ * frwkv_pretrain_forward (head size 64: 64-token chunks from every 4th entry;
+ * 128 and 256: every 16-token entry, with the slice allocation described at
+ * frwkv_statetune_backward for 256) and writes the six token gradients
+ * (grad_decay is dL/d(decay input)). grad_output may not be NULL. Replaces rwkv7_clampw_v3::backward / cuda_backward_v3
  * (csrc/sm90/tmix/wkv7/pretrain_recurrent_bf16_forward.cpp:31-53).
  */
 int frwkv_pretrain_backward(int io_dtype, int decay_mode, int32_t batch, int32_t tokens,
