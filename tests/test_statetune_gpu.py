@@ -219,3 +219,18 @@ def test_large_heads_backward_deterministic():
     _, g2, _, _ = _run(case, meta, scale=1.0)
     for nm in (*NAMES, "s0"):
         assert torch.equal(g1[nm], g2[nm]), nm
+
+
+@pytest.mark.parametrize("head_size", (128, 256))
+def test_large_heads_long_sequence(head_size):
+    """A 1000-token sequence next to a short one (63 and 3 kernel chunks after
+    the 64 -> 16 split), S0 ~ N(0, 0.1): forward outputs, boundaries, final
+    state and every gradient against the fp64 oracle."""
+    lengths = (1000, 37)
+    meta = oracle.chunk_metadata(lengths, 64)
+    case = workloads.make_case(lengths=lengths, heads=1, head_size=head_size,
+                               dtype=torch.bfloat16, seed=123 + head_size, state_std=0.1)
+    out, grads, dy, ds = _run(case, meta, scale=1.0)
+    ref_out, ref_grads = _oracle(case, meta, _np(case["w"]), scale=1.0, dy=dy, ds=ds,
+                                 batch=len(lengths))
+    _compare(out, grads, ref_out, ref_grads)
