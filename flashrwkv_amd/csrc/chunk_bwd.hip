@@ -68,6 +68,7 @@ struct BwdSmem {
   uint16_t dy_x[kOpTile];       // scale * dY [t][v]
   uint16_t v_x[kOpTile];        // V  [t][v]
   float gc[kHead];              // 2^GC
+  float inv_gc[kHead];          // 2^-GC
   float wave_tot[4][kHead];     // per-block sums of log2 w (prepare; read by tokens)
   float carry[4][kHead];        // token scan carries
   float carry3[4][kHead];
@@ -312,7 +313,10 @@ __device__ bool prepare_bwd(BwdSmem& sm, const BwdRows& rows, const float (&bias
   col_tile(sm.ktT, x0, x1, dn0, dn1, gcv);
   if (wave == 0 && tp == 0) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sm.gc[8 * kg + e] = gcv[e];
+    for (int e = 0; e < 8; ++e) {
+      sm.gc[8 * kg + e] = gcv[e];
+      sm.inv_gc[8 * kg + e] = __builtin_amdgcn_rcpf(gcv[e]);
+    }
   }
   __syncthreads();
   return whole;
@@ -977,26 +981,48 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
       raw4(raw_cur[4], rw);
       float grad_r[4], grad_a[4], grad_b[4], grad_k[4];
       const int t = 16 * pb + n;
+      // Per-feature chunk factors of the lane's 4 consecutive features, and
+      // the block sums of the earlier token blocks, as 16-byte LDS reads.
+      const int kf0 = 16 * kb + 4 * g;
+      const float4 gam4 = *reinterpret_cast<const float4*>(&sm.gc[kf0]);
+      const float4 inv4 = *reinterpret_cast<const float4*>(&sm.inv_gc[kf0]);
+      float4 carry4 = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        if (q < pb) {
+          const float4 c = *reinterpret_cast<const float4*>(&sm.wave_tot[q][kf0]);
+          carry4.x += c.x; carry4.y += c.y; carry4.z += c.z; carry4.w += c.w;
+        }
+      }
+      const float gam_v[4] = {gam4.x, gam4.y, gam4.z, gam4.w};
+      const float inv_v[4] = {inv4.x, inv4.y, inv4.z, inv4.w};
+      const float carry_v[4] = {carry4.x, carry4.y, carry4.z, carry4.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int kf = 16 * kb + 4 * g + j;
+        const int kf = kf0 + j;
         float xin = rw[j];
         if constexpr (M == DecayMode::kLogits) {
           if (p.bias != nullptr) {
             xin += to_f32<T>(static_cast<const S16*>(p.bias)[static_cast<int64_t>(head) * kHead + kf]);
           }
         }
-        const float lg = t < ntok ? log2_retention<M>(xin) : 0.0f;
-        const float gam = sm.gc[kf];
-        const float inv_g = __builtin_amdgcn_rcpf(gam);
+        const bool on = t < ntok;
+        const float lg = on ? log2_retention<M>(xin) : 0.0f;
+        const float gam = gam_v[j];
+        const float inv_g = inv_v[j];
         // Inclusive cumulative log2 decay G_t: the block sums of earlier
         // token blocks plus a scan over this block's 16 tokens (lane n).
-        float G = prefix16(lg);
-#pragma unroll
-        for (int q = 0; q < 3; ++q) G += q < pb ? sm.wave_tot[q][kf] : 0.0f;
-        const float upg = fast_exp2(G);
-        const float dng = fast_exp2(-G);
+        const float G = prefix16(lg) + carry_v[j];
         const float upp = fast_exp2(G - lg);
+        // 2^G = 2^(G - lg) w: in raw-retention mode w is the (clamped) input,
+        // which saves an exponential; the logits mode evaluates 2^G directly.
+        float upg;
+        if constexpr (M == DecayMode::kRawW) {
+          upg = upp * (on ? __builtin_amdgcn_fmed3f(xin, 0x1p-20f, 1.0f) : 1.0f);
+        } else {
+          upg = fast_exp2(G);
+        }
+        const float dng = fast_exp2(-G);
         const float dRt = acc_s[j] + inv_g * acc_r[j];
         const float dAt = acc_z[j] + inv_g * acc_a[j];
         const float dBc = acc_bh[j] + gam * acc_bt[j];  // dBh + g dBt
