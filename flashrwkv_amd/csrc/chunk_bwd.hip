@@ -1094,9 +1094,9 @@ __global__ __launch_bounds__(kChunkThreads, 1) void chunk_bwd_kernel(ChunkBwdPar
             const float sig = __builtin_amdgcn_rcpf(1.0f + fast_exp2(-kLog2E * xin));
             d = dlg * (-kExpNegHalf) * sig * (1.0f - sig);
           } else {
-            // log2 w is clamped to [-20, 0]: zero derivative outside.
-            const float raw = __builtin_amdgcn_logf(xin);
-            d = (raw < kLog2Min || raw > 0.0f) ? 0.0f : dlg * __builtin_amdgcn_rcpf(xin);
+            // log2 w is clamped to [-20, 0]: zero derivative outside, i.e.
+            // for w outside [2^-20, 1].
+            d = (xin < 0x1p-20f || xin > 1.0f) ? 0.0f : dlg * __builtin_amdgcn_rcpf(xin);
           }
           dwv[j] = d;
         }
