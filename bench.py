@@ -1,6 +1,6 @@
 """WKV7 benchmark on one MI355X (driver contract: one JSON line on stdout).
 
-Default workload: batched decode, B=256 sequences, H=40
+Default workload (benchmark config 1): batched decode, B=256 sequences, H=40
 heads, D=64, T=1 per step, bf16 token io, fp32 state pool [256,40,64,64]
 updated in place, S0 ~ N(0, 0.1), retention w = exp(-exp(u)), u ~ U(-5,0)
 (raw-retention mode). One step = one launch over the whole batch.
@@ -18,7 +18,7 @@ the launch stream bracket the timed region; the average launch duration is
 elapsed / steps.
 
 The default run (--workload all) adds a "chunked_prefill" object measuring
-BASELINE config 3 (chunked prefill, B=16, T=4096, H=32) against the bf16 MFMA
+benchmark config 3 (chunked prefill, B=16, T=4096, H=32) against the bf16 MFMA
 roofline; --workload prefill makes that the headline line instead.
 """
 
@@ -331,7 +331,7 @@ def bench_decode(args, fp16_state=False):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "data": "synthetic (seeded; BASELINE config 1 distributions)",
+        "data": "synthetic (seeded; benchmark config 1 distributions)",
         "config": {
             "workload": "wkv7_decode_cfg1: B=256, H=40, D=64, T=1 per step, bf16 io, "
                         "fp32 state pool in place, raw retention, 4 rotating pool "
@@ -536,7 +536,7 @@ def _kernel_ms(fn, steps, stream, warmup=2):
 
 
 def bench_prefill(args):
-    """chunked prefill, B=16, T=4096, H=32, D=64, bf16 io,
+    """benchmark config 3: chunked prefill, B=16, T=4096, H=32, D=64, bf16 io,
     raw retention u ~ U(-8, 0), fp32 state pool updated in place."""
     import torch
 
@@ -618,7 +618,7 @@ def bench_prefill(args):
 
 
 def bench_prefill_varlen(args):
-    """BASELINE config 3, varlen batch: 64 packed sequences with lengths
+    """benchmark config 3, varlen batch: 64 packed sequences with lengths
     uniform in [128, 4096] (seeded), H=32, D=64, bf16 io, u ~ U(-8, 0), fp32
     pool. Algorithmic FLOPs count each sequence's chunks at their real length
     (a partial last chunk of c tokens costs chunk_flops(c))."""
@@ -691,7 +691,7 @@ def bench_prefill_varlen(args):
 
 
 def bench_training(args):
-    """chunked forward + backward (StateTune), B=8, T=4096,
+    """benchmark config 4: chunked forward + backward (StateTune), B=8, T=4096,
     H=64, D=64, chunk 64, bf16 io, raw retention, S0 ~ N(0, 0.1), dY ~ N(0, 1),
     dS_T ~ N(0, 0.01). One step = autograd forward + backward."""
     import torch
@@ -833,7 +833,7 @@ def bench_training_large(args):
     kernels): B=8, T=4096, C=H*D=4096, bf16 io, raw retention, S0 ~ N(0, 0.1),
     dY ~ N(0, 1), dS_T ~ N(0, 0.01), caller chunks of 64 tokens (split into
     16-token kernel chunks by the wrapper). One step = autograd forward +
-    backward. No BASELINE config uses these head sizes; this leg records their
+    backward. No benchmark config uses these head sizes; this leg records their
     cost beside config 4's D=64 step."""
     import torch
 
@@ -902,7 +902,7 @@ def bench_copy(args):
 
 
 def bench_recurrent_long(args):
-    """B=8, T=4096, H=32, D=64, bf16 io, fp32 state, S0 = 0,
+    """benchmark config 2: B=8, T=4096, H=32, D=64, bf16 io, fp32 state, S0 = 0,
     through the per-token recurrent kernel and through the chunked kernel."""
     import torch
 
@@ -1167,7 +1167,7 @@ def main():
             "n_gpus": 1, "steps": args.prefill_steps, "warmup": 3,
             "ms_per_step": pre["ms_per_step"], "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-            "data": "synthetic (seeded; BASELINE config 3 distributions)",
+            "data": "synthetic (seeded; benchmark config 3 distributions)",
             "config": {"workload": pre["workload"], "parallelism": "single GPU"},
             "roofline": pre["roofline"], "hbm": pre["hbm"],
         }

@@ -435,7 +435,7 @@ int dispatch_decay(const RecurrentArgs& p, int decay_mode) {
 //   producer (reference kk_a_gate): u = k k_k, kk = u / max(|u|, 1e-12),
 //     gate = sigmoid(a0 + a12), k' = k (gate k_a + 1 - k_a);
 //   WKV7 step with k', a = -kk, b = kk gate (S += b (a^T S), the RWKV-7
-//     update as BASELINE's configs state it), y = scale S^T r;
+//     update as the benchmark configs state it), y = scale S^T r;
 //   consumer (reference lnx_rkvres_xg): out = ((y - mean) rstd ln_w + ln_b
 //     + rkv v) g with rstd = 1 / sqrt(var + 64e-5), rkv = sum r k' r_k.
 // Norms over key features reduce across the four row groups (xor 16, 32),

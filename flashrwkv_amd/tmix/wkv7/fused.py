@@ -14,7 +14,7 @@ through HBM (composed in its ``tests/tmix/wkv7/test.py:310-414``):
 kernel that keeps every intermediate in registers (and in fp32, with no
 rounding to 16 bits between the stages). The WKV7 inputs are ``k = new_k``,
 ``a = -kk`` and ``b = kk gate``: the RWKV-7 update
-``S = diag(w) S + (kk gate)((-kk)^T S) + k v^T`` as BASELINE's configs state it.
+``S = diag(w) S + (kk gate)((-kk)^T S) + k v^T`` as the benchmark configs state it.
 (The reference's chain test passes the two directions the other way round,
 ``a = kka, b = neg_kk``, to both its kernel and its oracle, so it checks the
 composition rather than which ordering is RWKV-7's.)

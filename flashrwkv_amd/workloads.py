@@ -87,7 +87,7 @@ def make_case(*, lengths, heads: int, head_size: int, dtype: torch.dtype, seed: 
 def varlen_lengths(count: int = 64, low: int = 128, high: int = 4096,
                    seed: int = 20260807) -> list[int]:
     """Sequence lengths uniform in [low, high] (seeded, CPU). The defaults are
-    BASELINE config 3's varlen batch: 64 sequences, lengths in [128, 4096]."""
+    benchmark config 3's varlen batch: 64 sequences, lengths in [128, 4096]."""
     g = _gen(seed, "cpu")
     return [int(x) for x in torch.randint(low, high + 1, (count,), generator=g)]
 

@@ -405,7 +405,7 @@ def tmix_fused(r, w, k, v, a12, g, k_k, a0, k_a, r_k, ln_weight, ln_bias, state_
                cu_seqlens, state_indices, scale=1.0):
     """The fused chain, with no rounding between its stages: the producer
     (:func:`kk_a_gate`) gives the WKV7 inputs k = new_k, a = -kk and
-    b = kk gate (the RWKV-7 update S += (kk gate)((-kk)^T S), as BASELINE's
+    b = kk gate (the RWKV-7 update S += (kk gate)((-kk)^T S), as the benchmark
     configs state it), then :func:`forward_varlen` with retention ``w``, then
     the consumer (:func:`lnx_rkvres_xg`) with the producer's new_k. Token
     tensors ``[N, H, D]``, vectors ``[H*D]``; returns ``(out [N,H,D], pool)``."""

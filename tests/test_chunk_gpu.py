@@ -158,7 +158,7 @@ def test_chunk_matches_recurrent_kernel_and_is_deterministic():
 
 
 def test_config3_full_shape_sampled_heads():
-    """BASELINE config 3 at full shape; heads are independent, so the oracle
+    """benchmark config 3 at full shape; heads are independent, so the oracle
     runs on a sample of (sequence, head) pairs at the full T=4096."""
     batch, t_len, heads = 16, 4096, 32
     case = workloads.make_case(lengths=[t_len] * batch, heads=heads, head_size=64,
@@ -184,7 +184,7 @@ def test_config3_full_shape_sampled_heads():
 
 
 def test_config3_varlen_batch_sampled_sequences():
-    """BASELINE config 3's varlen batch: 64 packed sequences with lengths
+    """benchmark config 3's varlen batch: 64 packed sequences with lengths
     uniform in [128, 4096] (cu_seqlens offsets, slots permuted). Sequences and
     heads are independent, so the oracle checks a sample of (sequence, head)
     pairs at their full lengths, including the shortest and longest."""

@@ -126,7 +126,7 @@ def test_public_logits_matches_reference_case():
 
 
 def test_config4_sampled_heads_full_length():
-    """BASELINE config 4 shape (B=8, T=4096, H=64, chunk 64, S0 ~ N(0, 0.1),
+    """benchmark config 4 shape (B=8, T=4096, H=64, chunk 64, S0 ~ N(0, 0.1),
     dS_T ~ N(0, 0.01)); heads are independent, so the fp64 oracle checks a
     sample of (sequence, head) pairs at the full length."""
     batch, t_len, heads = 8, 4096, 64
