@@ -52,3 +52,19 @@ def test_relative_rmse_definition():
     e = torch.tensor([3.0, 4.0])
     assert bench.relative_rmse(e, e) == 0.0
     assert abs(bench.relative_rmse(e + 1.0, e) - 1.0 / np.sqrt(12.5)) < 1e-6
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU; --gpus N > 1 exits with status 2 and a JSON
+    message, before anything touches a device."""
+    import json
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    proc = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"],
+                          capture_output=True, text=True, timeout=120)
+    assert proc.returncode == 2
+    line = json.loads(proc.stdout.strip().splitlines()[-1])
+    assert "one GPU" in line["error"]
