@@ -132,18 +132,15 @@ __device__ __forceinline__ float sum_row_groups(float x) {
   if constexpr (kLow) {
     return reduce_row_groups<NG>(x);
   } else {
-#pragma unroll
-    for (int offset = 64 / NG; offset < 64; offset <<= 1) x += __shfl_xor(x, offset, 64);
-    return x;
+    static_assert(NG == 4, "high-bit row groups are the lanes' two top bits");
+    return add_xor32(add_xor16(x));
   }
 }
 
 // Sum over 4 row groups held in the high lane bits (xor 16, xor 32): the
 // fused TMix kernel's layout.
 __device__ __forceinline__ float reduce_row_groups_high(float x) {
-  x += __shfl_xor(x, 16, 64);
-  x += __shfl_xor(x, 32, 64);
-  return x;
+  return add_xor32(add_xor16(x));
 }
 
 // Unit ranges: sequence s covers tokens cu_seqlens[s] .. cu_seqlens[s+1]-1,
@@ -455,10 +452,9 @@ __device__ __forceinline__ float sigmoid_fast(float x) {
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-kLog2E * x));
 }
 
+// Sum over the 16 lanes of a DPP row (the DPP butterfly of reduce_row_groups).
 __device__ __forceinline__ float reduce_col_groups(float x) {
-#pragma unroll
-  for (int offset = 1; offset < 16; offset <<= 1) x += __shfl_xor(x, offset, 64);
-  return x;
+  return reduce_row_groups<16>(x);
 }
 
 template <typename T, DecayMode M>

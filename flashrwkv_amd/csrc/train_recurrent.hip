@@ -34,8 +34,9 @@
 // sums to its own fp32 slice and a second kernel adds the slices in group
 // order, so the gradients are deterministic. Chunks are walked in reverse and
 // must be at most 16 tokens; S_{t-1} is recomputed from the chunk's stored
-// start state (never by dividing by the decay), or from a register copy of the
-// state 8 tokens into the chunk.
+// start state (never by dividing by the decay), from a register copy of the
+// state 8 tokens into the chunk, or at D = 128 from an LDS copy of the state 4
+// tokens in.
 //
 // The recomputed states are bitwise equal to the forward's: both kernels use
 // the same lane layout per head size, the same fma forms and the same
@@ -152,21 +153,28 @@ __device__ __forceinline__ float dpp(float x) {
 
 // Sum over the key row groups of a wave: lanes sharing lane % kCg. Inside a
 // 16-lane DPP row, rotations by kCg, 2 kCg, ... (row_ror) gather one residue
-// class; the four rows are then added with two lane exchanges.
-template <int kCg>
+// class; the four rows are then added across lanes xor 16 and xor 32, either
+// with the VALU lane swaps (kSwap: the backward, whose single wave per SIMD
+// waits on every LDS round trip) or with LDS-crossbar shuffles (the forward,
+// whose VALU is the busier unit). Addition is commutative, so both forms give
+// the same bits and the backward's recomputed states match the forward's.
+template <int kCg, bool kSwap>
 __device__ __forceinline__ float sum_keys(float x) {
   if constexpr (kCg <= 2) x += dpp<0x122>(x);  // row_ror:2
   x += dpp<0x124>(x);                          // row_ror:4
   x += dpp<0x128>(x);                          // row_ror:8
-  x += __shfl_xor(x, 16, 64);
-  x += __shfl_xor(x, 32, 64);
-  return x;
+  if constexpr (kSwap) {
+    return add_xor32(add_xor16(x));
+  } else {
+    x += __shfl_xor(x, 16, 64);
+    return x + __shfl_xor(x, 32, 64);
+  }
 }
 
-template <int kCg>
+template <int kCg, bool kSwap>
 __device__ __forceinline__ float4 sum_keys4(float4 x) {
-  return make_float4(sum_keys<kCg>(x.x), sum_keys<kCg>(x.y), sum_keys<kCg>(x.z),
-                     sum_keys<kCg>(x.w));
+  return make_float4(sum_keys<kCg, kSwap>(x.x), sum_keys<kCg, kSwap>(x.y),
+                     sum_keys<kCg, kSwap>(x.z), sum_keys<kCg, kSwap>(x.w));
 }
 
 // Sum over the kCg column lanes of a row group (quad_perm xor 1, xor 2).
@@ -224,7 +232,7 @@ __device__ __forceinline__ void store_slab(float* base, const float4 (&s)[kRpl],
 // One forward step on a lane's state slab: s <- diag(w) s + b sa^T + k v^T
 // with sa = s^T a (returned, the lane's 4 columns), token rows read from LDS.
 // The fma forms are those of the inference kernels.
-template <int D, typename T>
+template <int D, typename T, bool kSwap>
 __device__ __forceinline__ float4 step_state(float4 (&s)[Layout<D>::kRpl], const uint16_t* a_row,
                                              const uint16_t* b_row, const uint16_t* k_row,
                                              const float* w_row, float4 vv, int row0) {
@@ -243,7 +251,7 @@ __device__ __forceinline__ float4 step_state(float4 (&s)[Layout<D>::kRpl], const
       sa.w = fmaf(aa[j], x.w, sa.w);
     }
   }
-  sa = sum_keys4<Layout<D>::kCg>(sa);
+  sa = sum_keys4<Layout<D>::kCg, kSwap>(sa);
 #pragma unroll
   for (int q = 0; q < kRpl / 4; ++q) {
     float bb[4], kk[4];
@@ -417,7 +425,8 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_fwd_kernel(TrainPar
     const FwdStage<D>& cur = st[buf];
     for (int i = 0; i < n; ++i) {
       const float4 vv = decode4f<T>(lds8(&cur.v[i][wcol]));
-      const float4 sa = step_state<D, T>(s, cur.a[i], cur.b[i], cur.k[i], cur.w[i], vv, row0);
+      const float4 sa =
+          step_state<D, T, false>(s, cur.a[i], cur.b[i], cur.k[i], cur.w[i], vv, row0);
       float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
       for (int q = 0; q < kRpl / 4; ++q) {
@@ -432,7 +441,7 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_fwd_kernel(TrainPar
           y.w = fmaf(rr[j], x.w, y.w);
         }
       }
-      y = sum_keys4<L::kCg>(y);
+      y = sum_keys4<L::kCg, false>(y);
       if (rg == 0) {
         const int64_t e = (t0 + i) * hd + head_off + col;
         *reinterpret_cast<float4*>(p.state_dot_a + e) = sa;
@@ -472,6 +481,11 @@ struct BwdSmem {
   // Per-wave partial sums over the wave's columns: [buffer][wave][gradient][key]
   // with gradients dr, dk, db, dw, da.
   float red[2][kNW][5][D];
+  // D = 128: the workgroup's state slab 4 tokens into the chunk ([key][column],
+  // each lane reading back only what it wrote), which the LDS budget allows
+  // there and not at D = 256.
+  static constexpr bool kMid4 = D == 128;
+  float mid4[kMid4 ? D : 1][kMid4 ? kCols : 4];
 };
 
 template <int D, typename T, DecayMode M>
@@ -608,13 +622,29 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_bwd_kernel(TrainPar
     const float* ck = p.ckpt + ch.ckpt_off;
     auto step = [&](float4 (&s)[kRpl], int i) {
       const float4 vv = decode4f<T>(lds8(&sm.v[i][wcol]));
-      step_state<D, T>(s, sm.a[i], sm.b[i], sm.k[i], sm.w[i], vv, row0);
+      step_state<D, T, true>(s, sm.a[i], sm.b[i], sm.k[i], sm.w[i], vv, row0);
     };
-    // S^8, the state 8 tokens into the chunk (when the chunk is longer).
+    // S^8, the state 8 tokens into the chunk (when the chunk is longer), and
+    // at D = 128 also S^4 in LDS, passed on the way.
+    constexpr bool kMid4 = BwdSmem<D>::kMid4;
+    auto mid4_row = [&](int j) -> float4* {
+      return reinterpret_cast<float4*>(&sm.mid4[kMid4 ? row0 + j : 0][kMid4 ? wcol : 0]);
+    };
     float4 cm[kRpl];
-    if (n > 8) {
+    const int last = n > 8 ? 8 : (kMid4 && n > 4 ? 4 : 0);
+    if (last > 0) {
       load_slab<D, kRpl>(cm, ck, row0, col);
-      for (int i = 0; i < 8; ++i) step(cm, i);
+      for (int i = 0; i < last; ++i) {
+        if (kMid4 && i == 4) {
+#pragma unroll
+          for (int j = 0; j < kRpl; ++j) *mid4_row(j) = cm[j];
+        }
+        step(cm, i);
+      }
+      if (kMid4 && last == 4) {
+#pragma unroll
+        for (int j = 0; j < kRpl; ++j) *mid4_row(j) = cm[j];
+      }
     }
 
     for (int jt = n - 1; jt >= 0; --jt) {
@@ -625,6 +655,10 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_bwd_kernel(TrainPar
 #pragma unroll
         for (int j = 0; j < kRpl; ++j) s[j] = cm[j];
         i0 = 8;
+      } else if (kMid4 && jt >= 4) {
+#pragma unroll
+        for (int j = 0; j < kRpl; ++j) s[j] = *mid4_row(j);
+        i0 = 4;
       } else {
         load_slab<D, kRpl>(s, ck, row0, col);
       }
@@ -648,7 +682,7 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_bwd_kernel(TrainPar
           sa.w = fmaf(aa[j], x.w, sa.w);
         }
       }
-      sa = sum_keys4<L::kCg>(sa);
+      sa = sum_keys4<L::kCg, true>(sa);
 
       float(&red)[5][D] = sm.red[buf][wave];
       float4 dsa = make_float4(0.f, 0.f, 0.f, 0.f), dv = dsa;
@@ -695,8 +729,8 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_bwd_kernel(TrainPar
           *reinterpret_cast<float4*>(&red[3][r4]) = make_float4(pw[0], pw[1], pw[2], pw[3]);
         }
       }
-      dsa = sum_keys4<L::kCg>(dsa);
-      dv = sum_keys4<L::kCg>(dv);
+      dsa = sum_keys4<L::kCg, true>(dsa);
+      dv = sum_keys4<L::kCg, true>(dv);
       const int32_t t = ch.start + jt;
       if (rg == 0) {
         store4<T>(static_cast<St*>(p.dv) + t * hd + head_off + col, dv.x, dv.y, dv.z, dv.w);

@@ -237,6 +237,24 @@ __device__ __forceinline__ typename IoTraits<T>::storage nan_value() {
   return from_f32<T>(__int_as_float(0x7fc00000));
 }
 
+// x + x[lane ^ 16] and x + x[lane ^ 32] through the gfx950 lane swaps
+// (v_permlane16_swap / v_permlane32_swap: VALU exchanges between the 16-lane
+// rows, or the 32-lane halves, of two registers; no LDS-crossbar round trip).
+// Swapping a register with itself leaves x[lo] in one result and x[hi] in the
+// other at both lanes of a pair, so both lanes add the same two values and
+// end with the same bits, as x + __shfl_xor(x, 16 or 32) does.
+__device__ __forceinline__ float add_xor16(float x) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
+__device__ __forceinline__ float add_xor32(float x) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
 // Grid-stride NaN fill used when the metadata status word reports an error:
 // outputs become NaN and no state is written (fail closed).
 template <typename T>
