@@ -29,6 +29,10 @@ if not OPS_LIBRARY.exists() or not HIP_LIBRARY.exists():
 
 torch.ops.load_library(str(OPS_LIBRARY))
 ops = torch.ops.flashrwkv_amd
+# The same library is also a Python extension module: direct (pybind11)
+# entry points for the per-token decode chain, which run the same C++
+# functions as the ops above without the dispatcher's boxed call.
+from . import _flashrwkv_amd_ops as direct  # noqa: E402
 
 
 def prepare_recurrent_metadata(query_start_loc, state_indices, total_tokens,
@@ -42,7 +46,7 @@ def recurrent_fp32_from_decay_logits(query_start_loc, state_indices, state, r,
                                      decay_logits, k, v, a, b, output, scale,
                                      decay_bias=None, validated_metadata=None,
                                      max_seqlen=-1):
-    ops.recurrent_fp32_from_decay_logits(
+    direct.recurrent_fp32_from_decay_logits(
         query_start_loc, state_indices, state, r, decay_logits, k, v, a, b,
         output, float(scale), decay_bias, validated_metadata, int(max_seqlen))
 
@@ -51,7 +55,7 @@ def recurrent_fp32_forward_internal(query_start_loc, state_indices, state, r,
                                     decay, k, v, a, b, output, scale, decay_mode,
                                     decay_bias=None, validated_metadata=None,
                                     max_seqlen=-1):
-    ops.recurrent_fp32_forward_internal(
+    direct.recurrent_fp32_forward_internal(
         query_start_loc, state_indices, state, r, decay, k, v, a, b, output,
         float(scale), int(decay_mode), decay_bias, validated_metadata,
         int(max_seqlen))
@@ -137,38 +141,39 @@ def recurrent_fp16_from_decay_logits(query_start_loc, state_indices, elapsed_sta
                                      r, decay_logits, k, v, a, b, output, scale,
                                      decay_bias=None, validated_metadata=None, max_seqlen=-1):
     """Reference infer_recurrent_fp16_forward_varlen.cpp:210-270, 289-301."""
-    ops.recurrent_fp16_from_decay_logits(
+    direct.recurrent_fp16_from_decay_logits(
         query_start_loc, state_indices, elapsed_state_pool, state, r, decay_logits, k, v, a,
         b, output, float(scale), decay_bias, validated_metadata, int(max_seqlen))
 
 
 def recurrent_fp16_advance_i32(elapsed_state, amount):
     """Reference infer_recurrent_fp16_forward_varlen.cpp:129-135."""
-    ops.recurrent_fp16_advance_i32(elapsed_state, int(amount))
+    direct.recurrent_fp16_advance_i32(elapsed_state, int(amount))
 
 
 def recurrent_fp16_advance_i32_varlen(query_start_loc, state_indices, elapsed_state_pool,
                                       total_tokens, validated_metadata=None):
     """Reference infer_recurrent_fp16_forward_varlen.cpp:137-191."""
-    ops.recurrent_fp16_advance_i32_varlen(query_start_loc, state_indices, elapsed_state_pool,
-                                          int(total_tokens), validated_metadata)
+    direct.recurrent_fp16_advance_i32_varlen(query_start_loc, state_indices,
+                                             elapsed_state_pool, int(total_tokens),
+                                             validated_metadata)
 
 
 def recurrent_add_vec_forward_varlen(x, vec):
     """Reference infer_recurrent_fp16_forward_varlen.cpp:193-208."""
-    return ops.recurrent_add_vec_forward_varlen(x, vec)
+    return direct.recurrent_add_vec_forward_varlen(x, vec)
 
 
 def tmix_kk_a_gate_forward_varlen(k, k_k, a0, a12, k_a, head_size=64, batch_size=1,
                                   max_seqlen=1):
     """Reference kk_a_gate/infer_fp16_forward_varlen.cpp:41-85: returns (new_k, neg_kk, kka)."""
-    return ops.tmix_kk_a_gate_forward_varlen(k, k_k, a0, a12, k_a, int(head_size),
-                                             int(batch_size), int(max_seqlen))
+    return direct.tmix_kk_a_gate_forward_varlen(k, k_k, a0, a12, k_a, int(head_size),
+                                                int(batch_size), int(max_seqlen))
 
 
 def tmix_lnx_rkvres_xg_forward_varlen(x, r, k, v, r_k, weight, bias, g, head_size=64,
                                       batch_size=1, max_seqlen=1):
     """Reference lnx_rkvres_xg/infer_fp16_forward_varlen.cpp:40-98."""
-    return ops.tmix_lnx_rkvres_xg_forward_varlen(x, r, k, v, r_k, weight, bias, g,
-                                                 int(head_size), int(batch_size),
-                                                 int(max_seqlen))
+    return direct.tmix_lnx_rkvres_xg_forward_varlen(x, r, k, v, r_k, weight, bias, g,
+                                                    int(head_size), int(batch_size),
+                                                    int(max_seqlen))

@@ -15,6 +15,7 @@ from __future__ import annotations
 import concurrent.futures
 import os
 import subprocess
+import sysconfig
 import sys
 from pathlib import Path
 
@@ -81,12 +82,13 @@ def build_binding() -> Path:
     tmp = OPS.with_suffix(".so.tmp")
     _run([
         os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared",
-        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", "-DFRWKV_PYTHON_MODULE=1",
+        "-DTORCH_EXTENSION_NAME=_flashrwkv_amd_ops", "-I", sysconfig.get_paths()["include"],
         "-I", str(inc), "-I", str(inc / "torch" / "csrc" / "api" / "include"),
         "-I", "/opt/rocm/include", "-I", str(REPO / "include"),
         str(BINDING_SOURCE), "-o", str(tmp),
         "-L", str(PKG), "-lflashrwkv_amd",
-        "-L", str(lib), "-ltorch", "-ltorch_cpu", "-lc10", "-lc10_hip",
+        "-L", str(lib), "-ltorch", "-ltorch_cpu", "-lc10", "-lc10_hip", "-ltorch_python",
         f"-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{lib}",
     ])
     os.replace(tmp, OPS)

@@ -1314,3 +1314,78 @@ TORCH_LIBRARY(rwkv7_clampw_v3, m) {
       "Tensor(e!) da, Tensor(f!) db, int head_size) -> ()",
       &clampw_backward);
 }
+
+#ifdef FRWKV_PYTHON_MODULE
+// Direct Python entry points for the per-token decode chain, in the
+// reference's binding style (a pybind11 module, csrc/registration.cpp:6-8).
+// A call converts its arguments once and runs the same function as the
+// TORCH_LIBRARY op above (same checks, same errors); it skips the
+// dispatcher's boxed path, which costs several microseconds per call at
+// these ops' 10-19 arguments. The ticket arrives as the custom class's
+// Python object and is unwrapped to the same intrusive pointer.
+#include <torch/csrc/jit/python/pybind_utils.h>
+#include <torch/extension.h>
+
+namespace {
+
+std::optional<TicketPtr> ticket_arg(const pybind11::object& obj) {
+  if (obj.is_none()) return std::nullopt;
+  const c10::IValue value =
+      torch::jit::toIValue(obj, c10::getCustomClassType<TicketPtr>());
+  return value.toCustomClass<MetadataTicket>();
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_flashrwkv_amd_ops, m) {
+  namespace py = pybind11;
+  // TORCH_CHECK failures surface as RuntimeError with the check's message,
+  // as they do through the ops (no C++ backtrace).
+  py::register_local_exception_translator([](std::exception_ptr error) {
+    try {
+      if (error) std::rethrow_exception(error);
+    } catch (const c10::Error& e) {
+      PyErr_SetString(PyExc_RuntimeError, e.what_without_backtrace());
+    }
+  });
+  m.def("recurrent_fp32_from_decay_logits",
+        [](Tensor cu, Tensor slots, Tensor state, Tensor r, Tensor x, Tensor k, Tensor v,
+           Tensor a, Tensor b, Tensor out, double scale, std::optional<Tensor> bias,
+           py::object ticket, int64_t max_seqlen) {
+          recurrent_fp32_from_decay_logits(cu, slots, state, r, x, k, v, a, b, out, scale,
+                                           bias, ticket_arg(ticket), max_seqlen);
+        });
+  m.def("recurrent_fp32_forward_internal",
+        [](Tensor cu, Tensor slots, Tensor state, Tensor r, Tensor x, Tensor k, Tensor v,
+           Tensor a, Tensor b, Tensor out, double scale, int64_t decay_mode,
+           std::optional<Tensor> bias, py::object ticket, int64_t max_seqlen) {
+          recurrent_fp32_forward_internal(cu, slots, state, r, x, k, v, a, b, out, scale,
+                                          decay_mode, bias, ticket_arg(ticket), max_seqlen);
+        });
+  m.def("recurrent_fp16_from_decay_logits",
+        [](Tensor cu, Tensor slots, Tensor elapsed, Tensor state, Tensor r, Tensor x, Tensor k,
+           Tensor v, Tensor a, Tensor b, Tensor out, double scale, std::optional<Tensor> bias,
+           py::object ticket, int64_t max_seqlen) {
+          recurrent_fp16_from_decay_logits(cu, slots, elapsed, state, r, x, k, v, a, b, out,
+                                           scale, bias, ticket_arg(ticket), max_seqlen);
+        });
+  m.def("recurrent_fp16_advance_i32", &recurrent_fp16_advance_i32);
+  m.def("recurrent_fp16_advance_i32_varlen",
+        [](Tensor cu, Tensor slots, Tensor elapsed, int64_t total_tokens, py::object ticket) {
+          recurrent_fp16_advance_i32_varlen(cu, slots, elapsed, total_tokens,
+                                            ticket_arg(ticket));
+        });
+  m.def("recurrent_add_vec_forward_varlen", &recurrent_add_vec_forward_varlen);
+  m.def("tmix_kk_a_gate_forward_varlen", &tmix_kk_a_gate_forward_varlen);
+  m.def("tmix_lnx_rkvres_xg_forward_varlen", &tmix_lnx_rkvres_xg_forward_varlen);
+  m.def("recurrent_tmix_fused_forward",
+        [](Tensor cu, Tensor slots, Tensor state, Tensor r, Tensor decay, Tensor k, Tensor v,
+           Tensor a12, Tensor g, Tensor k_k, Tensor a0, Tensor k_a, Tensor r_k,
+           Tensor ln_weight, Tensor ln_bias, double scale, int64_t decay_mode,
+           std::optional<Tensor> bias, py::object ticket) {
+          return recurrent_tmix_fused_forward(cu, slots, state, r, decay, k, v, a12, g, k_k,
+                                              a0, k_a, r_k, ln_weight, ln_bias, scale,
+                                              decay_mode, bias, ticket_arg(ticket));
+        });
+}
+#endif  // FRWKV_PYTHON_MODULE

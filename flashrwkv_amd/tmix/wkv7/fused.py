@@ -56,7 +56,7 @@ def _fused(r, decay, k, v, a12, g, k_k, a0, k_a, r_k, ln_weight, ln_bias, *, sta
         else prepare_recurrent_metadata(cu_seqlens, state_indices, total_tokens=r.shape[0],
                                         state_pool_size=state_pool.shape[0])
     )
-    return _extension().ops.recurrent_tmix_fused_forward(
+    return _extension().direct.recurrent_tmix_fused_forward(
         cu_seqlens, state_indices, state_pool, *packed, k_k, a0, k_a, r_k, ln_weight,
         ln_bias, float(scale), int(decay_mode), decay_bias, ticket)
 

@@ -114,3 +114,36 @@ def test_fp16_state_entry_points_reject_bad_arguments_without_a_gpu():
     fake = ctypes.c_void_p(0x1000)
     assert lib.frwkv_add_vec(3, 7, fake, fake, fake, null) == 1
     assert b"even C" in lib.frwkv_last_error()
+
+
+DIRECT_ENTRY_POINTS = (
+    "recurrent_fp32_from_decay_logits", "recurrent_fp32_forward_internal",
+    "recurrent_fp16_from_decay_logits", "recurrent_fp16_advance_i32",
+    "recurrent_fp16_advance_i32_varlen", "recurrent_add_vec_forward_varlen",
+    "tmix_kk_a_gate_forward_varlen", "tmix_lnx_rkvres_xg_forward_varlen",
+    "recurrent_tmix_fused_forward",
+)
+
+
+def test_direct_entry_points_match_the_ops_without_a_gpu():
+    """The pybind11 entry points of the decode chain exist, and an argument
+    error reads exactly as it does through the TORCH_LIBRARY op (no backtrace),
+    raised before anything reaches a GPU (CPU tensors are rejected first)."""
+    from flashrwkv_amd import _C
+
+    for name in DIRECT_ENTRY_POINTS:
+        assert callable(getattr(_C.direct, name)), name
+        assert hasattr(_C.ops, name), name
+    tok = [torch.zeros(1, 1, 64, dtype=torch.bfloat16) for _ in range(7)]
+    args = (torch.tensor([0, 1], dtype=torch.int32), torch.zeros(1, dtype=torch.int32),
+            torch.zeros(1, 1, 64, 64), *tok, 1.0, None, None, -1)
+    with pytest.raises(RuntimeError) as via_op:
+        _C.ops.recurrent_fp32_from_decay_logits(*args)
+    with pytest.raises(RuntimeError) as via_direct:
+        _C.direct.recurrent_fp32_from_decay_logits(*args)
+    assert str(via_direct.value) == str(via_op.value)
+    assert "must be CUDA" in str(via_direct.value)
+    assert "Exception raised from" not in str(via_direct.value)
+    # The public facade goes through the direct entry point.
+    with pytest.raises(RuntimeError, match="must be CUDA"):
+        _C.recurrent_fp32_from_decay_logits(*args[:10], 1.0)
