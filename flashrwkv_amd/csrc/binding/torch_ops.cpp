@@ -1330,8 +1330,14 @@ namespace {
 
 std::optional<TicketPtr> ticket_arg(const pybind11::object& obj) {
   if (obj.is_none()) return std::nullopt;
-  const c10::IValue value =
-      torch::jit::toIValue(obj, c10::getCustomClassType<TicketPtr>());
+  c10::IValue value;
+  try {
+    value = torch::jit::toIValue(obj, c10::getCustomClassType<TicketPtr>());
+  } catch (const std::exception&) {
+    TORCH_CHECK(false, "validated_metadata must be None or a ticket returned by "
+                "prepare_recurrent_metadata, got ",
+                pybind11::str(pybind11::type::of(obj).attr("__name__")).cast<std::string>());
+  }
   return value.toCustomClass<MetadataTicket>();
 }
 

@@ -144,6 +144,9 @@ def test_direct_entry_points_match_the_ops_without_a_gpu():
     assert str(via_direct.value) == str(via_op.value)
     assert "must be CUDA" in str(via_direct.value)
     assert "Exception raised from" not in str(via_direct.value)
+    # A metadata argument that is not a ticket is named in the error.
+    with pytest.raises(RuntimeError, match="validated_metadata must be None or a ticket"):
+        _C.direct.recurrent_fp32_from_decay_logits(*args[:12], "not a ticket", -1)
     # The public facade goes through the direct entry point.
     with pytest.raises(RuntimeError, match="must be CUDA"):
         _C.recurrent_fp32_from_decay_logits(*args[:10], 1.0)
