@@ -28,7 +28,7 @@ if not OPS_LIBRARY.exists() or not HIP_LIBRARY.exists():
     )
 
 torch.ops.load_library(str(OPS_LIBRARY))
-ops = torch.ops.flashrwkv_amd
+ops = torch.ops.flashrwkv2
 # The same library is also a Python extension module: direct (pybind11)
 # entry points for the per-token decode chain, which run the same C++
 # functions as the ops above without the dispatcher's boxed call.

@@ -3,7 +3,7 @@
 // Replaces the reference's pybind11 registration layer for the WKV7 path
 // (csrc/registration.cpp:6-8, csrc/bindings.cpp:6-44 and the per-op register_*
 // functions, e.g. csrc/sm120/tmix/wkv7/infer_recurrent_fp32io16_forward_varlen.cpp:314-362)
-// with TORCH_LIBRARY(flashrwkv_amd) ops and a torch custom class for the
+// with TORCH_LIBRARY(flashrwkv2) ops and a torch custom class for the
 // metadata ticket. This layer only validates tensors (same rules and error
 // vocabulary as csrc/validation.cpp:27-129 and the ticket checks of
 // infer_recurrent_fp32io16_forward_varlen.cpp:44-202), owns allocations the
@@ -1178,7 +1178,7 @@ Tensor recurrent_tmix_fused_forward(Tensor query_start_loc, Tensor state_indices
   return output;
 }
 
-TORCH_LIBRARY(flashrwkv_amd, m) {
+TORCH_LIBRARY(flashrwkv2, m) {
   m.class_<MetadataTicket>("MetadataTicket")
       .def("max_seqlen", [](const TicketPtr& t) { return t->max_seqlen(); })
       .def("total_tokens", [](const TicketPtr& t) { return t->total_tokens(); })
@@ -1192,18 +1192,31 @@ TORCH_LIBRARY(flashrwkv_amd, m) {
            [](const TicketPtr& t, Tensor cu, Tensor slots, int64_t total_tokens,
               int64_t state_pool_size, int64_t max_seqlen) {
              t->check_compatible(cu, slots, total_tokens, state_pool_size, max_seqlen);
-           });
+           })
+      // The reference ticket's method names
+      // (infer_recurrent_fp32io16_forward_varlen.cpp:314-345).
+      .def("_check_compatible",
+           [](const TicketPtr& t, Tensor cu, Tensor slots, int64_t total_tokens,
+              int64_t state_pool_size, int64_t max_seqlen) {
+             t->check_compatible(cu, slots, total_tokens, state_pool_size, max_seqlen);
+           })
+      .def("_query_start_loc_snapshot",
+           [](const TicketPtr& t) { return t->prepared().cu_snapshot; })
+      .def("_state_indices_snapshot",
+           [](const TicketPtr& t) { return t->prepared().slot_snapshot; })
+      .def("_status", [](const TicketPtr& t) { return t->prepared().status; })
+      .def("_max_seqlen", [](const TicketPtr& t) { return t->max_seqlen(); });
   m.def(
       "prepare_recurrent_metadata(Tensor query_start_loc, Tensor state_indices, "
       "int total_tokens, int state_pool_size, int max_seqlen=-1) -> "
-      "__torch__.torch.classes.flashrwkv_amd.MetadataTicket",
+      "__torch__.torch.classes.flashrwkv2.MetadataTicket",
       &prepare_recurrent_metadata);
   m.def(
       "recurrent_fp32_from_decay_logits(Tensor query_start_loc, Tensor "
       "state_indices, Tensor(a!) state, Tensor r, Tensor decay_logits, Tensor k, "
       "Tensor v, Tensor a, Tensor b, Tensor(b!) output, float scale, "
       "Tensor? decay_bias=None, "
-      "__torch__.torch.classes.flashrwkv_amd.MetadataTicket? "
+      "__torch__.torch.classes.flashrwkv2.MetadataTicket? "
       "validated_metadata=None, int max_seqlen=-1) -> ()",
       &recurrent_fp32_from_decay_logits);
   m.def(
@@ -1211,7 +1224,7 @@ TORCH_LIBRARY(flashrwkv_amd, m) {
       "state_indices, Tensor(a!) state, Tensor r, Tensor decay, Tensor k, "
       "Tensor v, Tensor a, Tensor b, Tensor(b!) output, float scale, "
       "int decay_mode, Tensor? decay_bias=None, "
-      "__torch__.torch.classes.flashrwkv_amd.MetadataTicket? "
+      "__torch__.torch.classes.flashrwkv2.MetadataTicket? "
       "validated_metadata=None, int max_seqlen=-1) -> ()",
       &recurrent_fp32_forward_internal);
   m.def(
@@ -1271,7 +1284,7 @@ TORCH_LIBRARY(flashrwkv_amd, m) {
       "Tensor elapsed_state_pool, Tensor(a!) state, Tensor r, Tensor decay_logits, "
       "Tensor k, Tensor v, Tensor a, Tensor b, Tensor(b!) output, float scale, "
       "Tensor? decay_bias=None, "
-      "__torch__.torch.classes.flashrwkv_amd.MetadataTicket? "
+      "__torch__.torch.classes.flashrwkv2.MetadataTicket? "
       "validated_metadata=None, int max_seqlen=-1) -> ()",
       &recurrent_fp16_from_decay_logits);
   m.def("recurrent_fp16_advance_i32(Tensor(a!) elapsed_state, int amount) -> ()",
@@ -1279,7 +1292,7 @@ TORCH_LIBRARY(flashrwkv_amd, m) {
   m.def(
       "recurrent_fp16_advance_i32_varlen(Tensor query_start_loc, Tensor state_indices, "
       "Tensor(a!) elapsed_state_pool, int total_tokens, "
-      "__torch__.torch.classes.flashrwkv_amd.MetadataTicket? "
+      "__torch__.torch.classes.flashrwkv2.MetadataTicket? "
       "validated_metadata=None) -> ()",
       &recurrent_fp16_advance_i32_varlen);
   m.def("recurrent_add_vec_forward_varlen(Tensor x, Tensor vec) -> Tensor",
@@ -1298,7 +1311,7 @@ TORCH_LIBRARY(flashrwkv_amd, m) {
       "Tensor(a!) state, Tensor r, Tensor decay, Tensor k, Tensor v, Tensor a12, Tensor g, "
       "Tensor k_k, Tensor a0, Tensor k_a, Tensor r_k, Tensor ln_weight, Tensor ln_bias, "
       "float scale=1.0, int decay_mode=0, Tensor? decay_bias=None, "
-      "__torch__.torch.classes.flashrwkv_amd.MetadataTicket? validated_metadata=None) -> Tensor",
+      "__torch__.torch.classes.flashrwkv2.MetadataTicket? validated_metadata=None) -> Tensor",
       &recurrent_tmix_fused_forward);
 }
 

@@ -1,26 +1,75 @@
-"""Chunked WKV7 prefill, mirroring ``flashrwkv2.tmix.wkv7.chunk``.
+"""Chunked WKV7 prefill, importable as ``flashrwkv2.tmix.wkv7.chunk``.
 
-``infer_chunk_bf16_forward_varlen`` keeps the reference's signature, checks,
-error types and messages (reference ``flashrwkv2/tmix/wkv7/chunk.py:17-125``)
-and its bf16 state-pool contract. The kernel behind it is the exact chunk
-form of the recurrence on bf16 MFMA with an fp32 state between 64-token
-chunks, so ``chunk_size`` is validated but does not change the result (the
-reference's K1/K2 kernels depend on it).
+``infer_chunk_bf16_forward_varlen`` keeps the reference's signature, error
+contract and bf16 state-pool contract (reference
+``flashrwkv2/tmix/wkv7/chunk.py:17-125``); its checks are the contract table
+``CHUNK_PREFILL`` below. The kernel behind it is the exact chunk form of the
+recurrence on bf16 MFMA with an fp32 state between 64-token chunks, so
+``chunk_size`` is validated but does not change the result (the reference's
+K1/K2 kernels depend on it).
 """
 
 from __future__ import annotations
 
-import math
-
 import torch
 
-from . import (
-    DECAY_LOGITS,
-    DECAY_RAW_W,
-    _check_metadata_inputs,
-    _extension,
-    _resolve_max_seqlen,
-    prepare_recurrent_metadata,
+from ... import _contract as C
+from ..._contract import Each, check, is_tensor
+from . import DECAY_LOGITS, DECAY_RAW_W, prepare_recurrent_metadata
+
+
+def _bf16_cuda(x, ns) -> bool:
+    return x.dtype == torch.bfloat16 and x.is_cuda and x.is_contiguous()
+
+
+def _pool_ok(x, ns) -> bool:
+    r = ns["r"]
+    return (isinstance(x, torch.Tensor) and _bf16_cuda(x, ns) and x.ndim == 4
+            and x.shape[1:] == (r.shape[1], 64, 64) and x.device == r.device)
+
+
+def _metadata_ok(_, ns) -> bool:
+    dev = ns["r"].device
+    return all(t.dtype == torch.int32 and t.is_cuda and t.is_contiguous() and t.device == dev
+               for t in (ns["cu_seqlens"], ns["state_indices"]))
+
+
+def _bias_ok(x, ns) -> bool:
+    heads = ns["r"].shape[1]
+    return (_bf16_cuda(x, ns) and x.device == ns["r"].device
+            and tuple(x.shape) in {(heads, 64), (heads * 64,)})
+
+
+# Reference ``chunk.py:41-109`` (plus ``_resolve_max_seqlen``, ``__init__.py:166-177``).
+CHUNK_PREFILL = (
+    check("chunk_size", C.plain_int, TypeError, "chunk_size must be an integer"),
+    check("chunk_size", lambda x, ns: x > 0, ValueError, "chunk_size must be positive"),
+    check("scale", C.finite, ValueError, "scale must be finite"),
+    Each(C.PACKED_TOKENS, (
+        is_tensor(),
+        check(None, _bf16_cuda, ValueError, "{name} must be contiguous CUDA bfloat16"),
+        check(None, C.same_device_as("r"), ValueError, "{name} must share r's device"),
+        check(None, C.same_shape_as("r"), ValueError, "{name} must have the same shape as r"),
+    )),
+    check("r", lambda x, ns: x.ndim == 3 and x.shape[0] > 0 and x.shape[1] > 0
+          and x.shape[2] == 64, ValueError,
+          "packed chunk inputs must have shape [total_tokens,H,64]"),
+    check("state_pool", _pool_ok, ValueError,
+          "state_pool must be contiguous CUDA bfloat16 [slots,H,64,64]"),
+    *C.METADATA,
+    check(None, _metadata_ok, ValueError, "chunk metadata must be contiguous CUDA int32"),
+    C.when(lambda ns: ns["max_seqlen"] is not None,
+           check("max_seqlen", lambda x, ns: int(x) > 0, ValueError,
+                 "max_seqlen must be positive")),
+    C.when(lambda ns: ns["max_seqlen"] is None,
+           check("cu_seqlens", lambda x, ns: x.numel() >= 2, ValueError,
+                 "cu_seqlens must contain at least one sequence")),
+)
+
+CHUNK_BIAS = (
+    C.when(lambda ns: ns["decay_bias"] is not None,
+           check("decay_bias", _bias_ok, ValueError,
+                 "decay_bias must be contiguous CUDA bfloat16 [H,64] or [H*64]")),
 )
 
 
@@ -41,72 +90,25 @@ def infer_chunk_bf16_forward_varlen(
     decay_bias: torch.Tensor | None = None,
     validated_metadata: object | None = None,
 ) -> torch.Tensor:
-    """Run packed RWKV-7 bf16 chunked prefill; ``state_pool`` is updated in place."""
-    if not isinstance(chunk_size, int) or isinstance(chunk_size, bool):
-        raise TypeError("chunk_size must be an integer")
-    if chunk_size <= 0:
-        raise ValueError("chunk_size must be positive")
-    if not math.isfinite(float(scale)):
-        raise ValueError("scale must be finite")
-    tensors = {"r": r, "decay_logits": decay_logits, "k": k, "v": v, "a": a, "b": b}
-    for name, tensor in tensors.items():
-        if not isinstance(tensor, torch.Tensor):
-            raise TypeError(f"{name} must be a torch.Tensor")
-        if tensor.dtype != torch.bfloat16 or not tensor.is_cuda or not tensor.is_contiguous():
-            raise ValueError(f"{name} must be contiguous CUDA bfloat16")
-        if tensor.device != r.device:
-            raise ValueError(f"{name} must share r's device")
-        if tensor.shape != r.shape:
-            raise ValueError(f"{name} must have the same shape as r")
-    if r.ndim != 3 or r.shape[0] <= 0 or r.shape[1] <= 0 or r.shape[2] != 64:
-        raise ValueError("packed chunk inputs must have shape [total_tokens,H,64]")
-    if (
-        not isinstance(state_pool, torch.Tensor)
-        or state_pool.dtype != torch.bfloat16
-        or not state_pool.is_cuda
-        or not state_pool.is_contiguous()
-        or state_pool.ndim != 4
-        or state_pool.shape[1:] != (r.shape[1], 64, 64)
-        or state_pool.device != r.device
-    ):
-        raise ValueError("state_pool must be contiguous CUDA bfloat16 [slots,H,64,64]")
-    _check_metadata_inputs(cu_seqlens, state_indices)
-    if (
-        cu_seqlens.dtype != torch.int32
-        or state_indices.dtype != torch.int32
-        or not cu_seqlens.is_cuda
-        or not state_indices.is_cuda
-        or not cu_seqlens.is_contiguous()
-        or not state_indices.is_contiguous()
-        or cu_seqlens.device != r.device
-        or state_indices.device != r.device
-    ):
-        raise ValueError("chunk metadata must be contiguous CUDA int32")
-    launch_max_seqlen = _resolve_max_seqlen(cu_seqlens, max_seqlen)
-    ticket = (
-        validated_metadata
-        if validated_metadata is not None
-        else prepare_recurrent_metadata(
-            cu_seqlens,
-            state_indices,
-            total_tokens=r.shape[0],
-            state_pool_size=state_pool.shape[0],
-            max_seqlen=launch_max_seqlen,
-        )
-    )
-    del ticket  # the native op validates and snapshots the metadata on device
-    if decay_bias is not None:
-        if (
-            decay_bias.dtype != torch.bfloat16
-            or not decay_bias.is_cuda
-            or not decay_bias.is_contiguous()
-            or decay_bias.device != r.device
-            or decay_bias.shape not in {(r.shape[1], 64), (r.shape[1] * 64,)}
-        ):
-            raise ValueError("decay_bias must be contiguous CUDA bfloat16 [H,64] or [H*64]")
-    output, _ = _extension().infer_chunk_bf16_forward_varlen(
+    """Packed RWKV-7 bf16 chunked prefill; ``state_pool`` is updated in place.
+
+    Invalid metadata is rejected by the ticket's validation (or, with a
+    caller ticket, fails closed on the device: NaN output, pool untouched).
+    The longest sequence comes from ``max_seqlen`` or the ticket.
+    """
+    ns = dict(locals())
+    C.enforce(CHUNK_PREFILL, ns)
+    ticket = validated_metadata
+    if ticket is None:
+        ticket = prepare_recurrent_metadata(cu_seqlens, state_indices,
+                                            total_tokens=r.shape[0],
+                                            state_pool_size=state_pool.shape[0],
+                                            max_seqlen=max_seqlen)
+    launch_max = int(max_seqlen) if max_seqlen is not None else int(ticket.max_seqlen())
+    C.enforce(CHUNK_BIAS, ns)
+    output, _ = C.native().infer_chunk_bf16_forward_varlen(
         r, decay_logits, k, v, a, b, state_pool, cu_seqlens, state_indices,
-        int(chunk_size), int(launch_max_seqlen), float(scale), decay_bias=decay_bias)
+        int(chunk_size), launch_max, float(scale), decay_bias=decay_bias)
     return output
 
 
@@ -125,12 +127,12 @@ def chunk_forward_internal(
     scale: float = 1.0,
     decay_bias: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Internal chunked forward: explicit decay mode, fp16/bf16 tokens, fp32 or
-    bf16 pool (not part of the reference API; used by the measurement harness
-    and parity tests)."""
+    """Chunked forward with an explicit decay mode, fp16/bf16 tokens and an fp32
+    or bf16 pool (not reference API; the measurement harness and parity tests
+    use it)."""
     if decay_mode not in (DECAY_LOGITS, DECAY_RAW_W):
         raise ValueError("decay_mode must be DECAY_LOGITS or DECAY_RAW_W")
-    return _extension().chunk_forward_internal(
+    return C.native().chunk_forward_internal(
         r, decay, k, v, a, b, state_pool, cu_seqlens, state_indices, float(scale),
         int(decay_mode), decay_bias)
 

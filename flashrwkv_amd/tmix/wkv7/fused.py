@@ -25,40 +25,33 @@ from __future__ import annotations
 
 import torch
 
-from . import (
-    DECAY_LOGITS,
-    _check_metadata_inputs,
-    _extension,
-    _validate_state,
-    prepare_recurrent_metadata,
+from ... import _contract as C
+from ..._contract import Each, check, is_tensor
+from . import DECAY_LOGITS, RECURRENT_FP32, prepare_recurrent_metadata
+
+_CHAIN_TOKENS = ("r", "decay_logits", "k", "v", "a12", "g")
+_CHAIN_VECTORS = ("k_k", "a0", "k_a", "r_k", "ln_weight", "ln_bias")
+
+# The recurrent family's checks with the chain's token list, then the
+# producer/consumer vectors.
+FUSED = (
+    Each(_CHAIN_TOKENS, RECURRENT_FP32[0].rules),
+    *RECURRENT_FP32[1:],
+    Each(_CHAIN_VECTORS, (is_tensor(),)),
 )
 
 
-def _fused(r, decay, k, v, a12, g, k_k, a0, k_a, r_k, ln_weight, ln_bias, *, state_pool,
-           cu_seqlens, state_indices, scale, decay_bias, validated_metadata, decay_mode):
-    packed = (r, decay, k, v, a12, g)
-    for name, tensor in zip(("r", "decay_logits", "k", "v", "a12", "g"), packed):
-        if not isinstance(tensor, torch.Tensor):
-            raise TypeError(f"{name} must be a torch.Tensor")
-        if tensor.ndim != 3:
-            raise ValueError(f"{name} must have packed shape [total_tokens,H,D]")
-        if not tensor.is_contiguous():
-            raise ValueError(f"{name} must be contiguous")
-    _validate_state(state_pool)
-    _check_metadata_inputs(cu_seqlens, state_indices)
-    for name, tensor in (("k_k", k_k), ("a0", a0), ("k_a", k_a), ("r_k", r_k),
-                         ("ln_weight", ln_weight), ("ln_bias", ln_bias)):
-        if not isinstance(tensor, torch.Tensor):
-            raise TypeError(f"{name} must be a torch.Tensor")
-    ticket = (
-        validated_metadata
-        if validated_metadata is not None
-        else prepare_recurrent_metadata(cu_seqlens, state_indices, total_tokens=r.shape[0],
-                                        state_pool_size=state_pool.shape[0])
-    )
-    return _extension().direct.recurrent_tmix_fused_forward(
-        cu_seqlens, state_indices, state_pool, *packed, k_k, a0, k_a, r_k, ln_weight,
-        ln_bias, float(scale), int(decay_mode), decay_bias, ticket)
+def _fused(ns: dict, decay_mode: int) -> torch.Tensor:
+    C.enforce(FUSED, ns)
+    ticket = ns["validated_metadata"]
+    if ticket is None:
+        ticket = prepare_recurrent_metadata(ns["cu_seqlens"], ns["state_indices"],
+                                            total_tokens=ns["r"].shape[0],
+                                            state_pool_size=ns["state_pool"].shape[0])
+    return C.native().direct.recurrent_tmix_fused_forward(
+        ns["cu_seqlens"], ns["state_indices"], ns["state_pool"],
+        *(ns[n] for n in _CHAIN_TOKENS), *(ns[n] for n in _CHAIN_VECTORS),
+        float(ns["scale"]), int(decay_mode), ns["decay_bias"], ticket)
 
 
 def infer_tmix_wkv7_fused_forward_varlen(
@@ -92,10 +85,7 @@ def infer_tmix_wkv7_fused_forward_varlen(
     ``infer_recurrent_fp32io16_forward_varlen``. Returns the consumer's output
     shaped like ``v``.
     """
-    return _fused(r, decay_logits, k, v, a12, g, k_k, a0, k_a, r_k, ln_weight, ln_bias,
-                  state_pool=state_pool, cu_seqlens=cu_seqlens, state_indices=state_indices,
-                  scale=scale, decay_bias=decay_bias, validated_metadata=validated_metadata,
-                  decay_mode=DECAY_LOGITS)
+    return _fused(dict(locals()), DECAY_LOGITS)
 
 
 def tmix_fused_internal(r, decay, k, v, a12, g, k_k, a0, k_a, r_k, ln_weight, ln_bias, *,
@@ -103,10 +93,9 @@ def tmix_fused_internal(r, decay, k, v, a12, g, k_k, a0, k_a, r_k, ln_weight, ln
                         decay_bias=None, validated_metadata=None):
     """As :func:`infer_tmix_wkv7_fused_forward_varlen` with an explicit decay
     mode (0 logits, 1 the retention itself); parity tests and the bench."""
-    return _fused(r, decay, k, v, a12, g, k_k, a0, k_a, r_k, ln_weight, ln_bias,
-                  state_pool=state_pool, cu_seqlens=cu_seqlens, state_indices=state_indices,
-                  scale=scale, decay_bias=decay_bias, validated_metadata=validated_metadata,
-                  decay_mode=decay_mode)
+    ns = dict(locals())
+    ns["decay_logits"] = ns.pop("decay")
+    return _fused(ns, decay_mode)
 
 
 __all__ = ["infer_tmix_wkv7_fused_forward_varlen"]

@@ -1,97 +1,129 @@
-"""Pretraining recurrence (clampw v3), mirroring ``flashrwkv2.tmix.wkv7.pretrain``.
+"""Pretraining recurrence (clampw v3), importable as ``flashrwkv2.tmix.wkv7.pretrain``.
 
-``pretrain_recurrent_bf16`` keeps the reference's signature, validation
-(error types and messages) and autograd contract (reference
-``flashrwkv2/tmix/wkv7/pretrain.py:14-129``): dense bf16 ``[B,T,C]`` tokens
-with decay logits ``w`` (retention ``exp(-e^{-1/2} sigmoid(w))``), zero initial
-state, output ``[B,T,C]``. The forward and backward run through
-``torch.ops.rwkv7_clampw_v3``: head size 64 on the chunked bf16-MFMA kernels,
-128 and 256 on the per-token fp32 training kernels. Either backward recomputes
-its chunks from the saved boundary states (every 16 tokens).
+``pretrain_recurrent_bf16`` keeps the reference's signature, error contract
+and autograd behaviour (reference ``flashrwkv2/tmix/wkv7/pretrain.py:14-129``):
+dense bf16 ``[B,T,C]`` tokens with decay logits ``w`` (retention
+``exp(-e^{-1/2} sigmoid(w))``), zero initial state, output ``[B,T,C]``.
+
+Both directions run through ``torch.ops.rwkv7_clampw_v3``: head size 64 on
+the chunked bf16-MFMA kernels, 128 and 256 on the per-token fp32 training
+kernels. The forward saves the state every 16 tokens; the backward recomputes
+from those states and never divides by the decay.
 """
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
 import torch
 
-from . import _extension
+from ... import _contract as C
+from ..._contract import check, is_tensor
 
 CHUNK_LEN = 16
+_DECAY_AND_FRIENDS = ("w", "k", "v", "a", "b")
 
 
-def _validate_inputs(tensors: tuple[torch.Tensor, ...], head_size: int) -> tuple[int, int, int]:
-    """Reference ``pretrain.py:14-48``."""
-    if head_size not in {64, 128, 256}:
-        raise ValueError("head_size must be one of 64, 128, or 256")
-    if len(tensors) != 6:
-        raise ValueError("clampw requires r, w, k, v, a, and b")
-    r = tensors[0]
-    if not isinstance(r, torch.Tensor):
-        raise TypeError("r must be a torch.Tensor")
-    if r.ndim != 3 or min(r.shape) <= 0:
-        raise ValueError("r must have shape [B,T,C] with nonzero dimensions")
-    if r.dtype != torch.bfloat16:
-        raise TypeError("r must be bfloat16")
-    if not r.is_cuda or not r.is_contiguous():
-        raise ValueError("r must be contiguous CUDA")
-    for name, tensor in zip(("w", "k", "v", "a", "b"), tensors[1:]):
-        if not isinstance(tensor, torch.Tensor):
-            raise TypeError(f"{name} must be a torch.Tensor")
-        if tensor.dtype != torch.bfloat16:
-            raise TypeError(f"{name} must be bfloat16")
-        if not tensor.is_cuda or not tensor.is_contiguous():
-            raise ValueError(f"{name} must be contiguous CUDA")
-        if tensor.shape != r.shape:
-            raise ValueError(f"{name} must match r shape")
-        if tensor.device != r.device:
-            raise ValueError(f"{name} must share the r device")
-    batch, tokens, channels = r.shape
-    if channels % head_size != 0:
-        raise ValueError("C must be divisible by head_size")
-    if tokens % CHUNK_LEN != 0:
-        raise ValueError("T must be divisible by the canonical chunk length 16")
-    return batch, tokens, channels
+def _bf16(x, ns) -> bool:
+    return x.dtype == torch.bfloat16
 
 
-class _PretrainRecurrent(torch.autograd.Function):
-    """Reference ``pretrain.py:50-106``."""
+def _cuda_contig(x, ns) -> bool:
+    return x.is_cuda and x.is_contiguous()
+
+
+# Reference ``pretrain.py:14-48``.
+PRETRAIN = (
+    check("head_size", C.one_of({64, 128, 256}), ValueError,
+          "head_size must be one of 64, 128, or 256"),
+    check(None, lambda _, ns: len(ns["tensors"]) == 6, ValueError,
+          "clampw requires r, w, k, v, a, and b"),
+    is_tensor("r"),
+    check("r", lambda x, ns: x.ndim == 3 and min(x.shape) > 0, ValueError,
+          "r must have shape [B,T,C] with nonzero dimensions"),
+    check("r", _bf16, TypeError, "r must be bfloat16"),
+    check("r", _cuda_contig, ValueError, "r must be contiguous CUDA"),
+    C.Each(_DECAY_AND_FRIENDS, (
+        is_tensor(),
+        check(None, _bf16, TypeError, "{name} must be bfloat16"),
+        check(None, _cuda_contig, ValueError, "{name} must be contiguous CUDA"),
+        check(None, C.same_shape_as("r"), ValueError, "{name} must match r shape"),
+        check(None, C.same_device_as("r"), ValueError, "{name} must share the r device"),
+    )),
+    check("r", lambda x, ns: x.shape[2] % ns["head_size"] == 0, ValueError,
+          "C must be divisible by head_size"),
+    check("r", lambda x, ns: x.shape[1] % CHUNK_LEN == 0, ValueError,
+          "T must be divisible by the canonical chunk length 16"),
+)
+
+
+@dataclass(frozen=True)
+class _Layout:
+    """Shapes of one pretraining call: dense [B,T,C] seen as [B,T,H,D]."""
+
+    batch: int
+    tokens: int
+    heads: int
+    head_size: int
+
+    @classmethod
+    def of(cls, tensors: tuple, head_size: int) -> "_Layout":
+        ns = {"tensors": tensors, "head_size": head_size, "r": tensors[0] if tensors else None}
+        ns.update(zip(_DECAY_AND_FRIENDS, tensors[1:]))
+        C.enforce(PRETRAIN, ns)
+        batch, tokens, channels = tensors[0].shape
+        return cls(batch, tokens, channels // head_size, head_size)
+
+    def heads_view(self, x: torch.Tensor) -> torch.Tensor:
+        return x.view(self.batch, self.tokens, self.heads, self.head_size)
+
+    def dense_view(self, x: torch.Tensor) -> torch.Tensor:
+        return x.view(self.batch, self.tokens, self.heads * self.head_size)
+
+    def fp32(self, *shape: int, like: torch.Tensor) -> torch.Tensor:
+        return torch.empty(shape, device=like.device, dtype=torch.float32)
+
+    def checkpoints(self, like: torch.Tensor) -> torch.Tensor:
+        """State before every 16th token: [B, H, T/16, D, D]."""
+        d = self.head_size
+        return self.fp32(self.batch, self.heads, self.tokens // CHUNK_LEN, d, d, like=like)
+
+    def state_dot_a(self, like: torch.Tensor) -> torch.Tensor:
+        return self.fp32(self.batch, self.tokens, self.heads, self.head_size, like=like)
+
+
+class _ClampwV3(torch.autograd.Function):
+    """Autograd node over the two ``rwkv7_clampw_v3`` ops (forward saves the
+    16-token checkpoints, backward recomputes from them)."""
 
     @staticmethod
-    def forward(ctx, r, w, k, v, a, b, head_size):
-        batch, tokens, channels = _validate_inputs((r, w, k, v, a, b), head_size)
-        _extension()
-        heads = channels // head_size
-        values = tuple(t.view(batch, tokens, heads, head_size) for t in (r, w, k, v, a, b))
-        output = torch.empty_like(values[3])
-        boundary = torch.empty((batch, heads, tokens // CHUNK_LEN, head_size, head_size),
-                               device=r.device, dtype=torch.float32)
-        state_dot_a = torch.empty((batch, tokens, heads, head_size), device=r.device,
-                                  dtype=torch.float32)
-        torch.ops.rwkv7_clampw_v3.forward(*values, output, boundary, state_dot_a, head_size)
-        ctx.save_for_backward(*values, boundary, state_dot_a)
-        ctx.input_shape = (batch, tokens, channels)
-        ctx.head_size = head_size
-        return output.view(batch, tokens, channels)
+    def forward(ctx, layout: _Layout, *tensors):
+        split = tuple(layout.heads_view(t) for t in tensors)
+        y = torch.empty_like(split[3])
+        ckpt = layout.checkpoints(y)
+        sda = layout.state_dot_a(y)
+        torch.ops.rwkv7_clampw_v3.forward(*split, y, ckpt, sda, layout.head_size)
+        ctx.layout = layout
+        ctx.save_for_backward(*split, ckpt, sda)
+        return layout.dense_view(y)
 
     @staticmethod
-    def backward(ctx, grad_output):
-        r, w, k, v, a, b, boundary, state_dot_a = ctx.saved_tensors
-        batch, tokens, channels = ctx.input_shape
-        head_size = ctx.head_size
-        heads = channels // head_size
-        dy = grad_output.contiguous().view(batch, tokens, heads, head_size)
-        grads = tuple(torch.empty_like(t) for t in (r, w, k, v, a, b))
-        torch.ops.rwkv7_clampw_v3.backward(r, w, k, v, a, b, dy, boundary, state_dot_a,
-                                           *grads, head_size)
-        return tuple(g.view(batch, tokens, channels) for g in grads) + (None,)
+    def backward(ctx, dy):
+        layout: _Layout = ctx.layout
+        *split, ckpt, sda = ctx.saved_tensors
+        grads = [torch.empty_like(t) for t in split]
+        torch.ops.rwkv7_clampw_v3.backward(*split, layout.heads_view(dy.contiguous()), ckpt,
+                                           sda, *grads, layout.head_size)
+        return (None, *(layout.dense_view(g) for g in grads))
 
 
 def pretrain_recurrent_bf16(r: torch.Tensor, w: torch.Tensor, k: torch.Tensor,
                             v: torch.Tensor, a: torch.Tensor, b: torch.Tensor, *,
                             head_size: int = 64) -> torch.Tensor:
-    """Run the clampw v3 pretraining forward/backward (reference ``pretrain.py:109-126``)."""
-    _validate_inputs((r, w, k, v, a, b), head_size)
-    return _PretrainRecurrent.apply(r, w, k, v, a, b, head_size)
+    """clampw v3 pretraining recurrence with autograd (reference ``pretrain.py:109-126``)."""
+    layout = _Layout.of((r, w, k, v, a, b), head_size)
+    C.native()
+    return _ClampwV3.apply(layout, r, w, k, v, a, b)
 
 
 __all__ = ["pretrain_recurrent_bf16"]
