@@ -138,15 +138,8 @@ struct ChunkBwdParams {
   int32_t dense_t;
 };
 
-// The kernel's argument block through an opaque kernarg pointer. Fields read
-// through it are fetched with scalar loads at each use; read through the
-// by-value argument, the compiler hoists every pointer and descriptor out of
-// the piece loop and keeps them in SGPRs, which then spill.
 __device__ __forceinline__ const __attribute__((address_space(4))) ChunkBwdParams& args() {
-  auto ptr = (const __attribute__((address_space(4))) ChunkBwdParams*)(
-      __builtin_amdgcn_kernarg_segment_ptr());
-  asm volatile("" : "+s"(ptr));
-  return *ptr;
+  return kernel_args<ChunkBwdParams>();
 }
 
 // Raw token rows of one piece in the token layout (16 bytes per tensor).
@@ -160,16 +153,6 @@ struct Piece {
   int64_t ckpt;      // float index of its 64 x 64 start state
   bool from_interior;
 };
-
-// threadIdx.x through an empty volatile asm: values derived from it (per-lane
-// LDS and buffer offsets) are then recomputed in each phase instead of being
-// hoisted out of the piece loop, where dozens of them would stay live in
-// registers across every phase.
-__device__ __forceinline__ int lane_tid() {
-  int t = static_cast<int>(threadIdx.x);
-  asm volatile("" : "+v"(t));
-  return t;
-}
 
 __device__ __forceinline__ const uint16_t* tri_blk(const uint16_t* m, int p, int q) {
   return m + tri_index(p, q) * kTriBlock;
@@ -585,7 +568,6 @@ __device__ __forceinline__ void adjoint_chain(BwdSmem& sm, const f32x4 (&S0)[4],
   const i16x8 gds01 = cat(gds[0], gds[1]), gds23 = cat(gds[2], gds[3]);
   const i16x8 dy01 = cat(dys[0], dys[1]), dy23 = cat(dys[2], dys[3]);
 
-  __builtin_amdgcn_sched_barrier(0);
   // dSA_p = Bh_p (g o dS) + sum_{q>=p} Arb^T(q, p) dYs_q.
   f32x4 dsa[4];
 #pragma unroll
@@ -601,7 +583,6 @@ __device__ __forceinline__ void adjoint_chain(BwdSmem& sm, const f32x4 (&S0)[4],
   dsa[2] = mfma32(cat(Lt(kArb, 2, 2), Lt(kArb, 3, 2)), dy23, dsa[2]);
   dsa[3] = mfma32(lo32(Lt(kArb, 3, 3)), lo32(dys[3]), dsa[3]);
 
-  __builtin_amdgcn_sched_barrier(0);
   // dZ = T^T dSA: dZ_p = T_pp^T (dSA_p + sum_{q>p} Lab^T(q, p) dZ_q).
   auto Tt = [&](int pb) {
     return lds_operand_tr<kTriStride>(sm.u.f.tinv[pb], 0, 0, g, n);
@@ -626,7 +607,6 @@ __device__ __forceinline__ void adjoint_chain(BwdSmem& sm, const f32x4 (&S0)[4],
   for (int pb = 0; pb < 4; ++pb)
     lds_store_transposed(sm.dz + (16 * cs) * kOpStride + 16 * pb, kOpStride, g, n, dz[pb]);
 
-  __builtin_amdgcn_sched_barrier(0);
   // dV^T (rows v of this slab, cols t of block pb):
   //   (g o dS)^T Kh^T + sum_{q>=pb} (dYs_q^T Ark(q, pb) + dZ_q^T Lak(q, pb)).
   // The C-layout operands of (g o dS), dYs and dZ serve as A operands of their
@@ -663,7 +643,6 @@ __device__ __forceinline__ void adjoint_chain(BwdSmem& sm, const f32x4 (&S0)[4],
     }
   }
 
-  __builtin_amdgcn_sched_barrier(0);
   // dS0 = g o dS + Rt^T dYs + At^T dZ.
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
@@ -824,8 +803,7 @@ __device__ void run_backward_step(BwdSmem& sm, const ChunkBwdParams& p, const To
     float e12[4];
 
     // ---- pass A: dRt = dYs S0^T + dArb Bh + dArk Kh, dAt = dZ S0^T + dLab Bh + dLak Kh.
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_setprio(1);
+      __builtin_amdgcn_s_setprio(1);
     {
       f32x4 acc_r = zero4(), acc_a = zero4();
 #pragma unroll
@@ -880,8 +858,7 @@ __device__ void run_backward_step(BwdSmem& sm, const ChunkBwdParams& p, const To
 
     // ---- pass B: dBc = dLab^T At + dArb^T Rt + g (SA dS^T), dKc likewise
     // with dLak, dArk and V.
-    __builtin_amdgcn_sched_barrier(0);
-    {
+      {
       f32x4 acc_b = zero4(), acc_k = zero4(), acc_bt = zero4(), acc_kt = zero4();
 #pragma unroll
       for (int c = 0; c < 64; c += 32) {

@@ -31,6 +31,27 @@ __device__ __forceinline__ int tri_index(int p, int q) { return (p * (p + 1)) / 
 
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// threadIdx.x through an empty volatile asm: values derived from it (per-lane
+// LDS and buffer offsets) are then recomputed in each phase of a chunk loop
+// instead of being hoisted out of it, where dozens of them would stay live
+// in registers across every phase.
+__device__ __forceinline__ int lane_tid() {
+  int t = static_cast<int>(threadIdx.x);
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
+// A kernel's by-value argument block read through an opaque kernarg pointer:
+// fields are fetched with scalar loads where used. Read through the argument
+// itself, the compiler hoists every pointer and buffer descriptor out of the
+// chunk loop into SGPRs, which then spill.
+template <typename P>
+__device__ __forceinline__ const __attribute__((address_space(4))) P& kernel_args() {
+  auto ptr = (const __attribute__((address_space(4))) P*)(__builtin_amdgcn_kernarg_segment_ptr());
+  asm volatile("" : "+s"(ptr));
+  return *ptr;
+}
+
 // 2^x on the hardware exponential (v_exp_f32). Every exponent here lies in
 // [-80, 80] (the decay span limit), inside fp32's normal range, so the
 // denormal-range handling of exp2f is not needed.
