@@ -745,14 +745,17 @@ def bench_training(args):
     sda = torch.empty((n_tok, heads, d), device=dev)
     grads_k = [torch.empty_like(t) for t in raw]
     ds0_k = torch.empty_like(ds)
+    # 64-token chunks have no interior piece starts; the buffer is passed as
+    # the autograd path passes it.
+    inner = torch.empty(capi.statetune_interior_bytes(d, heads, n_tok) // 4, device=dev)
     fwd_ms = _kernel_ms(lambda: capi.statetune_forward(
         *raw, sequence_chunk_offsets=offsets, chunk_token_starts=starts,
-        chunk_token_ends=ends, state=st_k, output=y_k, boundary=bnd, state_dot_a=sda),
-        args.training_steps, stream)
+        chunk_token_ends=ends, state=st_k, output=y_k, boundary=bnd, state_dot_a=sda,
+        interior=inner), args.training_steps, stream)
     bwd_ms = _kernel_ms(lambda: capi.statetune_backward(
         *raw, sequence_chunk_offsets=offsets, chunk_token_starts=starts,
         chunk_token_ends=ends, boundary=bnd, grad_output=dy, grad_final_state=ds,
-        grads=grads_k, grad_initial_state=ds0_k), args.training_steps, stream)
+        grads=grads_k, grad_initial_state=ds0_k, interior=inner), args.training_steps, stream)
     kernel_ms = fwd_ms + bwd_ms
     chunk_heads = batch * heads * (t_len // 64)
     flops = 3 * chunk_heads * chunk_flops()

@@ -91,10 +91,10 @@ def statetune_recurrent_fp32io16_forward(sequence_chunk_offsets, chunk_token_sta
 
 def statetune_forward_internal(sequence_chunk_offsets, chunk_token_starts,
                                chunk_token_ends, state, r, decay, k, v, a, b, output,
-                               boundary, state_dot_a, scale, decay_mode):
+                               boundary, state_dot_a, interior, scale, decay_mode):
     ops.statetune_forward_internal(
         sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, state, r, decay,
-        k, v, a, b, output, boundary, state_dot_a, float(scale), int(decay_mode))
+        k, v, a, b, output, boundary, state_dot_a, interior, float(scale), int(decay_mode))
 
 
 def statetune_recurrent_fp32io16_backward(sequence_chunk_offsets, chunk_token_starts,
@@ -112,11 +112,11 @@ def statetune_recurrent_fp32io16_backward(sequence_chunk_offsets, chunk_token_st
 def statetune_backward_internal(sequence_chunk_offsets, chunk_token_starts, chunk_token_ends,
                                 r, decay, k, v, a, b, grad_output, grad_final_state, boundary,
                                 grad_r, grad_decay, grad_k, grad_v, grad_a, grad_b,
-                                grad_initial_state, scale, decay_mode):
+                                grad_initial_state, interior, scale, decay_mode):
     ops.statetune_backward_internal(
         sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, r, decay, k, v, a, b,
         grad_output, grad_final_state, boundary, grad_r, grad_decay, grad_k, grad_v, grad_a,
-        grad_b, grad_initial_state, float(scale), int(decay_mode))
+        grad_b, grad_initial_state, interior, float(scale), int(decay_mode))
 
 
 def rl_infctx_chunk_fp32io16_forward(sequence_chunk_offsets, chunk_token_starts,

@@ -20,7 +20,7 @@ DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 DECAY_LOGITS, DECAY_RAW_W = 0, 1
 
 _INT, _I32, _I64 = ctypes.c_int, ctypes.c_int32, ctypes.c_int64
-_F32, _VP = ctypes.c_float, ctypes.c_void_p
+_F32, _VP, _SZ = ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
 
 # name -> argtypes, in the header's parameter order.
 SIGNATURES = {
@@ -30,10 +30,14 @@ SIGNATURES = {
     "frwkv_metadata_validate": [_VP, _VP, _I32, _I32, _I32, _VP, _VP, _VP, _VP],
     "frwkv_recurrent_forward": [_INT, _INT] + [_I32] * 6 + [_VP] * 12 + [_F32, _VP],
     "frwkv_chunk_forward": [_INT] * 3 + [_I32] * 5 + [_VP] * 12 + [_F32, _VP],
-    "frwkv_statetune_forward": [_INT] * 2 + [_I32] * 5 + [_VP] * 14 + [_F32, _VP],
-    "frwkv_statetune_backward": [_INT] * 2 + [_I32] * 5 + [_VP] * 20 + [_F32, _VP],
+    "frwkv_statetune_forward": [_INT] * 2 + [_I32] * 5 + [_VP] * 15 + [_F32, _VP],
+    "frwkv_statetune_interior_bytes": [_I32] * 3,
+    "frwkv_statetune_interior": [_INT] * 2 + [_I32] * 4 + [_VP] * 11 + [_VP],
+    "frwkv_statetune_backward": [_INT] * 2 + [_I32] * 5 + [_VP] * 22 + [_SZ, _F32, _VP],
+    "frwkv_statetune_backward_workspace_bytes": [_I32] * 3 + [_INT],
     "frwkv_pretrain_forward": [_INT] * 2 + [_I32] * 4 + [_VP] * 10,
-    "frwkv_pretrain_backward": [_INT] * 2 + [_I32] * 4 + [_VP] * 15,
+    "frwkv_pretrain_backward": [_INT] * 2 + [_I32] * 4 + [_VP] * 15 + [_SZ, _VP],
+    "frwkv_pretrain_backward_workspace_bytes": [_I32] * 4,
     "frwkv_chunk_replay": [_INT] * 2 + [_I32] * 4 + [_VP] * 12 + [_F32, _VP],
     "frwkv_recurrent_fp16_forward": [_I32] * 6 + [_VP] * 13 + [_F32, _VP],
     "frwkv_advance_i32": [_VP, _I64, _I32, _VP],
@@ -57,7 +61,7 @@ def library() -> ctypes.CDLL:
         for name, argtypes in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = argtypes
-            fn.restype = ctypes.c_int
+            fn.restype = ctypes.c_size_t if name.endswith("_bytes") else ctypes.c_int
         lib.frwkv_status_string.restype = ctypes.c_char_p
         lib.frwkv_last_error.restype = ctypes.c_char_p
         _LIB = lib
@@ -113,28 +117,49 @@ def chunk_forward(r, decay, k, v, a, b, *, state_pool, cu_seqlens, state_indices
 
 
 def statetune_forward(r, decay, k, v, a, b, *, sequence_chunk_offsets, chunk_token_starts,
-                      chunk_token_ends, state, output, boundary, state_dot_a, scale=1.0,
-                      decay_mode=DECAY_RAW_W, decay_bias=None):
+                      chunk_token_ends, state, output, boundary, state_dot_a, interior=None,
+                      scale=1.0, decay_mode=DECAY_RAW_W, decay_bias=None):
     n, h, d = r.shape
     _check(library().frwkv_statetune_forward(
         DTYPE[r.dtype], decay_mode, sequence_chunk_offsets.numel() - 1, h, d, n,
         chunk_token_starts.numel(), _p(sequence_chunk_offsets), _p(chunk_token_starts),
         _p(chunk_token_ends), _p(state), _p(r), _p(decay), _p(decay_bias), _p(k), _p(v),
-        _p(a), _p(b), _p(output), _p(boundary), _p(state_dot_a), float(scale), _stream()))
+        _p(a), _p(b), _p(output), _p(boundary), _p(state_dot_a), _p(interior), float(scale),
+        _stream()))
+
+
+def statetune_interior_bytes(head_size: int, heads: int, total_tokens: int) -> int:
+    return int(library().frwkv_statetune_interior_bytes(head_size, heads, total_tokens))
+
+
+def statetune_backward_workspace_bytes(head_size: int, heads: int, total_tokens: int,
+                                       interior_given: bool) -> int:
+    return int(library().frwkv_statetune_backward_workspace_bytes(
+        head_size, heads, total_tokens, int(bool(interior_given))))
+
+
+def workspace(nbytes: int, device) -> torch.Tensor | None:
+    """Device scratch of ``nbytes`` (None for 0)."""
+    return None if nbytes == 0 else torch.empty(nbytes, dtype=torch.uint8, device=device)
 
 
 def statetune_backward(r, decay, k, v, a, b, *, sequence_chunk_offsets, chunk_token_starts,
                        chunk_token_ends, boundary, grad_output, grad_final_state, grads,
-                       grad_initial_state, scale=1.0, decay_mode=DECAY_RAW_W,
-                       decay_bias=None):
-    """``grads`` = (grad_r, grad_decay, grad_k, grad_v, grad_a, grad_b)."""
+                       grad_initial_state, interior=None, work=None, scale=1.0,
+                       decay_mode=DECAY_RAW_W, decay_bias=None):
+    """``grads`` = (grad_r, grad_decay, grad_k, grad_v, grad_a, grad_b). ``work``:
+    the workspace (allocated here when None and needed)."""
     n, h, d = r.shape
+    if work is None:
+        work = workspace(statetune_backward_workspace_bytes(d, h, n, interior is not None),
+                         r.device)
     _check(library().frwkv_statetune_backward(
         DTYPE[r.dtype], decay_mode, sequence_chunk_offsets.numel() - 1, h, d, n,
         chunk_token_starts.numel(), _p(sequence_chunk_offsets), _p(chunk_token_starts),
-        _p(chunk_token_ends), _p(boundary), _p(r), _p(decay), _p(decay_bias), _p(k), _p(v),
-        _p(a), _p(b), _p(grad_output), _p(grad_final_state), *(_p(g) for g in grads),
-        _p(grad_initial_state), float(scale), _stream()))
+        _p(chunk_token_ends), _p(boundary), _p(interior), _p(r), _p(decay), _p(decay_bias),
+        _p(k), _p(v), _p(a), _p(b), _p(grad_output), _p(grad_final_state),
+        *(_p(g) for g in grads), _p(grad_initial_state), _p(work),
+        0 if work is None else work.numel(), float(scale), _stream()))
 
 
 def pretrain_forward(r, decay, k, v, a, b, *, output, boundary, state_dot_a,
@@ -150,9 +175,12 @@ def pretrain_backward(r, decay, k, v, a, b, *, grad_output, boundary, grads,
                       decay_mode=DECAY_LOGITS):
     """``grads`` = (grad_r, grad_decay, grad_k, grad_v, grad_a, grad_b)."""
     bsz, t_len, h, d = r.shape
+    work = workspace(int(library().frwkv_pretrain_backward_workspace_bytes(bsz, t_len, h, d)),
+                     r.device)
     _check(library().frwkv_pretrain_backward(
         DTYPE[r.dtype], decay_mode, bsz, t_len, h, d, _p(r), _p(decay), _p(k), _p(v), _p(a),
-        _p(b), _p(grad_output), _p(boundary), *(_p(g) for g in grads), _stream()))
+        _p(b), _p(grad_output), _p(boundary), *(_p(g) for g in grads), _p(work),
+        0 if work is None else work.numel(), _stream()))
 
 
 def chunk_replay(r, decay, k, v, a, b, *, chunk_token_starts, chunk_token_ends, boundary,

@@ -470,6 +470,27 @@ Tensor chunk_forward_internal(Tensor r, Tensor decay, Tensor k, Tensor v, Tensor
 
 // ------------------------------------------------------------ statetune ---
 
+// The interior-state buffer of the training ops: [ceil(N/P), H, D, D] fp32
+// (P = 64 at head size 64, else 16), or none.
+float* checked_interior(const std::optional<Tensor>& interior, const Tensor& r, int64_t d) {
+  if (!interior.has_value() || !interior->defined()) return nullptr;
+  check_device_contiguous(*interior, "interior");
+  TORCH_CHECK(interior->device() == r.device(), "interior must share the token device");
+  const size_t need = frwkv_statetune_interior_bytes(
+      static_cast<int32_t>(d), static_cast<int32_t>(r.size(1)), static_cast<int32_t>(r.size(0)));
+  TORCH_CHECK(interior->scalar_type() == at::kFloat &&
+                  static_cast<size_t>(interior->numel()) * sizeof(float) >= need,
+              "interior must be float32 with at least ", need, " bytes");
+  return interior->data_ptr<float>();
+}
+
+// Device scratch of the given size from PyTorch's caching allocator (on the
+// current stream), or an undefined tensor for 0 bytes.
+Tensor workspace_like(const Tensor& like, size_t bytes) {
+  if (bytes == 0) return Tensor();
+  return at::empty({static_cast<int64_t>(bytes)}, like.options().dtype(at::kByte));
+}
+
 void check_statetune_metadata(const Tensor& offsets, const Tensor& starts,
                               const Tensor& ends, const Tensor& state) {
   const std::pair<const Tensor*, const char*> all[] = {
@@ -493,7 +514,8 @@ void statetune_forward_impl(const Tensor& offsets, const Tensor& starts, const T
                             Tensor& state, const Tensor& r, const Tensor& decay,
                             const Tensor& k, const Tensor& v, const Tensor& a,
                             const Tensor& b, Tensor& output, Tensor& boundary,
-                            Tensor& state_dot_a, double scale, int decay_mode) {
+                            Tensor& state_dot_a, const std::optional<Tensor>& interior,
+                            double scale, int decay_mode) {
   TORCH_CHECK(std::isfinite(scale), "scale must be finite");
   check_device_contiguous(state, "state");
   TORCH_CHECK(state.scalar_type() == at::kFloat, "state must be float32");
@@ -518,6 +540,7 @@ void statetune_forward_impl(const Tensor& offsets, const Tensor& starts, const T
               "boundary must have shape [chunks,H,D,D] float32");
   TORCH_CHECK(state_dot_a.scalar_type() == at::kFloat && state_dot_a.sizes() == r.sizes(),
               "state_dot_a must have shape [total_tokens,H,D] float32");
+  float* interior_ptr = checked_interior(interior, r, d);
   c10::DeviceGuard guard(state.device());
   check_rc(frwkv_statetune_forward(
       io_code(r.scalar_type()), decay_mode, static_cast<int32_t>(state.size(0)),
@@ -526,7 +549,8 @@ void statetune_forward_impl(const Tensor& offsets, const Tensor& starts, const T
       starts.data_ptr<int32_t>(), ends.data_ptr<int32_t>(), state.data_ptr<float>(),
       r.data_ptr(), decay.data_ptr(), nullptr, k.data_ptr(), v.data_ptr(), a.data_ptr(),
       b.data_ptr(), output.data_ptr(), boundary.data_ptr<float>(),
-      state_dot_a.data_ptr<float>(), static_cast<float>(scale), current_stream(state)));
+      state_dot_a.data_ptr<float>(), interior_ptr, static_cast<float>(scale),
+      current_stream(state)));
 }
 
 // Reference statetune_recurrent_fp32io16_forward.cpp:26-44 (decay logits).
@@ -536,17 +560,18 @@ void statetune_recurrent_fp32io16_forward(Tensor offsets, Tensor starts, Tensor 
                                           Tensor output, Tensor boundary,
                                           Tensor state_dot_a, double scale) {
   statetune_forward_impl(offsets, starts, ends, state, r, decay_logits, k, v, a, b, output,
-                         boundary, state_dot_a, scale, FRWKV_DECAY_LOGITS);
+                         boundary, state_dot_a, std::nullopt, scale, FRWKV_DECAY_LOGITS);
 }
 
 void statetune_forward_internal(Tensor offsets, Tensor starts, Tensor ends, Tensor state,
                                 Tensor r, Tensor decay, Tensor k, Tensor v, Tensor a,
                                 Tensor b, Tensor output, Tensor boundary,
-                                Tensor state_dot_a, double scale, int64_t decay_mode) {
+                                Tensor state_dot_a, std::optional<Tensor> interior, double scale,
+                                int64_t decay_mode) {
   TORCH_CHECK(decay_mode == FRWKV_DECAY_LOGITS || decay_mode == FRWKV_DECAY_RAW_W,
               "decay_mode must be 0 (logits) or 1 (raw retention)");
   statetune_forward_impl(offsets, starts, ends, state, r, decay, k, v, a, b, output,
-                         boundary, state_dot_a, scale, static_cast<int>(decay_mode));
+                         boundary, state_dot_a, interior, scale, static_cast<int>(decay_mode));
 }
 
 // Reference statetune_recurrent_fp32io16_backward.cpp:34-82: optional
@@ -563,7 +588,8 @@ void statetune_backward_impl(const Tensor& offsets, const Tensor& starts, const 
                              std::optional<Tensor> grad_v, std::optional<Tensor> grad_a,
                              std::optional<Tensor> grad_b,
                              std::optional<Tensor> grad_initial_state, int64_t num_sequences,
-                             double scale, int decay_mode) {
+                             const std::optional<Tensor>& interior, double scale,
+                             int decay_mode) {
   TORCH_CHECK(std::isfinite(scale), "scale must be finite");
   check_chunk_tokens(r, decay, k, v, a, b, /*bf16_only=*/false, /*any_head_size=*/true);
   const int64_t heads = r.size(1), d = r.size(2);
@@ -616,18 +642,26 @@ void statetune_backward_impl(const Tensor& offsets, const Tensor& starts, const 
   TORCH_CHECK(grad_initial_state->scalar_type() == at::kFloat &&
                   grad_initial_state->numel() == num_sequences * heads * d * d,
               "grad_initial_state must have shape [B,H,D,D] float32");
+  const float* interior_ptr = checked_interior(interior, r, d);
   c10::DeviceGuard guard(r.device());
   const bool has_dy = grad_output.has_value() && grad_output->defined();
   const bool has_ds = grad_final_state.has_value() && grad_final_state->defined();
+  // Without the forward's interior states the call recomputes them into the
+  // workspace (chunks longer than one piece only), so any chunk length works.
+  const size_t ws_bytes = frwkv_statetune_backward_workspace_bytes(
+      static_cast<int32_t>(d), static_cast<int32_t>(heads), static_cast<int32_t>(r.size(0)),
+      interior_ptr != nullptr);
+  Tensor ws = workspace_like(r, ws_bytes);
   check_rc(frwkv_statetune_backward(
       io_code(r.scalar_type()), decay_mode, static_cast<int32_t>(num_sequences),
       static_cast<int32_t>(heads), static_cast<int32_t>(d), static_cast<int32_t>(r.size(0)),
       static_cast<int32_t>(starts.numel()), offsets.data_ptr<int32_t>(),
       starts.data_ptr<int32_t>(), ends.data_ptr<int32_t>(), boundary.data_ptr<float>(),
-      r.data_ptr(), decay.data_ptr(), nullptr, k.data_ptr(), v.data_ptr(), a.data_ptr(),
-      b.data_ptr(), has_dy ? grad_output->data_ptr() : nullptr,
+      interior_ptr, r.data_ptr(), decay.data_ptr(), nullptr, k.data_ptr(), v.data_ptr(),
+      a.data_ptr(), b.data_ptr(), has_dy ? grad_output->data_ptr() : nullptr,
       has_ds ? grad_final_state->data_ptr<float>() : nullptr, gr, gd, gk, gv, ga, gb,
-      grad_initial_state->data_ptr<float>(), static_cast<float>(scale), current_stream(r)));
+      grad_initial_state->data_ptr<float>(), ws.defined() ? ws.data_ptr() : nullptr, ws_bytes,
+      static_cast<float>(scale), current_stream(r)));
 }
 
 void statetune_recurrent_fp32io16_backward(
@@ -642,7 +676,7 @@ void statetune_recurrent_fp32io16_backward(
   statetune_backward_impl(offsets, starts, ends, r, decay_logits, k, v, a, b, grad_output,
                           grad_final_state, boundary, grad_r, grad_decay_logits, grad_k,
                           grad_v, grad_a, grad_b, grad_initial_state, final_state.size(0),
-                          scale, FRWKV_DECAY_LOGITS);
+                          std::nullopt, scale, FRWKV_DECAY_LOGITS);
 }
 
 void statetune_backward_internal(
@@ -650,13 +684,13 @@ void statetune_backward_internal(
     Tensor a, Tensor b, std::optional<Tensor> grad_output,
     std::optional<Tensor> grad_final_state, Tensor boundary, Tensor grad_r, Tensor grad_decay,
     Tensor grad_k, Tensor grad_v, Tensor grad_a, Tensor grad_b, Tensor grad_initial_state,
-    double scale, int64_t decay_mode) {
+    std::optional<Tensor> interior, double scale, int64_t decay_mode) {
   TORCH_CHECK(decay_mode == FRWKV_DECAY_LOGITS || decay_mode == FRWKV_DECAY_RAW_W,
               "decay_mode must be 0 (logits) or 1 (raw retention)");
   statetune_backward_impl(offsets, starts, ends, r, decay, k, v, a, b, grad_output,
                           grad_final_state, boundary, grad_r, grad_decay, grad_k, grad_v,
-                          grad_a, grad_b, grad_initial_state, offsets.numel() - 1, scale,
-                          static_cast<int>(decay_mode));
+                          grad_a, grad_b, grad_initial_state, offsets.numel() - 1, interior,
+                          scale, static_cast<int>(decay_mode));
 }
 
 // ---------------------------------------------------------------------------
@@ -726,13 +760,17 @@ void clampw_backward(Tensor r, Tensor w, Tensor k, Tensor v, Tensor a, Tensor b,
                        {&da, "da"}, {&db, "db"}}, head_size);
   check_clampw_side(r, s, sa);
   c10::DeviceGuard guard(r.device());
+  const size_t ws_bytes = frwkv_pretrain_backward_workspace_bytes(
+      static_cast<int32_t>(r.size(0)), static_cast<int32_t>(r.size(1)),
+      static_cast<int32_t>(r.size(2)), static_cast<int32_t>(head_size));
+  Tensor ws = workspace_like(r, ws_bytes);
   check_rc(frwkv_pretrain_backward(
       io_code(r.scalar_type()), FRWKV_DECAY_LOGITS, static_cast<int32_t>(r.size(0)),
       static_cast<int32_t>(r.size(1)), static_cast<int32_t>(r.size(2)),
       static_cast<int32_t>(head_size), r.data_ptr(), w.data_ptr(), k.data_ptr(), v.data_ptr(),
       a.data_ptr(), b.data_ptr(), dy.data_ptr(), s.data_ptr<float>(), dr.data_ptr(),
       dw.data_ptr(), dk.data_ptr(), dv.data_ptr(), da.data_ptr(), db.data_ptr(),
-      current_stream(r)));
+      ws.defined() ? ws.data_ptr() : nullptr, ws_bytes, current_stream(r)));
 }
 
 // ---------------------------------------------------------------------------
@@ -1248,7 +1286,8 @@ TORCH_LIBRARY(flashrwkv2, m) {
       "statetune_forward_internal(Tensor sequence_chunk_offsets, "
       "Tensor chunk_token_starts, Tensor chunk_token_ends, Tensor(a!) state, Tensor r, "
       "Tensor decay, Tensor k, Tensor v, Tensor a, Tensor b, Tensor(b!) output, "
-      "Tensor(c!) boundary, Tensor(d!) state_dot_a, float scale, int decay_mode) -> ()",
+      "Tensor(c!) boundary, Tensor(d!) state_dot_a, Tensor(e!)? interior, float scale, "
+      "int decay_mode) -> ()",
       &statetune_forward_internal);
   m.def(
       "statetune_recurrent_fp32io16_backward(Tensor sequence_chunk_offsets, "
@@ -1264,8 +1303,8 @@ TORCH_LIBRARY(flashrwkv2, m) {
       "Tensor chunk_token_ends, Tensor r, Tensor decay, Tensor k, Tensor v, Tensor a, "
       "Tensor b, Tensor? grad_output, Tensor? grad_final_state, Tensor boundary, "
       "Tensor(a!) grad_r, Tensor(b!) grad_decay, Tensor(c!) grad_k, Tensor(d!) grad_v, "
-      "Tensor(e!) grad_a, Tensor(f!) grad_b, Tensor(g!) grad_initial_state, float scale, "
-      "int decay_mode) -> ()",
+      "Tensor(e!) grad_a, Tensor(f!) grad_b, Tensor(g!) grad_initial_state, "
+      "Tensor? interior, float scale, int decay_mode) -> ()",
       &statetune_backward_internal);
   m.def(
       "rl_infctx_chunk_fp32io16_forward(Tensor sequence_chunk_offsets, Tensor chunk_token_starts, "

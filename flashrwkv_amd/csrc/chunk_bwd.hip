@@ -1239,14 +1239,27 @@ int dispatch_bwd(const ChunkBwdParams& p, int io_dtype, int decay_mode, int unit
 }  // namespace
 }  // namespace frwkv
 
+namespace {
+constexpr size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+}  // namespace
+
+extern "C" size_t frwkv_statetune_backward_workspace_bytes(int32_t head_size, int32_t num_heads,
+                                                           int32_t total_tokens,
+                                                           int interior_given) {
+  size_t bytes = align256(frwkv_train_slice_bytes(head_size, num_heads, total_tokens));
+  if (!interior_given) bytes += frwkv_statetune_interior_bytes(head_size, num_heads, total_tokens);
+  return bytes;
+}
+
 extern "C" int frwkv_statetune_backward(
     int io_dtype, int decay_mode, int32_t num_sequences, int32_t num_heads, int32_t head_size,
     int32_t total_tokens, int32_t num_chunks, const int32_t* sequence_chunk_offsets,
     const int32_t* chunk_token_starts, const int32_t* chunk_token_ends, const float* boundary,
-    const void* r, const void* decay, const void* decay_bias, const void* k, const void* v,
-    const void* a, const void* b, const void* grad_output, const float* grad_final_state,
-    void* grad_r, void* grad_decay, void* grad_k, void* grad_v, void* grad_a, void* grad_b,
-    float* grad_initial_state, float scale, void* stream) {
+    const float* interior, const void* r, const void* decay, const void* decay_bias,
+    const void* k, const void* v, const void* a, const void* b, const void* grad_output,
+    const float* grad_final_state, void* grad_r, void* grad_decay, void* grad_k, void* grad_v,
+    void* grad_a, void* grad_b, float* grad_initial_state, void* workspace,
+    size_t workspace_bytes, float scale, void* stream) {
   using namespace frwkv;
   if (!sequence_chunk_offsets || !chunk_token_starts || !chunk_token_ends || !boundary || !r ||
       !decay || !k || !v || !a || !b || !grad_r || !grad_decay || !grad_k || !grad_v ||
@@ -1261,17 +1274,38 @@ extern "C" int frwkv_statetune_backward(
   if (!__builtin_isfinite(scale)) {
     return set_error(FRWKV_ERR_INVALID_ARGUMENT, "scale must be finite");
   }
+  if (head_size != 64 && head_size != 128 && head_size != 256) {
+    return set_error(FRWKV_ERR_UNSUPPORTED, "head size must be 64, 128, or 256, got %d",
+                     head_size);
+  }
+  // Workspace: the gradient slices (head size 256), then, when interior is
+  // null, the interior states this call recomputes from the boundaries.
+  const size_t slice_bytes = frwkv_train_slice_bytes(head_size, num_heads, total_tokens);
+  const size_t need = frwkv_statetune_backward_workspace_bytes(head_size, num_heads,
+                                                               total_tokens, interior != nullptr);
+  const bool fill = interior == nullptr && workspace != nullptr;
+  if ((slice_bytes > 0 || fill) && (workspace == nullptr || workspace_bytes < need)) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT,
+                     "frwkv_statetune_backward: workspace of %zu bytes given, %zu needed",
+                     workspace != nullptr ? workspace_bytes : static_cast<size_t>(0), need);
+  }
+  float* slices = slice_bytes > 0 ? static_cast<float*>(workspace) : nullptr;
+  if (fill) {
+    float* filled = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(slice_bytes));
+    const int rc = frwkv_statetune_interior(io_dtype, decay_mode, num_heads, head_size,
+                                            total_tokens, num_chunks, chunk_token_starts,
+                                            chunk_token_ends, boundary, r, decay, decay_bias, k,
+                                            v, a, b, filled, stream);
+    if (rc != FRWKV_OK) return rc;
+    interior = filled;
+  }
   if (head_size == 128 || head_size == 256) {
     return frwkv_train_recurrent_backward(
         io_dtype, decay_mode, num_sequences, num_heads, head_size, total_tokens,
         sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, num_chunks, /*dense_t=*/0,
-        boundary,
-        r, decay, decay_bias, k, v, a, b, grad_output, grad_final_state, grad_r, grad_decay,
-        grad_k, grad_v, grad_a, grad_b, grad_initial_state, scale, stream);
-  }
-  if (head_size != 64) {
-    return set_error(FRWKV_ERR_UNSUPPORTED, "head size must be 64, 128, or 256, got %d",
-                     head_size);
+        boundary, r, decay, decay_bias, k, v, a, b, grad_output, grad_final_state, grad_r,
+        grad_decay, grad_k, grad_v, grad_a, grad_b, grad_initial_state, interior, slices, scale,
+        stream);
   }
   ChunkBwdParams p{};
   p.num_heads = num_heads;
@@ -1281,6 +1315,7 @@ extern "C" int frwkv_statetune_backward(
   p.seg_starts = chunk_token_starts;
   p.seg_ends = chunk_token_ends;
   p.checkpoint = boundary;
+  p.interior = interior;
   p.r = r;
   p.decay = decay;
   p.bias = decay_bias;
@@ -1302,13 +1337,20 @@ extern "C" int frwkv_statetune_backward(
                       static_cast<hipStream_t>(stream));
 }
 
+extern "C" size_t frwkv_pretrain_backward_workspace_bytes(int32_t batch, int32_t tokens,
+                                                          int32_t num_heads, int32_t head_size) {
+  if (batch <= 0 || tokens <= 0 || static_cast<int64_t>(batch) * tokens > INT32_MAX) return 0;
+  return frwkv_train_slice_bytes(head_size, num_heads, batch * tokens);
+}
+
 extern "C" int frwkv_pretrain_backward(int io_dtype, int decay_mode, int32_t batch,
                                        int32_t tokens, int32_t num_heads, int32_t head_size,
                                        const void* r, const void* decay, const void* k,
                                        const void* v, const void* a, const void* b,
                                        const void* grad_output, const float* boundary,
                                        void* grad_r, void* grad_decay, void* grad_k,
-                                       void* grad_v, void* grad_a, void* grad_b, void* stream) {
+                                       void* grad_v, void* grad_a, void* grad_b,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
   using namespace frwkv;
   if (!boundary || !r || !decay || !k || !v || !a || !b || !grad_output || !grad_r ||
       !grad_decay || !grad_k || !grad_v || !grad_a || !grad_b) {
@@ -1324,11 +1366,18 @@ extern "C" int frwkv_pretrain_backward(int io_dtype, int decay_mode, int32_t bat
     return set_error(FRWKV_ERR_INVALID_ARGUMENT, "frwkv_pretrain_backward: B * T too large");
   }
   if (head_size == 128 || head_size == 256) {
+    const size_t need = frwkv_train_slice_bytes(head_size, num_heads, batch * tokens);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
+      return set_error(FRWKV_ERR_INVALID_ARGUMENT,
+                       "frwkv_pretrain_backward: workspace of %zu bytes given, %zu needed",
+                       workspace != nullptr ? workspace_bytes : static_cast<size_t>(0), need);
+    }
     return frwkv_train_recurrent_backward(
         io_dtype, decay_mode, batch, num_heads, head_size, batch * tokens, nullptr, nullptr,
         nullptr, 0, tokens, boundary, r, decay, /*decay_bias=*/nullptr, k, v, a, b, grad_output,
         /*grad_final_state=*/nullptr, grad_r, grad_decay, grad_k, grad_v, grad_a, grad_b,
-        /*grad_initial_state=*/nullptr, 1.0f, stream);
+        /*grad_initial_state=*/nullptr, /*interior=*/nullptr,
+        need > 0 ? static_cast<float*>(workspace) : nullptr, 1.0f, stream);
   }
   if (head_size != 64) {
     return set_error(FRWKV_ERR_UNSUPPORTED, "head size must be 64, 128, or 256, got %d",

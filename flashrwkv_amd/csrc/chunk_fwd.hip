@@ -105,6 +105,15 @@ struct ChunkFwdParams {
   // 1: the initial states are read and never written back (replay from
   // stored boundaries).
   int32_t read_only_state;
+  // [ceil(total_tokens / 64), H, D, D] or null: the state at every 64-token
+  // piece start inside a segment (not at the segment start), at slot
+  // (piece start) / 64. Interior starts of different segments lie more than
+  // 64 tokens apart, so the slots are distinct.
+  float* interior;
+  // 1 (replay layout, one segment per unit): only the interior states are
+  // wanted; segments of at most 64 tokens have none and are skipped, and a
+  // segment's last piece is not computed.
+  int32_t fill_only;
 };
 
 // Token rows of one chunk held by a thread: r, w, k, a, b for 2 tokens x 8
@@ -776,8 +785,24 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
         }
       }
     }
+    if (p.fill_only && t_end - t_begin <= kChunk) continue;
     for (int c0 = t_begin; c0 < t_end; c0 += kChunk) {
       const int ntok = min(kChunk, t_end - c0);
+      if (p.interior != nullptr && c0 > t_begin) {
+        const auto irs = buffer_rsrc(
+            p.interior + (static_cast<int64_t>(c0 / kChunk) * heads + head) * kHead * kHead,
+            kHead * kHead * 4);
+        const uint32_t i_off = static_cast<uint32_t>((4 * g) * kHead + 16 * wave + n) * 4;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(S[kb][j]), irs, i_off,
+                                                  (16 * kb + j) * kHead * 4, 0);
+          }
+        }
+      }
+      if (p.fill_only && c0 + kChunk >= t_end) break;
       int nseg = seg, nc0 = c0, nend = t_end;
       const bool has_next = next_chunk(nseg, nc0, nend);
       // Every-16-tokens boundary layout [B, H, dense_t / 16, D, D]: the state
@@ -837,8 +862,9 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
         }
         {
           const int64_t base = (static_cast<int64_t>(c0) * heads + head) * kHead;
-          const auto out_rs = buffer_rsrc(static_cast<S16c*>(p.out) + base,
-                                          static_cast<uint32_t>(ntok) * row_bytes);
+          const auto out_rs = buffer_rsrc(
+              p.out != nullptr ? static_cast<S16c*>(p.out) + base : nullptr,
+              p.out != nullptr ? static_cast<uint32_t>(ntok) * row_bytes : 0u);
           const auto sda_rs = buffer_rsrc(
               p.state_dot_a != nullptr ? p.state_dot_a + base : nullptr,
               p.state_dot_a != nullptr ? 2u * static_cast<uint32_t>(ntok) * row_bytes : 0u);
@@ -979,7 +1005,8 @@ extern "C" int frwkv_statetune_forward(
     const int32_t* sequence_chunk_offsets, const int32_t* chunk_token_starts,
     const int32_t* chunk_token_ends, float* state, const void* r, const void* decay,
     const void* decay_bias, const void* k, const void* v, const void* a, const void* b,
-    void* output, float* boundary, float* state_dot_a, float scale, void* stream) {
+    void* output, float* boundary, float* state_dot_a, float* interior, float scale,
+    void* stream) {
   using namespace frwkv;
   if (!sequence_chunk_offsets || !chunk_token_starts || !chunk_token_ends || !state ||
       !boundary || !state_dot_a) {
@@ -1001,7 +1028,8 @@ extern "C" int frwkv_statetune_forward(
                                          chunk_token_starts, chunk_token_ends, num_chunks,
                                          /*dense_t=*/0,
                                          state, r, decay, decay_bias, k, v, a, b, output,
-                                         boundary, state_dot_a, scale, stream);
+                                         boundary, state_dot_a, interior, /*fill_only=*/0,
+                                         scale, stream);
   }
   if (head_size != 64) {
     return set_error(FRWKV_ERR_UNSUPPORTED, "head size must be 64, 128, or 256, got %d",
@@ -1026,9 +1054,69 @@ extern "C" int frwkv_statetune_forward(
   p.out = output;
   p.boundary = boundary;
   p.state_dot_a = state_dot_a;
+  p.interior = interior;
   p.scale = scale;
   p.out_elems = static_cast<int64_t>(total_tokens) * num_heads * head_size;
   return dispatch_chunk_io<float>(p, io_dtype, decay_mode, num_sequences * num_heads,
+                                  static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t frwkv_statetune_interior_bytes(int32_t head_size, int32_t num_heads,
+                                                 int32_t total_tokens) {
+  if (num_heads <= 0 || total_tokens <= 0) return 0;
+  const int64_t piece = head_size == 64 ? 64 : 16;
+  const int64_t slots = (total_tokens + piece - 1) / piece;
+  return static_cast<size_t>(slots * num_heads * head_size * head_size * 4);
+}
+
+extern "C" int frwkv_statetune_interior(int io_dtype, int decay_mode, int32_t num_heads,
+                                        int32_t head_size, int32_t total_tokens,
+                                        int32_t num_chunks, const int32_t* chunk_token_starts,
+                                        const int32_t* chunk_token_ends, const float* boundary,
+                                        const void* r, const void* decay, const void* decay_bias,
+                                        const void* k, const void* v, const void* a,
+                                        const void* b, float* interior, void* stream) {
+  using namespace frwkv;
+  if (!chunk_token_starts || !chunk_token_ends || !boundary || !interior || !r || !decay ||
+      !k || !v || !a || !b) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT, "frwkv_statetune_interior: null pointer argument");
+  }
+  if (num_chunks <= 0 || num_heads <= 0 || total_tokens <= 0) {
+    return set_error(FRWKV_ERR_INVALID_ARGUMENT,
+                     "frwkv_statetune_interior: sizes must be positive");
+  }
+  if (head_size == 128 || head_size == 256) {
+    return frwkv_train_recurrent_forward(io_dtype, decay_mode, num_chunks, num_heads, head_size,
+                                         total_tokens, nullptr, chunk_token_starts,
+                                         chunk_token_ends, num_chunks, /*dense_t=*/0,
+                                         const_cast<float*>(boundary), r, decay, decay_bias, k,
+                                         v, a, b, nullptr, nullptr, nullptr, interior,
+                                         /*fill_only=*/1, 1.0f, stream);
+  }
+  if (head_size != 64) {
+    return set_error(FRWKV_ERR_UNSUPPORTED, "head size must be 64, 128, or 256, got %d",
+                     head_size);
+  }
+  ChunkFwdParams p{};
+  p.num_heads = num_heads;
+  p.total_tokens = total_tokens;
+  p.state_slots = num_chunks;
+  p.seg_starts = chunk_token_starts;
+  p.seg_ends = chunk_token_ends;
+  p.num_segments = num_chunks;
+  p.state = const_cast<float*>(boundary);
+  p.read_only_state = 1;
+  p.r = r;
+  p.decay = decay;
+  p.bias = decay_bias;
+  p.k = k;
+  p.v = v;
+  p.a = a;
+  p.b = b;
+  p.interior = interior;
+  p.fill_only = 1;
+  p.scale = 1.0f;
+  return dispatch_chunk_io<float>(p, io_dtype, decay_mode, num_chunks * num_heads,
                                   static_cast<hipStream_t>(stream));
 }
 
@@ -1056,7 +1144,8 @@ extern "C" int frwkv_pretrain_forward(int io_dtype, int decay_mode, int32_t batc
     return frwkv_train_recurrent_forward(io_dtype, decay_mode, batch, num_heads, head_size,
                                          batch * tokens, nullptr, nullptr, nullptr, 0, tokens,
                                          /*state=*/nullptr, r, decay, /*decay_bias=*/nullptr, k,
-                                         v, a, b, output, boundary, state_dot_a, 1.0f, stream);
+                                         v, a, b, output, boundary, state_dot_a,
+                                         /*interior=*/nullptr, /*fill_only=*/0, 1.0f, stream);
   }
   if (head_size != 64) {
     return set_error(FRWKV_ERR_UNSUPPORTED, "head size must be 64, 128, or 256, got %d",

@@ -106,6 +106,15 @@ struct TrainParams {
   float* dstate0;  // or null
   float* accum;    // [groups, 5, N*H*D] fp32 slices (dr, dk, db, ddecay, da), groups > 1
   float scale;
+  // [ceil(N/16), H, D, D] or null: the state at every 16-token piece start
+  // inside a chunk (not at the chunk start), at slot (piece start) / 16;
+  // interior starts of different chunks lie more than 16 tokens apart, so the
+  // slots are distinct. Written by the forward, read by the backward.
+  float* interior;
+  // Forward only: 1 = one chunk per unit (seg_offsets null; chunk c starts from
+  // state[c]), only the interior states are written; chunks of at most 16
+  // tokens are skipped and a chunk's last piece is not computed.
+  int32_t fill_only;
 };
 
 struct Chunk {
@@ -118,6 +127,9 @@ __device__ __forceinline__ void chunk_range(const TrainParams& p, int seq, int& 
   if (p.dense_t > 0) {
     c_begin = 0;
     c_end = p.dense_t / kPiece;
+  } else if (p.seg_offsets == nullptr) {
+    c_begin = seq;
+    c_end = min(seq + 1, p.num_chunks);
   } else {
     // Clamped to the chunk arrays, so malformed offsets cannot address
     // outside them.
@@ -403,9 +415,16 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_fwd_kernel(TrainPar
   }
   __syncthreads();
 
+  if (p.fill_only && (c >= c_end || ch.end - ch.start <= kPiece)) return;
   while (c < c_end && ok) {
     const int n = min(kPiece, ch.end - t0);
     const bool first = t0 == ch.start;
+    if (!first && p.interior != nullptr) {
+      store_slab<D, kRpl>(p.interior + (static_cast<int64_t>(t0 / kPiece) * p.num_heads + head) *
+                                           static_cast<int64_t>(D) * D,
+                          s, row0, col);
+    }
+    if (p.fill_only && t0 + kPiece >= ch.end) break;
     int c_n = c;
     Chunk ch_n = ch;
     int32_t t0_n = t0 + kPiece;
@@ -421,7 +440,7 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_fwd_kernel(TrainPar
     const int n_n = has_next && ok_n ? min(kPiece, ch_n.end - t0_n) : 0;
     if (n_n > 0) load_piece(g, t0_n, n_n);
 
-    if (first) store_slab<D, kRpl>(p.ckpt + ch.ckpt_off, s, row0, col);
+    if (first && p.ckpt != nullptr) store_slab<D, kRpl>(p.ckpt + ch.ckpt_off, s, row0, col);
     const FwdStage<D>& cur = st[buf];
     for (int i = 0; i < n; ++i) {
       const float4 vv = decode4f<T>(lds8(&cur.v[i][wcol]));
@@ -442,7 +461,7 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_fwd_kernel(TrainPar
         }
       }
       y = sum_keys4<L::kCg, false>(y);
-      if (rg == 0) {
+      if (rg == 0 && p.out != nullptr) {
         const int64_t e = (t0 + i) * hd + head_off + col;
         *reinterpret_cast<float4*>(p.state_dot_a + e) = sa;
         store4<T>(static_cast<typename IoTraits<T>::storage*>(p.out) + e, p.scale * y.x,
@@ -458,7 +477,7 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_fwd_kernel(TrainPar
     buf ^= 1;
   }
 
-  if (p.state != nullptr) {
+  if (p.state != nullptr && !p.fill_only) {
     if (!ok) {
       const float nan = __int_as_float(0x7fc00000);
 #pragma unroll
@@ -569,14 +588,26 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_bwd_kernel(TrainPar
   int buf = 0;
 
   for (int c = c_end - 1; c >= c_begin; --c) {
-    const Chunk ch = chunk_at<D>(p, seq, head, c);
-    const bool range_ok = chunk_ok(ch, p.total_tokens);
-    const int n = ch.end - ch.start;
-    if (!range_ok || n > kPiece) failed = true;
+    const Chunk whole = chunk_at<D>(p, seq, head, c);
+    const bool range_ok = chunk_ok(whole, p.total_tokens);
+    const int len = whole.end - whole.start;
+    // Pieces of kPiece tokens from the chunk start; piece j > 0 starts from
+    // the interior state at slot (its first token) / kPiece.
+    const int pieces = len > kPiece ? (len + kPiece - 1) / kPiece : 1;
+    if (!range_ok || (pieces > 1 && p.interior == nullptr)) failed = true;
     if (failed) {
-      if (range_ok) nan_fill(ch);
+      if (range_ok) nan_fill(whole);
       continue;
     }
+   for (int pj = pieces - 1; pj >= 0; --pj) {
+    Chunk ch;
+    ch.start = whole.start + kPiece * pj;
+    ch.end = min(ch.start + kPiece, whole.end);
+    const float* ck =
+        pj == 0 ? p.ckpt + whole.ckpt_off
+                : p.interior + (static_cast<int64_t>(ch.start / kPiece) * p.num_heads + head) *
+                                   static_cast<int64_t>(D) * D;
+    const int n = ch.end - ch.start;
     if (n == 0) continue;
 
     // Stage the chunk (the previous chunk's last reads ended at a barrier).
@@ -619,7 +650,6 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_bwd_kernel(TrainPar
     }
     __syncthreads();
 
-    const float* ck = p.ckpt + ch.ckpt_off;
     auto step = [&](float4 (&s)[kRpl], int i) {
       const float4 vv = decode4f<T>(lds8(&sm.v[i][wcol]));
       step_state<D, T, true>(s, sm.a[i], sm.b[i], sm.k[i], sm.w[i], vv, row0);
@@ -779,7 +809,8 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_bwd_kernel(TrainPar
       }
       buf ^= 1;
     }
-    __syncthreads();  // staging of the next chunk overwrites the rows
+    __syncthreads();  // staging of the next piece overwrites the rows
+   }
   }
 
   if (p.dstate0 != nullptr) {
@@ -911,9 +942,11 @@ int frwkv_train_recurrent_forward(int io_dtype, int decay_mode, int32_t num_sequ
                                   const void* r, const void* decay, const void* decay_bias,
                                   const void* k, const void* v, const void* a, const void* b,
                                   void* output, float* boundary, float* state_dot_a,
-                                  float scale, void* stream) {
+                                  float* interior, int fill_only, float scale, void* stream) {
   using namespace frwkv;
   TrainParams p{};
+  p.interior = interior;
+  p.fill_only = fill_only;
   p.num_heads = num_heads;
   p.total_tokens = total_tokens;
   p.num_sequences = num_sequences;
@@ -947,10 +980,12 @@ int frwkv_train_recurrent_backward(int io_dtype, int decay_mode, int32_t num_seq
                                    const void* a, const void* b, const void* grad_output,
                                    const float* grad_final_state, void* grad_r,
                                    void* grad_decay, void* grad_k, void* grad_v, void* grad_a,
-                                   void* grad_b, float* grad_initial_state, float scale,
+                                   void* grad_b, float* grad_initial_state,
+                                   const float* interior, float* slices, float scale,
                                    void* stream) {
   using namespace frwkv;
   TrainParams p{};
+  p.interior = const_cast<float*>(interior);
   p.num_heads = num_heads;
   p.total_tokens = total_tokens;
   p.num_sequences = num_sequences;
@@ -978,23 +1013,22 @@ int frwkv_train_recurrent_backward(int io_dtype, int decay_mode, int32_t num_seq
   p.dstate0 = grad_initial_state;
   p.scale = scale;
   const auto s = static_cast<hipStream_t>(stream);
-  const int groups = slice_groups(head_size);
-  void* mem = nullptr;
-  if (groups > 1) {
-    // Per-group fp32 slices: stream-ordered allocation, released on the same
-    // stream after the kernel that adds them.
-    const size_t bytes =
-        static_cast<size_t>(groups) * 5 * static_cast<size_t>(total_tokens) * num_heads *
-        head_size * sizeof(float);
-    if (hipMallocAsync(&mem, bytes, s) != hipSuccess) {
-      (void)hipGetLastError();
-      return set_error(FRWKV_ERR_HIP,
-                       "training backward: cannot allocate %zu bytes of gradient slices", bytes);
+  if (slice_groups(head_size) > 1) {
+    if (slices == nullptr) {
+      return set_error(FRWKV_ERR_INVALID_ARGUMENT,
+                       "training backward at head size %d needs the gradient-slice workspace",
+                       head_size);
     }
-    p.accum = static_cast<float*>(mem);
+    p.accum = slices;
   }
   const int rc = dispatch_train_io(p, io_dtype, decay_mode, head_size,
                                    num_sequences * num_heads, /*backward=*/true, s);
-  if (mem != nullptr) (void)hipFreeAsync(mem, s);
   return rc;
+}
+
+size_t frwkv_train_slice_bytes(int32_t head_size, int32_t num_heads, int32_t total_tokens) {
+  const int groups = frwkv::slice_groups(head_size);
+  if (groups <= 1 || num_heads <= 0 || total_tokens <= 0) return 0;
+  return static_cast<size_t>(groups) * 5 * static_cast<size_t>(total_tokens) * num_heads *
+         head_size * sizeof(float);
 }

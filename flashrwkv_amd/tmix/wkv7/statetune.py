@@ -7,10 +7,11 @@ bf16-MFMA kernels, 128 and 256 the per-token fp32 training kernels; either
 backward recomputes every chunk from stored states instead of dividing by the
 decay.
 
-The backward kernels work on chunks of at most 64 tokens (head size 64) or 16
-tokens (128, 256). Caller chunks that are longer are split internally (one
-device-to-host copy of the chunk metadata per forward); the boundary output
-still holds the state at each caller chunk start.
+Caller chunks may have any length. The kernels walk a chunk in pieces of P
+tokens (P = 64 at head size 64, 16 at 128 and 256); the forward keeps the
+state at each interior piece start in a buffer indexed by (piece start) / P,
+which the backward reads. Nothing reads the chunk metadata on the host, so a
+training step never synchronises and can be captured in a HIP graph.
 """
 
 from __future__ import annotations
@@ -71,63 +72,44 @@ METADATA = (
 )
 
 
-def _kernel_chunk(head_size: int) -> int:
-    """Longest chunk the backward kernels take for this head size."""
+def _piece_len(head_size: int) -> int:
+    """Piece length of the training kernels for this head size."""
     return 64 if head_size == 64 else 16
 
 
-def _kernel_chunks(offsets, starts, ends, limit):
-    """Caller chunks cut into kernel chunks of at most ``limit`` tokens.
-
-    Returns ``None`` when every caller chunk fits, else ``(offsets, starts,
-    ends, first)`` on the device, where ``first[c]`` is the kernel chunk that
-    begins caller chunk ``c``.
-    """
-    lo = starts.cpu().long()
-    hi = ends.cpu().long()
-    if int((hi - lo).max()) <= limit:
-        return None
-    pieces = torch.clamp((hi - lo + limit - 1) // limit, min=1)
-    first = torch.zeros_like(pieces)
-    first[1:] = torch.cumsum(pieces, 0)[:-1]
-    owner = torch.repeat_interleave(torch.arange(pieces.numel()), pieces)
-    rank = torch.arange(int(pieces.sum())) - first[owner]
-    k_start = lo[owner] + rank * limit
-    k_end = torch.minimum(k_start + limit, hi[owner])
-    k_end = torch.maximum(k_end, k_start)  # an empty caller chunk stays one empty piece
-    k_off = torch.cat([first, first.new_tensor([int(pieces.sum())])])[offsets.cpu().long()]
-    dev = offsets.device
-    return tuple(t.to(device=dev, dtype=torch.int32) for t in (k_off, k_start, k_end, first))
+def _interior(r: torch.Tensor, heads: int, d: int) -> torch.Tensor:
+    """Buffer for the interior piece-start states: ceil(N / P) slots."""
+    p = _piece_len(d)
+    slots = (r.shape[0] + p - 1) // p
+    return torch.empty((slots, heads, d, d), device=r.device, dtype=torch.float32)
 
 
 class _StateTune(torch.autograd.Function):
-    """Forward saves the kernel-chunk start states; backward recomputes each
-    kernel chunk from them (reference ``statetune.py:79-199`` inverts the decay
-    instead)."""
+    """Forward keeps the chunk-start and interior piece-start states; backward
+    recomputes each piece from them (reference ``statetune.py:79-199``
+    divides by the decay instead)."""
 
     @staticmethod
     def forward(ctx, initial_state, offsets, starts, ends, r, decay, k, v, a, b, scale,
                 decay_mode):
         state = initial_state.detach().contiguous().clone()
         heads, d = state.shape[1], state.shape[2]
-        split = _kernel_chunks(offsets, starts, ends, _kernel_chunk(d))
-        meta = (offsets, starts, ends) if split is None else split[:3]
-        checkpoint = torch.empty((meta[1].numel(), heads, d, d), device=state.device,
-                                 dtype=torch.float32)
+        boundary = torch.empty((starts.numel(), heads, d, d), device=state.device,
+                               dtype=torch.float32)
+        interior = _interior(r, heads, d)
         output = torch.empty_like(v)
         state_dot_a = torch.empty_like(r, dtype=torch.float32)
-        C.native().statetune_forward_internal(*meta, state, r, decay, k, v, a, b, output,
-                                              checkpoint, state_dot_a, float(scale),
-                                              int(decay_mode))
-        boundary = checkpoint if split is None else checkpoint.index_select(0, split[3])
-        ctx.save_for_backward(*meta, r, decay, k, v, a, b, checkpoint)
+        C.native().statetune_forward_internal(offsets, starts, ends, state, r, decay, k, v, a, b,
+                                              output, boundary, state_dot_a, interior,
+                                              float(scale), int(decay_mode))
+        ctx.save_for_backward(offsets, starts, ends, r, decay, k, v, a, b, boundary, interior)
         ctx.scale, ctx.decay_mode = float(scale), int(decay_mode)
         ctx.mark_non_differentiable(boundary, state_dot_a)
         return output, state, boundary, state_dot_a
 
     @staticmethod
     def backward(ctx, grad_output, grad_final_state, _grad_boundary, _grad_state_dot_a):
-        offsets, starts, ends, r, decay, k, v, a, b, checkpoint = ctx.saved_tensors
+        offsets, starts, ends, r, decay, k, v, a, b, boundary, interior = ctx.saved_tensors
         grads = [torch.empty_like(t) for t in (r, decay, k, v, a, b)]
         d = r.shape[2]
         grad_state = torch.empty((offsets.numel() - 1, r.shape[1], d, d), device=r.device,
@@ -135,8 +117,8 @@ class _StateTune(torch.autograd.Function):
         dy = None if grad_output is None else grad_output.contiguous()
         ds = None if grad_final_state is None else grad_final_state.contiguous().float()
         C.native().statetune_backward_internal(offsets, starts, ends, r, decay, k, v, a, b, dy,
-                                               ds, checkpoint, *grads, grad_state, ctx.scale,
-                                               ctx.decay_mode)
+                                               ds, boundary, *grads, grad_state, interior,
+                                               ctx.scale, ctx.decay_mode)
         return (grad_state, None, None, None, *grads, None, None)
 
 

@@ -4,9 +4,11 @@
  * libflashrwkv_amd.so exports these entry points. They take plain device
  * pointers, sizes and a HIP stream (passed as void*, a hipStream_t; NULL is
  * the null stream), launch hand-written gfx950 HIP kernels on that stream and
- * return immediately (no host synchronisation, no allocation). Every call
- * returns FRWKV_OK or an error code; frwkv_last_error() gives the message of
- * the last failing call on the calling thread.
+ * return immediately: no host synchronisation and no device allocation (entry
+ * points that need scratch memory take a caller workspace, sized by a
+ * matching *_bytes query). Every call returns FRWKV_OK or an error code;
+ * frwkv_last_error() gives the message of the last failing call on the
+ * calling thread.
  *
  * Tensor conventions (all row-major, contiguous, device memory):
  *   tokens   r, decay, k, v, a, b, output: [total_tokens, H, D] of io_dtype
@@ -31,7 +33,7 @@
 extern "C" {
 #endif
 
-#define FRWKV_ABI_VERSION 1
+#define FRWKV_ABI_VERSION 2
 
 enum frwkv_status {
   FRWKV_OK = 0,
@@ -192,15 +194,20 @@ int frwkv_chunk_forward(int io_dtype, int decay_mode, int pool_dtype,
 /*
  * Training (StateTune) forward with caller chunk metadata: sequence s owns
  * chunks sequence_chunk_offsets[s] .. sequence_chunk_offsets[s+1]-1, chunk c
- * covers tokens chunk_token_starts[c] .. chunk_token_ends[c]-1. state
- * [B,H,D,D] fp32 holds S0 on entry and the final state on return (the caller
- * passes a copy). boundary [num_chunks,H,D,D] fp32 receives the state at each
- * chunk start; state_dot_a [total_tokens,H,D] fp32 receives a_t^T S_{t-1}.
+ * covers tokens chunk_token_starts[c] .. chunk_token_ends[c]-1 (any length).
+ * state [B,H,D,D] fp32 holds S0 on entry and the final state on return (the
+ * caller passes a copy). boundary [num_chunks,H,D,D] fp32 receives the state
+ * at each chunk start; state_dot_a [total_tokens,H,D] fp32 receives
+ * a_t^T S_{t-1}. interior (NULL: not written) receives the state at every
+ * piece start inside a chunk, at slot (piece start) / P, where the piece
+ * length P is 64 tokens for head size 64 and 16 for 128 and 256; it holds
+ * frwkv_statetune_interior_bytes, and only the slots of chunks longer than P
+ * are written. Interior piece starts of different chunks lie more than P
+ * tokens apart, so the slots never collide.
  * Replaces statetune_recurrent_fp32io16_forward_cuda
  * (csrc/sm90/tmix/wkv7/statetune_recurrent_fp32io16_forward.cu:32-224;
  * binding statetune_recurrent_fp32io16_forward.cpp:26-56). head_size 64
- * runs the chunked MFMA kernel; 128 and 256 run the per-token fp32 kernel
- * (any chunk length).
+ * runs the chunked MFMA kernel; 128 and 256 run the per-token fp32 kernel.
  */
 int frwkv_statetune_forward(int io_dtype, int decay_mode, int32_t num_sequences,
                             int32_t num_heads, int32_t head_size,
@@ -212,27 +219,52 @@ int frwkv_statetune_forward(int io_dtype, int decay_mode, int32_t num_sequences,
                             const void* decay_bias, const void* k,
                             const void* v, const void* a, const void* b,
                             void* output, float* boundary, float* state_dot_a,
-                            float scale, void* stream);
+                            float* interior, float scale, void* stream);
+
+/* Bytes of the interior-state buffer of frwkv_statetune_forward /
+ * frwkv_statetune_backward: ceil(total_tokens / P) x H x D x D fp32. */
+size_t frwkv_statetune_interior_bytes(int32_t head_size, int32_t num_heads,
+                                      int32_t total_tokens);
 
 /*
- * Training (StateTune) backward. Recomputes every chunk's forward quantities
- * from boundary (the state at each chunk start, as written by
- * frwkv_statetune_forward) and runs the chunked adjoint in reverse; it never
- * divides by the decay. Each chunk must span at most 64 tokens (the training
- * wrapper splits longer caller chunks and keeps their boundaries). grad_output
- * [total_tokens,H,D] (io dtype) and grad_final_state [B,H,D,D] fp32 may be
- * NULL (zero). Writes every token gradient (grad_decay is dL/d(decay input):
- * logits or retention per decay_mode) and grad_initial_state [B,H,D,D] fp32.
- * A chunk longer than 64 tokens, or whose decay span exceeds the kernels'
- * single-reference limit, makes its sequence's gradients NaN.
+ * The interior states of frwkv_statetune_forward, recomputed from the chunk
+ * start states boundary [num_chunks,H,D,D] (read only): for every chunk longer
+ * than the piece length P, the state at each of its interior piece starts
+ * goes to interior at slot (piece start) / P. Chunks of at most P tokens are
+ * skipped, and no output is written. No counterpart in the reference, whose
+ * backward rebuilds states by dividing by the decay; for callers of the
+ * backward that did not keep the forward's interior states.
+ */
+int frwkv_statetune_interior(int io_dtype, int decay_mode, int32_t num_heads,
+                             int32_t head_size, int32_t total_tokens,
+                             int32_t num_chunks, const int32_t* chunk_token_starts,
+                             const int32_t* chunk_token_ends, const float* boundary,
+                             const void* r, const void* decay, const void* decay_bias,
+                             const void* k, const void* v, const void* a,
+                             const void* b, float* interior, void* stream);
+
+/*
+ * Training (StateTune) backward. Recomputes every piece's forward quantities
+ * from its start state -- boundary (the state at each chunk start) for a
+ * chunk's first piece, interior for the others -- and runs the chunked
+ * adjoint in reverse; it never divides by the decay, and any chunk length
+ * and any retention are supported (pieces whose decay span exceeds the
+ * kernel's single-reference limit run as 16- and 4-token sub-pieces).
+ * interior: the forward's interior states, or NULL; then, with a workspace,
+ * the call first recomputes them into it (frwkv_statetune_interior), and
+ * without one every chunk must span at most P tokens (a longer one makes its
+ * sequence's gradients NaN). grad_output [total_tokens,H,D] (io dtype) and
+ * grad_final_state [B,H,D,D] fp32 may be NULL (zero). Writes every token
+ * gradient (grad_decay is dL/d(decay input): logits or retention per
+ * decay_mode) and grad_initial_state [B,H,D,D] fp32.
+ * workspace: frwkv_statetune_backward_workspace_bytes(head_size, H,
+ * total_tokens, interior != NULL) bytes of device memory, 256-byte aligned;
+ * it may be NULL when that is 0 (head sizes 64 and 128 with interior given).
  * Replaces statetune_recurrent_fp32io16_backward_cuda
  * (csrc/sm90/tmix/wkv7/statetune_recurrent_fp32io16_backward.cu:49-676;
  * binding statetune_recurrent_fp32io16_backward.cpp:34-82). head_size 64
- * runs the chunked MFMA kernel. head_size 128 and 256 run the per-token fp32
- * kernel, whose chunks must span at most 16 tokens (a longer one makes its
- * sequence's gradients NaN); at 256 the call takes 80 B per element of
- * [total_tokens,H,D] of fp32 gradient slices from hipMallocAsync on stream
- * and frees them on the same stream before it returns.
+ * runs the chunked MFMA kernel, 128 and 256 the per-token fp32 kernel (at 256
+ * with fp32 gradient slices in the workspace, added in a fixed order).
  */
 int frwkv_statetune_backward(int io_dtype, int decay_mode, int32_t num_sequences,
                              int32_t num_heads, int32_t head_size,
@@ -240,15 +272,19 @@ int frwkv_statetune_backward(int io_dtype, int decay_mode, int32_t num_sequences
                              const int32_t* sequence_chunk_offsets,
                              const int32_t* chunk_token_starts,
                              const int32_t* chunk_token_ends,
-                             const float* boundary, const void* r,
-                             const void* decay, const void* decay_bias,
+                             const float* boundary, const float* interior,
+                             const void* r, const void* decay, const void* decay_bias,
                              const void* k, const void* v, const void* a,
                              const void* b, const void* grad_output,
                              const float* grad_final_state, void* grad_r,
                              void* grad_decay, void* grad_k, void* grad_v,
                              void* grad_a, void* grad_b,
-                             float* grad_initial_state, float scale,
-                             void* stream);
+                             float* grad_initial_state, void* workspace,
+                             size_t workspace_bytes, float scale, void* stream);
+
+/* Workspace bytes of frwkv_statetune_backward (0: none needed). */
+size_t frwkv_statetune_backward_workspace_bytes(int32_t head_size, int32_t num_heads,
+                                                int32_t total_tokens, int interior_given);
 
 /*
  * Pretraining forward (clampw v3): dense tokens [B,T,H,D] (token t of
@@ -270,9 +306,11 @@ int frwkv_pretrain_forward(int io_dtype, int decay_mode, int32_t batch, int32_t 
 /*
  * Pretraining backward: recomputes every chunk from the boundary written by
  * frwkv_pretrain_forward (head size 64: 64-token chunks from every 4th entry;
- * 128 and 256: every 16-token entry, with the slice allocation described at
- * frwkv_statetune_backward for 256) and writes the six token gradients
- * (grad_decay is dL/d(decay input)). grad_output may not be NULL. Replaces rwkv7_clampw_v3::backward / cuda_backward_v3
+ * 128 and 256: every 16-token entry) and writes the six token gradients
+ * (grad_decay is dL/d(decay input)). grad_output may not be NULL. workspace:
+ * frwkv_pretrain_backward_workspace_bytes of device memory (head size 256:
+ * fp32 gradient slices; else 0, and workspace may be NULL).
+ * Replaces rwkv7_clampw_v3::backward / cuda_backward_v3
  * (csrc/sm90/tmix/wkv7/pretrain_recurrent_bf16_forward.cpp:31-53).
  */
 int frwkv_pretrain_backward(int io_dtype, int decay_mode, int32_t batch, int32_t tokens,
@@ -281,7 +319,11 @@ int frwkv_pretrain_backward(int io_dtype, int decay_mode, int32_t batch, int32_t
                             const void* a, const void* b, const void* grad_output,
                             const float* boundary, void* grad_r, void* grad_decay,
                             void* grad_k, void* grad_v, void* grad_a, void* grad_b,
-                            void* stream);
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of frwkv_pretrain_backward (0: none needed). */
+size_t frwkv_pretrain_backward_workspace_bytes(int32_t batch, int32_t tokens,
+                                               int32_t num_heads, int32_t head_size);
 
 /*
  * Replay stage of the RL/infctx chunk family: chunk c runs tokens

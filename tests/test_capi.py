@@ -150,3 +150,24 @@ def test_direct_entry_points_match_the_ops_without_a_gpu():
     # The public facade goes through the direct entry point.
     with pytest.raises(RuntimeError, match="must be CUDA"):
         _C.recurrent_fp32_from_decay_logits(*args[:10], 1.0)
+
+
+def test_library_imports_no_allocating_or_synchronizing_hip_call():
+    """The library's only HIP imports are kernel registration, launch and
+    error queries: no entry point allocates or frees device memory, copies,
+    sets memory or waits on the host (callers bring every buffer)."""
+    import shutil
+    import subprocess
+
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm is not installed")
+    out = subprocess.run([nm, "-D", "--undefined-only", str(LIB_PATH)], check=True,
+                         capture_output=True, text=True).stdout
+    imported = {line.split()[-1].split("@")[0] for line in out.splitlines()
+                if "hip" in line.lower()}
+    allowed = {"__hipPopCallConfiguration", "__hipPushCallConfiguration",
+               "__hipRegisterFatBinary", "__hipRegisterFunction", "__hipUnregisterFatBinary",
+               "__hipRegisterVar", "hipGetErrorString", "hipGetLastError", "hipLaunchKernel"}
+    assert imported <= allowed, sorted(imported - allowed)
+    assert "hipLaunchKernel" in imported

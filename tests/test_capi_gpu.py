@@ -111,8 +111,12 @@ def test_invalid_metadata_status_gives_nan_and_keeps_pool():
 
 
 def test_statetune_forward_and_backward():
-    lengths = (70, 9)
-    meta = oracle.chunk_metadata(lengths, 64)
+    """frwkv_statetune_forward/backward with caller chunks of 100 tokens (two
+    64-token pieces): the forward fills the interior buffer the backward
+    reads; a second backward without it recomputes the interior states into
+    its workspace and must give the same gradients bit for bit."""
+    lengths = (170, 9)
+    meta = oracle.chunk_metadata(lengths, 100)
     case = workloads.make_case(lengths=lengths, heads=2, head_size=64, dtype=torch.bfloat16,
                                seed=53, state_std=0.1)
     offsets, starts, ends = (torch.from_numpy(x).to(DEV) for x in meta[:3])
@@ -124,18 +128,27 @@ def test_statetune_forward_and_backward():
     out = torch.empty_like(toks[3])
     boundary = torch.empty((starts.numel(), heads, 64, 64), device=DEV)
     sda = torch.empty((n_tok, heads, 64), device=DEV)
+    inner_bytes = capi.statetune_interior_bytes(64, heads, n_tok)
+    assert inner_bytes == ((n_tok + 63) // 64) * heads * 64 * 64 * 4
+    interior = torch.empty(inner_bytes // 4, device=DEV)
     capi.statetune_forward(*toks, sequence_chunk_offsets=offsets, chunk_token_starts=starts,
                            chunk_token_ends=ends, state=state, output=out, boundary=boundary,
-                           state_dot_a=sda, scale=0.5)
+                           state_dot_a=sda, interior=interior, scale=0.5)
     gen = torch.Generator().manual_seed(54)
     dy = torch.randn((n_tok, heads, 64), generator=gen).to(torch.bfloat16)
     ds = torch.randn((batch, heads, 64, 64), generator=gen) * 0.01
-    grads = [torch.empty_like(t) for t in toks]
-    ds0 = torch.empty((batch, heads, 64, 64), device=DEV)
-    capi.statetune_backward(*toks, sequence_chunk_offsets=offsets, chunk_token_starts=starts,
-                            chunk_token_ends=ends, boundary=boundary,
-                            grad_output=dy.to(DEV), grad_final_state=ds.to(DEV), grads=grads,
-                            grad_initial_state=ds0, scale=0.5)
+    assert capi.statetune_backward_workspace_bytes(64, heads, n_tok, True) == 0
+    assert capi.statetune_backward_workspace_bytes(64, heads, n_tok, False) == inner_bytes
+    runs = []
+    for inner in (interior, None):
+        grads = [torch.empty_like(t) for t in toks]
+        ds0 = torch.empty((batch, heads, 64, 64), device=DEV)
+        capi.statetune_backward(*toks, sequence_chunk_offsets=offsets,
+                                chunk_token_starts=starts, chunk_token_ends=ends,
+                                boundary=boundary, grad_output=dy.to(DEV),
+                                grad_final_state=ds.to(DEV), grads=grads,
+                                grad_initial_state=ds0, interior=inner, scale=0.5)
+        runs.append((grads, ds0))
     torch.cuda.synchronize()
     args = [_np(case[n]) for n in NAMES]
     kw = dict(seg_offsets=meta[0], seg_starts=meta[1], seg_ends=meta[2],
@@ -147,6 +160,31 @@ def test_statetune_forward_and_backward():
     _check("final state", state, st, 2e-2)
     _check("boundary", boundary, bnd, 2e-2)
     _check("state_dot_a", sda, ref_sda, 2e-2)
+    grads, ds0 = runs[0]
     for name, g in zip(NAMES, grads):
         _check(f"d{name}", g, ref["d" + name], 2e-2)
     _check("dS0", ds0, ref["dstate0"], 2e-2)
+    for name, x, y2 in zip((*NAMES, "s0"), (*runs[0][0], runs[0][1]),
+                           (*runs[1][0], runs[1][1])):
+        assert torch.equal(x, y2), name
+
+
+def test_statetune_backward_rejects_short_workspace():
+    """Without interior states and with a workspace below the stated size
+    the backward returns an argument error before launching anything."""
+    lengths = (130,)
+    meta = oracle.chunk_metadata(lengths, 130)
+    case = workloads.make_case(lengths=lengths, heads=1, head_size=128,
+                               dtype=torch.bfloat16, seed=3, state_std=0.1)
+    offsets, starts, ends = (torch.from_numpy(x).to(DEV) for x in meta[:3])
+    toks = [case[n].to(DEV) for n in NAMES]
+    need = capi.statetune_backward_workspace_bytes(128, 1, 130, False)
+    assert need == ((130 + 15) // 16) * 128 * 128 * 4
+    grads = [torch.empty_like(t) for t in toks]
+    with pytest.raises(RuntimeError, match="workspace of 256 bytes given"):
+        capi.statetune_backward(*toks, sequence_chunk_offsets=offsets,
+                                chunk_token_starts=starts, chunk_token_ends=ends,
+                                boundary=torch.zeros((1, 1, 128, 128), device=DEV),
+                                grad_output=None, grad_final_state=None, grads=grads,
+                                grad_initial_state=torch.empty((1, 1, 128, 128), device=DEV),
+                                work=torch.empty(256, dtype=torch.uint8, device=DEV))

@@ -248,7 +248,7 @@ def test_statetune_forward_matches_oracle_boundaries_and_state_dot_a():
     meta = [torch.from_numpy(x).to(DEV) for x in (offsets, starts, ends)]
     flashrwkv_amd._C.statetune_forward_internal(
         *meta, state, d["r"], d["w"], d["k"], d["v"], d["a"], d["b"], y, boundary, sda,
-        0.5, DECAY_RAW_W)
+        None, 0.5, DECAY_RAW_W)
     torch.cuda.synchronize()
     y_ref, s_ref, b_ref, sda_ref = oracle.forward(
         *(_np(case[n]) for n in ("r", "w", "k", "v", "a", "b")), _np(case["state_pool"]),
