@@ -35,6 +35,7 @@ SIGNATURES = {
     "frwkv_statetune_interior": [_INT] * 2 + [_I32] * 4 + [_VP] * 11 + [_VP],
     "frwkv_statetune_backward": [_INT] * 2 + [_I32] * 5 + [_VP] * 22 + [_SZ, _F32, _VP],
     "frwkv_statetune_backward_workspace_bytes": [_I32] * 3 + [_INT],
+    "frwkv_statetune_backward_noalloc": [_INT] * 2 + [_I32] * 5 + [_VP] * 21 + [_F32, _VP],
     "frwkv_pretrain_forward": [_INT] * 2 + [_I32] * 4 + [_VP] * 10,
     "frwkv_pretrain_backward": [_INT] * 2 + [_I32] * 4 + [_VP] * 15 + [_SZ, _VP],
     "frwkv_pretrain_backward_workspace_bytes": [_I32] * 4,
@@ -160,6 +161,24 @@ def statetune_backward(r, decay, k, v, a, b, *, sequence_chunk_offsets, chunk_to
         _p(k), _p(v), _p(a), _p(b), _p(grad_output), _p(grad_final_state),
         *(_p(g) for g in grads), _p(grad_initial_state), _p(work),
         0 if work is None else work.numel(), float(scale), _stream()))
+
+
+NOALLOC_SCRATCH_BYTES = 64 << 20  # FRWKV_NOALLOC_SCRATCH_BYTES
+
+
+def statetune_backward_noalloc(r, decay, k, v, a, b, *, sequence_chunk_offsets,
+                               chunk_token_starts, chunk_token_ends, boundary, grad_output,
+                               grad_final_state, grads, grad_initial_state, interior=None,
+                               scale=1.0, decay_mode=DECAY_RAW_W, decay_bias=None):
+    """frwkv_statetune_backward_noalloc: the workspace is the library's static
+    per-device scratch; nothing is allocated."""
+    n, h, d = r.shape
+    _check(library().frwkv_statetune_backward_noalloc(
+        DTYPE[r.dtype], decay_mode, sequence_chunk_offsets.numel() - 1, h, d, n,
+        chunk_token_starts.numel(), _p(sequence_chunk_offsets), _p(chunk_token_starts),
+        _p(chunk_token_ends), _p(boundary), _p(interior), _p(r), _p(decay), _p(decay_bias),
+        _p(k), _p(v), _p(a), _p(b), _p(grad_output), _p(grad_final_state),
+        *(_p(g) for g in grads), _p(grad_initial_state), float(scale), _stream()))
 
 
 def pretrain_forward(r, decay, k, v, a, b, *, output, boundary, state_dot_a,

@@ -286,6 +286,41 @@ int frwkv_statetune_backward(int io_dtype, int decay_mode, int32_t num_sequences
 size_t frwkv_statetune_backward_workspace_bytes(int32_t head_size, int32_t num_heads,
                                                 int32_t total_tokens, int interior_given);
 
+/* Size of the per-device static scratch of frwkv_statetune_backward_noalloc. */
+#define FRWKV_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/*
+ * frwkv_statetune_backward without the workspace argument: the workspace
+ * (frwkv_statetune_backward_workspace_bytes(head_size, H, total_tokens,
+ * interior != NULL) bytes) lives in a static device array of
+ * FRWKV_NOALLOC_SCRATCH_BYTES (64 MiB) that each device holds from the
+ * library's first use on it until the process ends; larger needs are
+ * rejected with FRWKV_ERR_INVALID_ARGUMENT before anything runs. The call
+ * allocates and frees nothing. Every call on one device shares that device's
+ * array: calls that overlap on one device (other streams, other threads)
+ * race and must be serialised by the caller. Outputs and every other
+ * argument as frwkv_statetune_backward (the same kernels run).
+ * No counterpart in the reference; for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving or training loops,
+ * harnesses that forbid hipMalloc).
+ */
+int frwkv_statetune_backward_noalloc(int io_dtype, int decay_mode, int32_t num_sequences,
+                                     int32_t num_heads, int32_t head_size,
+                                     int32_t total_tokens, int32_t num_chunks,
+                                     const int32_t* sequence_chunk_offsets,
+                                     const int32_t* chunk_token_starts,
+                                     const int32_t* chunk_token_ends,
+                                     const float* boundary, const float* interior,
+                                     const void* r, const void* decay,
+                                     const void* decay_bias, const void* k,
+                                     const void* v, const void* a, const void* b,
+                                     const void* grad_output,
+                                     const float* grad_final_state, void* grad_r,
+                                     void* grad_decay, void* grad_k, void* grad_v,
+                                     void* grad_a, void* grad_b,
+                                     float* grad_initial_state, float scale,
+                                     void* stream);
+
 /*
  * Pretraining forward (clampw v3): dense tokens [B,T,H,D] (token t of
  * sequence s at row s*T + t), S0 = 0, no final state. boundary

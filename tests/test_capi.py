@@ -168,6 +168,25 @@ def test_library_imports_no_allocating_or_synchronizing_hip_call():
                 if "hip" in line.lower()}
     allowed = {"__hipPopCallConfiguration", "__hipPushCallConfiguration",
                "__hipRegisterFatBinary", "__hipRegisterFunction", "__hipUnregisterFatBinary",
-               "__hipRegisterVar", "hipGetErrorString", "hipGetLastError", "hipLaunchKernel"}
+               "__hipRegisterVar", "__hipRegisterManagedVar", "hipGetErrorString",
+               "hipGetLastError", "hipLaunchKernel",
+               # the static scratch of the allocation-free backward variant
+               "hipGetDevice", "hipGetSymbolAddress"}
     assert imported <= allowed, sorted(imported - allowed)
     assert "hipLaunchKernel" in imported
+
+
+def test_noalloc_backward_rejects_oversized_need_without_a_gpu():
+    """frwkv_statetune_backward_noalloc compares the workspace it needs with
+    its static scratch before anything else: head size 256 with 4096 tokens
+    is refused with an argument error (the placeholder pointers are never
+    used)."""
+    from flashrwkv_amd import capi
+
+    lib = capi.library()
+    fake = ctypes.c_void_p(256)
+    need = capi.statetune_backward_workspace_bytes(256, 1, 4096, False)
+    assert need > capi.NOALLOC_SCRATCH_BYTES
+    rc = lib.frwkv_statetune_backward_noalloc(2, 1, 1, 1, 256, 4096, 1, *([fake] * 21), 1.0,
+                                              None)
+    assert rc == 1 and b"bytes of scratch" in lib.frwkv_last_error()
