@@ -134,6 +134,59 @@ def cpu_baseline_decode(batch, heads, seconds):
     }
 
 
+def cpu_baseline_torch(lengths, heads, seconds, *, seed=97, u_low=-5.0, heads_total=None,
+                       backward=False):
+    """The torch fp32 restatement of the naive recurrence (oracle.forward_torch)
+    on the host CPU, timed once with every available core and once with
+    torch.set_num_threads(1): 1 warm-up, then repeats until ``seconds`` pass
+    (at least 3). tokens/s counts token-heads / heads_total (heads are
+    independent, so a head sample scales exactly). ``backward``: each repeat
+    also runs torch autograd back to every input and S0 (dy ~ N(0,1))."""
+    import torch
+
+    from flashrwkv_amd import workloads
+    from oracle import oracle
+
+    cores = len(os.sched_getaffinity(0))
+    heads_total = heads if heads_total is None else heads_total
+    case = workloads.make_case(lengths=lengths, heads=heads, head_size=64,
+                               dtype=torch.bfloat16, seed=seed, state_std=0.1, u_low=u_low)
+    args = [case[n].float().requires_grad_(backward) for n in ("r", "w", "k", "v", "a", "b")]
+    pool = case["state_pool"].float().requires_grad_(backward)
+    cu, slots = case["cu_seqlens"].numpy(), case["state_indices"].numpy()
+    tokens = sum(lengths)
+    dy = torch.randn(args[0].shape, generator=torch.Generator().manual_seed(seed))
+    before = torch.get_num_threads()
+    out = {"kind": "port", "unit": "train tokens/s" if backward else "tokens/s",
+           "cpu_count": os.cpu_count(), "affinity_cores": cores,
+           "sample": f"oracle.forward_torch (torch fp32, per token"
+                     f"{', + autograd backward' if backward else ''}) on {len(lengths)} "
+                     f"sequence(s) x {heads} heads, {tokens} tokens per repeat"}
+
+    def once():
+        y, _ = oracle.forward_torch(*args, pool, cu, slots)
+        if backward:
+            y.backward(dy)
+
+    try:
+        for label, threads in (("all_cores", cores), ("one_thread", 1)):
+            torch.set_num_threads(threads)
+            once()
+            reps, t0 = 0, time.perf_counter()
+            while True:
+                once()
+                reps += 1
+                elapsed = time.perf_counter() - t0
+                if reps >= 3 and elapsed >= seconds:
+                    break
+            out[label] = {"value": round(reps * tokens * heads / heads_total / elapsed, 1),
+                          "threads": torch.get_num_threads(),
+                          "wall_s": round(elapsed, 2), "repeats": reps}
+    finally:
+        torch.set_num_threads(before)
+    return out
+
+
 def cpu_baseline_gate(cores):
     """The reference bench's correctness gate (benchmarks/tmix/wkv7/bench.py:374-501),
     run beside the CPU baseline with the same fp64 oracle as the checker.
@@ -358,6 +411,8 @@ def bench_decode(args, fp16_state=False):
     }
     if args.cpu_seconds > 0:
         line["cpu_baseline"] = cpu_baseline_decode(batch, heads, args.cpu_seconds)
+        line["cpu_baseline"]["torch_fp32"] = cpu_baseline_torch(
+            [1] * batch, heads, args.cpu_seconds / 2)
         line["gate"] = cpu_baseline_gate(line["cpu_baseline"]["cores"])
     return line
 
@@ -614,6 +669,8 @@ def bench_prefill(args):
     }
     if args.cpu_seconds > 0:
         out["cpu_baseline"] = cpu_baseline_prefill(t_len, heads, args.cpu_seconds)
+        out["cpu_baseline"]["torch_fp32"] = cpu_baseline_torch(
+            [t_len], 8, args.cpu_seconds / 2, seed=98, u_low=-8.0, heads_total=heads)
     return out
 
 
@@ -788,6 +845,8 @@ def bench_training(args):
     }
     if args.cpu_seconds > 0:
         out["cpu_baseline"] = cpu_baseline_training(t_len, heads, args.cpu_seconds)
+        out["cpu_baseline"]["torch_fp32"] = cpu_baseline_torch(
+            [t_len], 4, args.cpu_seconds / 2, heads_total=heads, backward=True)
     return out
 
 

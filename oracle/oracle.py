@@ -11,6 +11,8 @@ Two independent restatements of the reference's naive recurrence
   loops in ``wkv7_oracle.c``), fast enough for full-length sampled heads.
 * :func:`forward_einsum` is a numpy einsum restatement (per token, vectorised
   over heads), used to cross-check the C loops.
+* :func:`forward_torch` is the same recurrence in torch fp32 on the CPU,
+  timed as the bench's torch CPU baseline.
 
 Decay transform: :func:`retention_from_logits` restates
 ``csrc/sm120/tmix/wkv7/recurrent_decay.cuh:18-22`` (``exp(-e^{-1/2} sigmoid(x))``);
@@ -24,7 +26,8 @@ How each function is pinned (see ``tests/test_oracle.py``):
   linear attention closed form, the w=1, a=b=0 matmul form
   ``Y = scale * tril(R K^T) V``, the k=0 explicit transition product, joint
   linearity in (v, S0), permutation invariance of packed sequences, and
-  agreement of the two independent restatements.
+  agreement of the two independent restatements; ``forward_torch`` agrees
+  with ``forward`` to fp32 rounding on equal-length and ragged batches.
 * ``backward``: torch fp64 autograd through an independent per-token torch
   forward (itself checked against ``forward``), and central finite
   differences at D=4.
@@ -271,6 +274,48 @@ def forward_einsum(r, w, k, v, a, b, state_pool, cu_seqlens, state_indices,
             s = w[t][:, :, None] * s + b[t][:, :, None] * sa[:, None, :] \
                 + k[t][:, :, None] * v[t][:, None, :]
             y[t] = scale * np.einsum("hk,hkv->hv", r[t], s)
+        pool[slots[seq]] = s
+    return y, pool
+
+
+def forward_torch(r, w, k, v, a, b, state_pool, cu_seqlens, state_indices, scale=1.0):
+    """torch fp32 restatement of test.py:157-213 on the CPU, per token.
+
+    The CPU baseline's "torch" leg (not a checker): the naive recurrence in
+    torch's own fp32 CPU kernels, as the reference's test runs it. Packed
+    sequences of one common length advance together (one batched matmul per
+    token over all sequences and heads); otherwise each sequence is stepped
+    on its own. Returns (y [N,H,D], updated pool), both fp32 torch tensors.
+    """
+    import torch
+
+    r, w, k, v, a, b = (torch.as_tensor(t).float() for t in (r, w, k, v, a, b))
+    pool = torch.as_tensor(state_pool).float().clone()
+    cu = [int(x) for x in np.asarray(cu_seqlens)]
+    slots = torch.as_tensor(np.asarray(state_indices), dtype=torch.long)
+    lengths = {e - s for s, e in zip(cu[:-1], cu[1:])}
+    y = torch.empty_like(r)
+    if len(lengths) == 1:
+        t_len = lengths.pop()
+        n_seq = len(cu) - 1
+        view = [t.view(n_seq, t_len, *t.shape[1:]) for t in (r, w, k, v, a, b)]
+        rr, ww, kk, vv, aa, bb = view
+        yy = y.view(n_seq, t_len, *y.shape[1:])
+        s = pool[slots]
+        for t in range(t_len):
+            sa = torch.matmul(aa[:, t].unsqueeze(-2), s)                  # [B,H,1,D]
+            s = ww[:, t].unsqueeze(-1) * s + bb[:, t].unsqueeze(-1) * sa \
+                + kk[:, t].unsqueeze(-1) * vv[:, t].unsqueeze(-2)
+            yy[:, t] = scale * torch.matmul(rr[:, t].unsqueeze(-2), s).squeeze(-2)
+        pool[slots] = s
+        return y, pool
+    for seq, (start, end) in enumerate(zip(cu[:-1], cu[1:])):
+        s = pool[slots[seq]]
+        for t in range(start, end):
+            sa = torch.matmul(a[t].unsqueeze(-2), s)
+            s = w[t].unsqueeze(-1) * s + b[t].unsqueeze(-1) * sa \
+                + k[t].unsqueeze(-1) * v[t].unsqueeze(-2)
+            y[t] = scale * torch.matmul(r[t].unsqueeze(-2), s).squeeze(-2)
         pool[slots[seq]] = s
     return y, pool
 

@@ -179,6 +179,19 @@ def test_c_loops_match_independent_einsum_restatement():
     np.testing.assert_allclose(s1, s2, rtol=1e-11, atol=1e-12)
 
 
+@pytest.mark.parametrize("lengths", ([1, 15, 16, 17, 65], [24, 24, 24]))
+def test_torch_fp32_baseline_matches_c_loops(lengths):
+    """The torch fp32 CPU baseline computes the pinned recurrence (ragged
+    batches per sequence, equal lengths batched) to fp32 rounding."""
+    (r, w, k, v, a, b), cu, _, _ = _single(lengths, h=2, d=16)
+    pool = RNG.standard_normal((9, 2, 16, 16)) * 0.03
+    slots = np.array([5, 0, 7, 2, 4][:len(lengths)], dtype=np.int32)
+    y1, s1 = oracle.forward_varlen(r, w, k, v, a, b, pool, cu, slots, 0.9)
+    y2, s2 = oracle.forward_torch(r, w, k, v, a, b, pool, cu, slots, 0.9)
+    assert oracle.max_rel_error(y2.double().numpy(), y1) < 1e-5
+    assert oracle.max_rel_error(s2.double().numpy(), s1) < 1e-5
+
+
 def test_segmentation_invariance_and_boundaries():
     lengths = [37, 9]
     (r, w, k, v, a, b), _, _, _ = _single(lengths, h=2, d=8)
