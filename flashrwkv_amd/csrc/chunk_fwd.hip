@@ -333,8 +333,8 @@ __device__ __forceinline__ void intra_chunk(ChunkSmem& sm, Issue&& issue) {
   const int g = lane >> 4;
   const int n = lane & 15;
 
-  auto store = [&](int m, int p, int q, f32x4 acc, bool strict) {
-    if (p == q) {
+  auto store = [&](int m, int p, int q, f32x4 acc, bool strict, bool diag) {
+    if (diag) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int i = 4 * g + j;
@@ -345,7 +345,7 @@ __device__ __forceinline__ void intra_chunk(ChunkSmem& sm, Issue&& issue) {
     lds_store_transposed(sm.tri[m] + tri_index(p, q) * kTriBlock, kTriStride, g, n, acc);
   };
 
-  auto group = [&](int p, int q, bool with_b, bool with_k) {
+  auto group = [&](int p, int q, bool with_b, bool with_k, bool diag) {
     f32x4 lab = zero4(), lak = zero4(), arb = zero4(), ark = zero4();
 #pragma unroll
     for (int c = 0; c < 64; c += 32) {
@@ -363,19 +363,19 @@ __device__ __forceinline__ void intra_chunk(ChunkSmem& sm, Issue&& issue) {
       }
     }
     if (with_b) {
-      store(kLab, p, q, lab, true);
-      store(kArb, p, q, arb, false);
+      store(kLab, p, q, lab, true, diag);
+      store(kArb, p, q, arb, false, diag);
     }
     if (with_k) {
-      store(kLak, p, q, lak, true);
-      store(kArk, p, q, ark, false);
+      store(kLak, p, q, lak, true, diag);
+      store(kArk, p, q, ark, false, diag);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
 
   // Diagonal pair first; its Lab block feeds the inverse.
   issue(0);
-  group(wave, wave, true, true);
+  group(wave, wave, true, true, true);
   issue(1);
   // T_pp = (I - L)^{-1} for the strictly lower 16 x 16 block L = Lab_pp:
   // L^16 = 0, so (I - L)^{-1} = (I + L)(I + L^2)(I + L^4)(I + L^8). All
@@ -421,7 +421,7 @@ __device__ __forceinline__ void intra_chunk(ChunkSmem& sm, Issue&& issue) {
     const int pair = item >> 1;
     const int p = pair < 1 ? 1 : (pair < 3 ? 2 : 3);
     const int q = pair - (p * (p - 1)) / 2;
-    group(p, q, (item & 1) == 0, (item & 1) == 1);
+    group(p, q, (item & 1) == 0, (item & 1) == 1, false);
     issue(3 + r);
   }
   __builtin_amdgcn_s_setprio(0);

@@ -53,6 +53,7 @@ struct StateTraits<StateKind::kFp16> {
 };
 
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Four consecutive state columns, streamed (each state slab moves once).
 template <StateKind SK>
@@ -392,6 +393,149 @@ int launch_recurrent(const RecurrentArgs& p) {
   return check_launch("recurrent_fp32_kernel");
 }
 
+// fp16-state decode shape (head size 64, one wave per state, a few tokens
+// per sequence). Lane (rg, cg) = (lane / 8, lane % 8) holds key rows
+// 8 rg .. 8 rg + 7 of value columns 8 cg .. 8 cg + 7: every state access is
+// 16 bytes per lane (8 fp16), and the 8 lanes of a row group cover one whole
+// 128-byte state row per load instruction. Token rows are 16-byte loads too
+// (the lane's 8 key features, or its 8 value columns). Sums over key rows
+// add the lane's 8 rows, then the 8 row groups held in lane bits 3..5
+// (row_ror 8 inside a DPP row, then the 16- and 32-lane swaps); each step
+// adds a lane pair symmetrically, so every lane of a column ends with the
+// same bits. Same arithmetic and rounding points as recurrent_fp32_kernel's
+// fp16-state path.
+__device__ __forceinline__ float sum_row_groups8(float x) {
+  x += dpp_read<0x128>(x);  // row_ror 8: lane ^ 8 inside the 16-lane row
+  return add_xor32(add_xor16(x));
+}
+
+__device__ __forceinline__ void unpack_f16x8(uint4 q, float (&x)[8]) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = f16_to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
+    x[2 * i + 1] = f16_to_f32(static_cast<uint16_t>(w[i] >> 16));
+  }
+}
+
+__device__ __forceinline__ uint4 load_x8(const uint16_t* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+
+__global__ __launch_bounds__(64) void recurrent_fp16_decode_kernel(
+    RecurrentKernelParams p, const uint16_t* __restrict__ r_ptr,
+    const uint16_t* __restrict__ decay_ptr, const uint16_t* __restrict__ bias_ptr,
+    const uint16_t* __restrict__ k_ptr, const uint16_t* __restrict__ v_ptr,
+    const uint16_t* __restrict__ a_ptr, const uint16_t* __restrict__ b_ptr,
+    uint16_t* __restrict__ out_ptr) {
+  constexpr int D = 64;
+  if (p.status != nullptr && p.status[0] != 0) {
+    fill_nan<F16>(out_ptr, p.output_elements);
+    return;
+  }
+  const int unit = blockIdx.x;
+  if (unit >= p.num_units) return;
+  const int lane = threadIdx.x & 63;
+  const int num_heads = p.num_heads;
+  const int seq = unit / num_heads;
+  const int head = unit % num_heads;
+  const int rg = lane >> 3, cg = lane & 7;
+  const int row0 = 8 * rg, col = 8 * cg;
+  const int32_t t_begin = __builtin_amdgcn_readfirstlane(p.cu_seqlens[seq]);
+  const int32_t t_end = __builtin_amdgcn_readfirstlane(p.cu_seqlens[seq + 1]);
+  const int32_t slot = __builtin_amdgcn_readfirstlane(p.slots[seq]);
+  if (t_begin < 0 || t_end > p.total_tokens || t_begin >= t_end || slot < 0 ||
+      slot >= p.state_pool_size) {
+    return;
+  }
+  uint16_t* sbase = static_cast<uint16_t*>(p.state) +
+                    ((static_cast<int64_t>(slot) * num_heads + head) * D) * D;
+  float s[8][8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const u32x4 q = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4*>(sbase + (row0 + j) * D + col));
+    unpack_f16x8(make_uint4(q.x, q.y, q.z, q.w), s[j]);
+  }
+  float bias[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (bias_ptr != nullptr) unpack_f16x8(load_x8(bias_ptr + head * D + row0), bias);
+  const uint32_t phase0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(p.elapsed[slot])) +
+                          static_cast<uint32_t>(head * D + row0) - static_cast<uint32_t>(t_begin);
+
+  for (int32_t t = t_begin; t < t_end; ++t) {
+    const int64_t base = (static_cast<int64_t>(t) * num_heads + head) * D;
+    float aa[8], xx[8], bb[8], kk[8], rr[8], vv[8];
+    unpack_f16x8(load_x8(a_ptr + base + row0), aa);
+    unpack_f16x8(load_x8(decay_ptr + base + row0), xx);
+    unpack_f16x8(load_x8(b_ptr + base + row0), bb);
+    unpack_f16x8(load_x8(k_ptr + base + row0), kk);
+    unpack_f16x8(load_x8(r_ptr + base + row0), rr);
+    unpack_f16x8(load_x8(v_ptr + base + col), vv);
+    float sa[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc = fmaf(aa[j], s[j][c], acc);
+      sa[c] = sum_row_groups8(acc);
+    }
+    float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float w = decay_retention<DecayMode::kLogits>(xx[j] + bias[j]);
+      const float delta =
+          round_f16(w - 1.0f + phase_dither(phase0 + static_cast<uint32_t>(j + t)));
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        s[j][c] = round_f16(fmaf(kk[j], vv[c], fmaf(bb[j], sa[c], fmaf(s[j][c], delta, s[j][c]))));
+        y[c] = fmaf(rr[j], s[j][c], y[c]);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) y[c] = sum_row_groups8(y[c]);
+    if (rg == 0) {
+      u32x4 q;
+      q.x = pack2<F16>(p.scale * y[0], p.scale * y[1]);
+      q.y = pack2<F16>(p.scale * y[2], p.scale * y[3]);
+      q.z = pack2<F16>(p.scale * y[4], p.scale * y[5]);
+      q.w = pack2<F16>(p.scale * y[6], p.scale * y[7]);
+      *reinterpret_cast<u32x4*>(out_ptr + base + col) = q;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    u32x4 q;
+    q.x = pack2<F16>(s[j][0], s[j][1]);
+    q.y = pack2<F16>(s[j][2], s[j][3]);
+    q.z = pack2<F16>(s[j][4], s[j][5]);
+    q.w = pack2<F16>(s[j][6], s[j][7]);
+    __builtin_nontemporal_store(q, reinterpret_cast<u32x4*>(sbase + (row0 + j) * D + col));
+  }
+}
+
+int launch_fp16_decode(const RecurrentArgs& p) {
+  const int units = p.num_sequences * p.num_heads;
+  RecurrentKernelParams kp{};
+  kp.num_heads = p.num_heads;
+  kp.num_units = units;
+  kp.output_elements = static_cast<int64_t>(p.total_tokens) * p.num_heads * 64;
+  kp.total_tokens = p.total_tokens;
+  kp.state_pool_size = p.state_pool_size;
+  kp.cu_seqlens = p.cu;
+  kp.slots = p.slots;
+  kp.status = p.status;
+  kp.elapsed = p.elapsed;
+  kp.state = p.state;
+  kp.scale = p.scale;
+  using S = uint16_t;
+  hipLaunchKernelGGL(recurrent_fp16_decode_kernel, dim3(units), dim3(64), 0, p.stream, kp,
+                     static_cast<const S*>(p.r), static_cast<const S*>(p.decay),
+                     static_cast<const S*>(p.bias), static_cast<const S*>(p.k),
+                     static_cast<const S*>(p.v), static_cast<const S*>(p.a),
+                     static_cast<const S*>(p.b), static_cast<S*>(p.out));
+  return check_launch("recurrent_fp16_decode_kernel");
+}
+
 template <typename T, DecayMode M, StateKind SK = StateKind::kFp32>
 int dispatch_head_size(const RecurrentArgs& p) {
   switch (p.head_size) {
@@ -399,6 +543,7 @@ int dispatch_head_size(const RecurrentArgs& p) {
       // Decode keeps one wave per state (fewest redundant decay evaluations);
       // longer sequences split the state over 4 waves for more parallelism.
       if (p.max_seqlen > 0 && p.max_seqlen <= 2) {
+        if constexpr (SK == StateKind::kFp16) return launch_fp16_decode(p);
         return launch_recurrent<64, 64, 64, T, M, SK>(p);
       }
       return launch_recurrent<64, 16, 256, T, M, SK>(p);
