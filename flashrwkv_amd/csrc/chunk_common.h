@@ -13,6 +13,7 @@ constexpr int kChunk = 64;
 constexpr int kHead = 64;
 constexpr int kChunkThreads = 256;
 constexpr float kSpanLimit = 80.0f;   // log2 units
+constexpr float kSpanFloor = 0x1p-80f; // 2^-kSpanLimit: the same limit as a decay product
 constexpr float kLog2Min = -20.0f;    // per-token clamp of log2 retention
 
 // Operand tiles: 64 rows x 64 bf16, row stride 68 elements (136 B = 34
@@ -85,6 +86,17 @@ __device__ __forceinline__ float log2_retention(float x) {
   return __builtin_amdgcn_fmed3f(lg, kLog2Min, 0.0f);
 }
 
+// The retention itself, clamped to [2^kLog2Min, 1] as log2_retention is:
+// raw mode clamps the input, logits mode is 2^(log2 w).
+template <DecayMode M>
+__device__ __forceinline__ float clamped_retention(float x) {
+  if constexpr (M == DecayMode::kLogits) {
+    return __builtin_amdgcn_exp2f(log2_retention<M>(x));
+  } else {
+    return __builtin_amdgcn_fmed3f(x, 0x1p-20f, 1.0f);
+  }
+}
+
 // 8 floats -> 8 bf16 at an 8-byte aligned LDS address (two 8-byte writes).
 __device__ __forceinline__ void store8_bf16(uint16_t* dst, const float (&x)[8]) {
   uint2 lo, hi;
@@ -103,6 +115,22 @@ __device__ __forceinline__ float scan8_step(float x, int tp) {
   const float y = __int_as_float(
       __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x110 + N, 0xf, 0xf, true));
   return tp >= N ? x + y : x;
+}
+
+// The same scan with products (lanes l % 8 < N keep x).
+template <int N>
+__device__ __forceinline__ float scan8_mul(float x, int tp) {
+  const float y = __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x110 + N, 0xf, 0xf, true));
+  return tp >= N ? x * y : x;
+}
+
+// Exclusive product scan from an inclusive one: lane l takes lane l - 1's
+// value, and the first lane of each 8-lane group the empty product 1.
+__device__ __forceinline__ float scan8_exclusive(float incl, int tp) {
+  const float y = __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(incl), 0x111, 0xf, 0xf, true));
+  return tp >= 1 ? y : 1.0f;
 }
 
 }  // namespace frwkv

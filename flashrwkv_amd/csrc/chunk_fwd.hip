@@ -173,9 +173,9 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
 
   __syncthreads();  // earlier readers of the tiles are done
 
-  // log2 retention and the retention itself; tokens outside [lo, hi) get
-  // lg = 0, w = 1 (no decay, and their operand rows are zero below).
-  float lg0[8], lg1[8], w0[8], w1[8];
+  // Retentions; tokens outside [lo, hi) get w = 1 (no decay, and their operand
+  // rows are zero below).
+  float w0[8], w1[8];
   {
     float x0[8], x1[8];
     unpack8<T>(rows.w[0], x0);
@@ -186,30 +186,26 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
         x0[e] += bias[e];
         x1[e] += bias[e];
       }
-      const float l0 = log2_retention<M>(x0[e]);
-      const float l1 = log2_retention<M>(x1[e]);
-      lg0[e] = on0 ? l0 : 0.0f;
-      lg1[e] = on1 ? l1 : 0.0f;
-      if constexpr (M == DecayMode::kRawW) {
-        // 2^lg is the input clamped to [2^-20, 1] (log2_retention's clamp).
-        w0[e] = on0 ? __builtin_amdgcn_fmed3f(x0[e], 0x1p-20f, 1.0f) : 1.0f;
-        w1[e] = on1 ? __builtin_amdgcn_fmed3f(x1[e], 0x1p-20f, 1.0f) : 1.0f;
-      } else {
-        w0[e] = fast_exp2(lg0[e]);
-        w1[e] = fast_exp2(lg1[e]);
-      }
+      const float r0 = clamped_retention<M>(x0[e]);
+      const float r1 = clamped_retention<M>(x1[e]);
+      w0[e] = on0 ? r0 : 1.0f;
+      w1[e] = on1 ? r1 : 1.0f;
     }
   }
 
-  // Inclusive scan over the wave's 8 token pairs (the 8 lanes of a feature
-  // group), then the carry of earlier waves through LDS.
+  // The cumulative decay as products, 2^G(t) = prod_{j<=t} w_j: an inclusive
+  // product scan over the wave's 8 token pairs (the 8 lanes of a feature
+  // group), then the carry of earlier waves through LDS. Every product that
+  // reaches an operand has a span within the limit, so it stays a normal
+  // fp32 number (>= 2^-80); a pass whose span exceeds the limit is
+  // discarded and redone as sub-chunks.
   float incl[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    float x = lg0[e] + lg1[e];
-    x = scan8_step<1>(x, tp);
-    x = scan8_step<2>(x, tp);
-    incl[e] = scan8_step<4>(x, tp);
+    float x = w0[e] * w1[e];
+    x = scan8_mul<1>(x, tp);
+    x = scan8_mul<2>(x, tp);
+    incl[e] = scan8_mul<4>(x, tp);
   }
   if (tp == 7) {
 #pragma unroll
@@ -217,9 +213,9 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
   }
   __syncthreads();
 
-  // Block totals x_q (q = 0..3, one per wave's 16 tokens); the carry into
-  // this wave is the sum of the blocks before it (a wave-uniform count).
-  float gp0[8], g1[8], total[8];
+  // Block products x_q (q = 0..3, one per wave's 16 tokens); the carry into
+  // this wave is the product of the blocks before it (a wave-uniform count).
+  float up_p[8], g1[8], total[8];
   float xq[4][8];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -230,24 +226,24 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
   }
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float lo2 = xq[0][e] + xq[1][e];
-    const float hi2 = xq[2][e] + xq[3][e];
-    total[e] = lo2 + hi2;
-    float base = 0.0f;
+    const float lo2 = xq[0][e] * xq[1][e];
+    const float hi2 = xq[2][e] * xq[3][e];
+    total[e] = lo2 * hi2;
+    float base = 1.0f;
     if (wave == 1) base = xq[0][e];
     if (wave == 2) base = lo2;
-    if (wave == 3) base = lo2 + xq[2][e];
-    g1[e] = base + incl[e];
-    gp0[e] = g1[e] - (lg0[e] + lg1[e]);
+    if (wave == 3) base = lo2 * xq[2][e];
+    g1[e] = base * incl[e];                   // 2^G(t0 + 1)
+    up_p[e] = base * scan8_exclusive(incl[e], tp);  // 2^Gp(t0)
   }
-  // A span exceeds the limit when its (non-positive) log2 decay sum is
-  // below -kSpanLimit; min reductions over the thread's 8 features, then a
-  // ballot. Every wave covers all 64 features, so the ballots agree.
+  // A span exceeds the limit when its decay product is below 2^-kSpanLimit;
+  // min reductions over the thread's 8 features, then a ballot. Every wave
+  // covers all 64 features, so the ballots agree.
   auto within = [](const float (&x)[8]) {
     float m = x[0];
 #pragma unroll
     for (int e = 1; e < 8; ++e) m = fminf(m, x[e]);
-    return __builtin_amdgcn_ballot_w64(m < -kSpanLimit) == 0;
+    return __builtin_amdgcn_ballot_w64(!(m >= kSpanFloor)) == 0;
   };
   Spans spans;
   spans.whole = within(total);
@@ -258,15 +254,13 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
   float fa0[8], fa1[8], fr0[8], fr1[8], fd0[8], fd1[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float up_p = fast_exp2(gp0[e]);  // 2^Gp(t0)
-    const float up0 = up_p * w0[e];        // 2^G(t0) = 2^Gp(t0 + 1)
-    const float up1 = up0 * w1[e];         // 2^G(t0 + 1)
-    const float dn1 = fast_exp2(-g1[e]);   // 2^-G(t0 + 1)
-    const float dn0 = dn1 * w1[e];         // 2^-G(t0)
-    fa0[e] = on0 ? up_p : 0.0f;
+    const float up0 = up_p[e] * w0[e];                // 2^G(t0) = 2^Gp(t0 + 1)
+    const float dn1 = __builtin_amdgcn_rcpf(g1[e]);   // 2^-G(t0 + 1)
+    const float dn0 = dn1 * w1[e];                    // 2^-G(t0)
+    fa0[e] = on0 ? up_p[e] : 0.0f;
     fa1[e] = on1 ? up0 : 0.0f;
     fr0[e] = on0 ? up0 : 0.0f;
-    fr1[e] = on1 ? up1 : 0.0f;
+    fr1[e] = on1 ? g1[e] : 0.0f;
     fd0[e] = on0 ? dn0 : 0.0f;
     fd1[e] = on1 ? dn1 : 0.0f;
   }
@@ -294,12 +288,12 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
   }
   if (wave == 0 && tp == 0) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sm.gc[8 * kg + e] = fast_exp2(total[e]);
+    for (int e = 0; e < 8; ++e) sm.gc[8 * kg + e] = total[e];
   }
   if (wave < 3 && tp == 7) {
     // Token t0 + 1 = 16 wave + 15 ends a 16-token block.
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sm.gsub[wave][8 * kg + e] = fast_exp2(g1[e]);
+    for (int e = 0; e < 8; ++e) sm.gsub[wave][8 * kg + e] = g1[e];
   }
   __syncthreads();
   return spans;
