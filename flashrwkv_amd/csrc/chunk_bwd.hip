@@ -92,7 +92,7 @@ struct BwdSmem {
     } f;
     uint16_t grad[4][kTriBlocks * kTriBlock];   // dArb, dArk, dLab, dLak: [t][i]
   } u;
-  float blk[4][kHead];    // per-block sums of log2 w
+  float blk[4][kHead];    // per-block products of the retention
   float gc[kHead];        // 2^GC
   float dgam[4][kHead];   // partial rowsum(S0 o dS) per column slab
   float car1[4][kHead];   // per-block totals of e1 + e2
@@ -176,6 +176,21 @@ __device__ __forceinline__ float prefix16(float x) {
 }
 __device__ __forceinline__ float suffix16(float x) {
   return row_shl_add<8>(row_shl_add<4>(row_shl_add<2>(row_shl_add<1>(x))));
+}
+// Products over the 16 lanes of a DPP row: a lane with no source keeps the
+// empty product 1 (bound_ctrl off, old value 1).
+template <int N>
+__device__ __forceinline__ float row_shr_mul(float x) {
+  return x * __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(1.0f), __float_as_int(x),
+                                                        0x110 + N, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float prefix16_mul(float x) {
+  return row_shr_mul<8>(row_shr_mul<4>(row_shr_mul<2>(row_shr_mul<1>(x))));
+}
+// The exclusive product from the inclusive one: lane n takes lane n - 1's.
+__device__ __forceinline__ float exclusive16(float incl) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(1.0f), __float_as_int(incl),
+                                                    0x111, 0xf, 0xf, false));
 }
 
 // Transpose read (see lds_operand_tr) whose column groups are 8 apart:
@@ -266,7 +281,12 @@ __device__ Spans prepare_piece(BwdSmem& sm, const TokRows& rows, const uint4& bi
 
   __syncthreads();  // earlier readers of the tiles are done
 
-  float lg[8], wr[8], G[8];
+  // Retentions (1 outside [lo, hi)) and the cumulative decay as products:
+  // 2^G(t) = prod_{j<=t} w_j by a product scan over the block's 16 tokens
+  // (one DPP row) and the products of the earlier blocks. Every product that
+  // reaches an operand has a span within the limit (>= 2^-80, a normal fp32
+  // number); a pass whose span exceeds it is redone as sub-pieces.
+  float wr[8], G[8];
   {
     float x[8], bias[8];
     unpack8<T>(rows.w, x);
@@ -275,26 +295,21 @@ __device__ Spans prepare_piece(BwdSmem& sm, const TokRows& rows, const uint4& bi
     for (int e = 0; e < 8; ++e) {
       float xin = x[e];
       if constexpr (M == DecayMode::kLogits) xin += bias[e];
-      const float l = log2_retention<M>(xin);
-      lg[e] = on ? l : 0.0f;
-      if constexpr (M == DecayMode::kRawW) {
-        wr[e] = on ? __builtin_amdgcn_fmed3f(xin, 0x1p-20f, 1.0f) : 1.0f;
-      } else {
-        wr[e] = fast_exp2(lg[e]);
-      }
+      const float r = clamped_retention<M>(xin);
+      wr[e] = on ? r : 1.0f;
     }
   }
 #pragma unroll
-  for (int e = 0; e < 8; ++e) G[e] = prefix16(lg[e]);
+  for (int e = 0; e < 8; ++e) G[e] = prefix16_mul(wr[e]);
   if (n == 15) {
     *reinterpret_cast<float4*>(&sm.blk[p][f0]) = make_float4(G[0], G[1], G[2], G[3]);
     *reinterpret_cast<float4*>(&sm.blk[p][f0 + 4]) = make_float4(G[4], G[5], G[6], G[7]);
   }
   __syncthreads();
 
-  float total[8];
+  float total[8], carry[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) total[e] = 0.0f;
+  for (int e = 0; e < 8; ++e) total[e] = carry[e] = 1.0f;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const float4 x0 = *reinterpret_cast<const float4*>(&sm.blk[q][f0]);
@@ -302,30 +317,32 @@ __device__ Spans prepare_piece(BwdSmem& sm, const TokRows& rows, const uint4& bi
     const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      if (q < p) G[e] += xs[e];
-      total[e] += xs[e];
+      if (q < p) carry[e] *= xs[e];
+      total[e] *= xs[e];
     }
   }
   // Spans over all 64 features: lane l looks at feature l.
   Spans spans;
   {
-    float bsum = 0.0f;
+    float bprod = 1.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const float x = sm.blk[q][lane];
-      bsum += x;
-      spans.block[q] = __builtin_amdgcn_ballot_w64(x < -kSpanLimit) == 0;
+      bprod *= x;
+      spans.block[q] = __builtin_amdgcn_ballot_w64(!(x >= kSpanFloor)) == 0;
     }
-    spans.whole = __builtin_amdgcn_ballot_w64(bsum < -kSpanLimit) == 0;
+    spans.whole = __builtin_amdgcn_ballot_w64(!(bprod >= kSpanFloor)) == 0;
   }
 
   // Scaled operand rows: At = a 2^Gp, Rt = r 2^G, Bh = b 2^-G, Kh = k 2^-G.
   float up[8], upp[8], dn[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    dn[e] = on ? fast_exp2(-G[e]) : 0.0f;
-    upp[e] = on ? fast_exp2(G[e] - lg[e]) : 0.0f;
-    up[e] = upp[e] * wr[e];
+    const float g = G[e] * carry[e];
+    const float gp = exclusive16(G[e]) * carry[e];
+    up[e] = on ? g : 0.0f;
+    upp[e] = on ? gp : 0.0f;
+    dn[e] = on ? __builtin_amdgcn_rcpf(g) : 0.0f;
   }
   auto row = [&](uint16_t* tile, uint4 raw, const float (&f)[8], float s) {
     float x[8];
@@ -344,11 +361,8 @@ __device__ Spans prepare_piece(BwdSmem& sm, const TokRows& rows, const uint4& bi
   row(sm.dy, rows.dy, ones, scale);
   row(sm.vv, rows.v, ones, 1.0f);
   if (p == 0 && n == 0) {
-    float gcv[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) gcv[e] = fast_exp2(total[e]);
-    *reinterpret_cast<float4*>(&sm.gc[f0]) = make_float4(gcv[0], gcv[1], gcv[2], gcv[3]);
-    *reinterpret_cast<float4*>(&sm.gc[f0 + 4]) = make_float4(gcv[4], gcv[5], gcv[6], gcv[7]);
+    *reinterpret_cast<float4*>(&sm.gc[f0]) = make_float4(total[0], total[1], total[2], total[3]);
+    *reinterpret_cast<float4*>(&sm.gc[f0 + 4]) = make_float4(total[4], total[5], total[6], total[7]);
   }
   __syncthreads();
   return spans;
@@ -770,18 +784,17 @@ __device__ void run_backward_step(BwdSmem& sm, const ChunkBwdParams& p, const To
   for (int u = 0; u < 2; ++u) {
     const int c0 = 32 * hf + 4 * u;
     const int fb = f0 + 4 * u;
-    // Decay factors of the lane's 4 features: G (the inclusive cumulative
-    // log2 decay of token t) again from the row scan and the earlier blocks'
-    // sums, as in prepare.
-    float carry[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // Decay factors of the lane's 4 features, recomputed exactly as in
+    // prepare: the row's product scan times the earlier blocks' products.
+    float carry[4] = {1.0f, 1.0f, 1.0f, 1.0f};
 #pragma unroll
-    for (int q = 0; q < 3; ++q) {
+    for (int q = 0; q < 4; ++q) {
       if (q < pt) {
         const float4 c = *reinterpret_cast<const float4*>(&sm.blk[q][fb]);
-        carry[0] += c.x;
-        carry[1] += c.y;
-        carry[2] += c.z;
-        carry[3] += c.w;
+        carry[0] *= c.x;
+        carry[1] *= c.y;
+        carry[2] *= c.z;
+        carry[3] *= c.w;
       }
     }
     float upp[4], up[4], dn[4];
@@ -790,17 +803,13 @@ __device__ void run_backward_step(BwdSmem& sm, const ChunkBwdParams& p, const To
       const int e = 4 * u + jj;
       float xin = raw(cur.w, e);
       if constexpr (M == DecayMode::kLogits) xin += raw(bias, e);
-      const float lg = on ? log2_retention<M>(xin) : 0.0f;
-      const float Gv = prefix16(lg) + carry[jj];
-      float wv;
-      if constexpr (M == DecayMode::kRawW) {
-        wv = __builtin_amdgcn_fmed3f(xin, 0x1p-20f, 1.0f);
-      } else {
-        wv = fast_exp2(lg);
-      }
-      upp[jj] = on ? fast_exp2(Gv - lg) : 0.0f;
-      up[jj] = upp[jj] * wv;
-      dn[jj] = on ? fast_exp2(-Gv) : 0.0f;
+      const float wv = on ? clamped_retention<M>(xin) : 1.0f;
+      const float Gi = prefix16_mul(wv);
+      const float g = Gi * carry[jj];
+      const float gp = exclusive16(Gi) * carry[jj];
+      up[jj] = on ? g : 0.0f;
+      upp[jj] = on ? gp : 0.0f;
+      dn[jj] = on ? __builtin_amdgcn_rcpf(g) : 0.0f;
     }
     float e12[4];
 
