@@ -80,8 +80,8 @@ struct BwdSmem {
   uint16_t kh[kOpTile];   // Kh  [t][k]
   uint16_t dy[kOpTile];   // dYs [t][v]
   uint16_t vv[kOpTile];   // V   [t][v]
-  uint16_t sa[kOpTile];   // SA  [v][t]
-  uint16_t dz[kOpTile];   // dZ  [v][t]
+  uint16_t sa[kOpTile];   // SA  [t][v]
+  uint16_t dz[kOpTile];   // dZ  [t][v]
   uint16_t s0[kOpTile];   // S0  [v][k]
   uint16_t ds[kOpTile];   // dS  [v][k] (adjoint at the piece end)
   uint16_t dv[kOpTile];   // dV  [t][v] in the io dtype (staged for row stores)
@@ -191,6 +191,17 @@ __device__ __forceinline__ float prefix16_mul(float x) {
 __device__ __forceinline__ float exclusive16(float incl) {
   return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(1.0f), __float_as_int(incl),
                                                     0x111, 0xf, 0xf, false));
+}
+
+// Stores a C-layout block (lane (g, n) holds X[4g + j][n]) into a row-major
+// [row][col] bf16 tile at dst: four 2-byte stores per lane, the 16 lanes of a
+// group writing 32 consecutive bytes of one row.
+__device__ __forceinline__ void lds_store_rows(uint16_t* dst, int stride, int g, int n,
+                                               f32x4 c) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    dst[(4 * g + j) * stride + n] = static_cast<uint16_t>(pack_bf16x2(c[j], 0.0f) & 0xffffu);
+  }
 }
 
 // Transpose read (see lds_operand_tr) whose column groups are 8 apart:
@@ -621,7 +632,7 @@ __device__ __forceinline__ void adjoint_chain(BwdSmem& sm, const f32x4 (&S0)[4],
   const i16x8 dz01 = cat(dzb[0], dzb[1]);
 #pragma unroll
   for (int pb = 0; pb < 4; ++pb)
-    lds_store_transposed(sm.dz + (16 * cs) * kOpStride + 16 * pb, kOpStride, g, n, dz[pb]);
+    lds_store_rows(sm.dz + (16 * pb) * kOpStride + 16 * cs, kOpStride, g, n, dz[pb]);
 
   // dV^T (rows v of this slab, cols t of block pb):
   //   (g o dS)^T Kh^T + sum_{q>=pb} (dYs_q^T Ark(q, pb) + dZ_q^T Lak(q, pb)).
@@ -672,37 +683,39 @@ __device__ __forceinline__ void adjoint_chain(BwdSmem& sm, const f32x4 (&S0)[4],
   }
 }
 
-// The four gradient matrices, 40 (matrix, block pair) items, five per wave:
-// M[t][i] = sum_v X[t][v] Y[i][v] (X = dYs or dZ, Y = SA or V), computed as
-// M^T in C layout and stored [t][i]. Ends with a barrier.
+// The four gradient matrices, 40 (matrix, block pair) items, five per wave
+// (item wave + 8 i): M[t][i] = sum_v X[t][v] Y[i][v] (X = dYs or dZ, Y = SA
+// or V, all four [t][v] tiles), computed as M^T in C layout and stored
+// [t][i]. The items differ only in their tile pointers, so the five are
+// unrolled without branches and their reads overlap. Ends with a barrier.
 __device__ __forceinline__ void gradient_matrices(BwdSmem& sm) {
   const int tid = lane_tid();
   const int wave = uniform(tid >> 6);
   const int lane = tid & 63;
   const int g = lane >> 4, n = lane & 15;
   __builtin_amdgcn_s_setprio(1);
-#pragma unroll 1
-  for (int item = wave; item < 40; item += 8) {
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {
+    const int item = wave + 8 * i;
     const int m = item / 10;  // kGArb, kGArk, kGLab, kGLak
     const int pair = item % 10;
     const int pb = pair < 1 ? 0 : pair < 3 ? 1 : pair < 6 ? 2 : 3;
     const int q = pair - (pb * (pb + 1)) / 2;
     const bool from_dz = m >= 2;
-    const bool with_v = (m & 1) != 0;
+    const uint16_t* xt = from_dz ? sm.dz : sm.dy;
+    const uint16_t* yt = (m & 1) != 0 ? sm.vv : sm.sa;
     f32x4 mt = zero4();
 #pragma unroll
     for (int c = 0; c < 64; c += 32) {
-      const i16x8 x = from_dz ? tr32<kOpStride>(sm.dz, c, 16 * pb, g, n)
-                              : lds_operand32<kOpStride>(sm.dy, 16 * pb + n, c, g);
-      const i16x8 y = with_v ? lds_operand32<kOpStride>(sm.vv, 16 * q + n, c, g)
-                             : tr32<kOpStride>(sm.sa, c, 16 * q, g, n);
+      const i16x8 x = lds_operand32<kOpStride>(xt, 16 * pb + n, c, g);
+      const i16x8 y = lds_operand32<kOpStride>(yt, 16 * q + n, c, g);
       mt = mfma32(y, x, mt);  // lane (g, n): M[t = 16 pb + n][i = 16 q + 4g + j]
     }
     if (pb == q) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int i = 4 * g + j;
-        mt[j] = (from_dz ? (i < n) : (i <= n)) ? mt[j] : 0.0f;
+        const int ii = 4 * g + j;
+        mt[j] = (from_dz ? (ii < n) : (ii <= n)) ? mt[j] : 0.0f;
       }
     }
     lds_store_transposed(sm.u.grad[m] + tri_index(pb, q) * kTriBlock, kTriStride, g, n, mt);
@@ -739,7 +752,7 @@ __device__ void run_backward_step(BwdSmem& sm, const ChunkBwdParams& p, const To
     sa_chain(sm, S0, cs, g, n, sa, sab, vs);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      lds_store_transposed(sm.sa + (16 * cs) * kOpStride + 16 * q, kOpStride, g, n, sa[q]);
+      lds_store_rows(sm.sa + (16 * q) * kOpStride + 16 * cs, kOpStride, g, n, sa[q]);
       lds_store_transposed(sm.s0 + (16 * cs) * kOpStride + 16 * q, kOpStride, g, n, S0[q]);
     }
   } else {
@@ -821,7 +834,7 @@ __device__ void run_backward_step(BwdSmem& sm, const ChunkBwdParams& p, const To
       for (int c = 0; c < 64; c += 32) {
         const i16x8 s0a = tr32_q8<kOpStride>(sm.s0, c, c0, g, n);
         acc_r = mfma32(s0a, lds_operand32<kOpStride>(sm.dy, t, c, g), acc_r);
-        acc_a = mfma32(s0a, tr32<kOpStride>(sm.dz, c, 16 * pt, g, n), acc_a);
+        acc_a = mfma32(s0a, lds_operand32<kOpStride>(sm.dz, t, c, g), acc_a);
       }
       // Source blocks q <= pt: A = Bh^T / Kh^T (rows: features), B = the
       // gradient blocks (pt, q) as stored.
@@ -874,7 +887,7 @@ __device__ void run_backward_step(BwdSmem& sm, const ChunkBwdParams& p, const To
 #pragma unroll
       for (int c = 0; c < 64; c += 32) {
         const i16x8 dsa = tr32_q8<kOpStride>(sm.ds, c, c0, g, n);
-        acc_bt = mfma32(dsa, tr32<kOpStride>(sm.sa, c, 16 * pt, g, n), acc_bt);
+        acc_bt = mfma32(dsa, lds_operand32<kOpStride>(sm.sa, t, c, g), acc_bt);
         acc_kt = mfma32(dsa, lds_operand32<kOpStride>(sm.vv, t, c, g), acc_kt);
       }
       // Target blocks qt >= pt: A = At^T / Rt^T, B = the gradient blocks
