@@ -177,20 +177,23 @@ __device__ __forceinline__ float prefix16(float x) {
 __device__ __forceinline__ float suffix16(float x) {
   return row_shl_add<8>(row_shl_add<4>(row_shl_add<2>(row_shl_add<1>(x))));
 }
-// Products over the 16 lanes of a DPP row: a lane with no source keeps the
-// empty product 1 (bound_ctrl off, old value 1).
+// Products over the 16 lanes of a DPP row (n = lane % 16): lanes n < N keep
+// x (the shifted-in value reads 0, and the select restores x).
 template <int N>
-__device__ __forceinline__ float row_shr_mul(float x) {
-  return x * __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(1.0f), __float_as_int(x),
-                                                        0x110 + N, 0xf, 0xf, false));
+__device__ __forceinline__ float row_shr_mul(float x, int n) {
+  const float y = x * __int_as_float(
+                          __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x110 + N, 0xf, 0xf, true));
+  return n >= N ? y : x;
 }
-__device__ __forceinline__ float prefix16_mul(float x) {
-  return row_shr_mul<8>(row_shr_mul<4>(row_shr_mul<2>(row_shr_mul<1>(x))));
+__device__ __forceinline__ float prefix16_mul(float x, int n) {
+  return row_shr_mul<8>(row_shr_mul<4>(row_shr_mul<2>(row_shr_mul<1>(x, n), n), n), n);
 }
-// The exclusive product from the inclusive one: lane n takes lane n - 1's.
-__device__ __forceinline__ float exclusive16(float incl) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(1.0f), __float_as_int(incl),
-                                                    0x111, 0xf, 0xf, false));
+// The exclusive product from the inclusive one: lane n takes lane n - 1's,
+// lane 0 the empty product 1.
+__device__ __forceinline__ float exclusive16(float incl, int n) {
+  const float y = __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(incl), 0x111, 0xf, 0xf, true));
+  return n >= 1 ? y : 1.0f;
 }
 
 // Stores a C-layout block (lane (g, n) holds X[4g + j][n]) into a row-major
@@ -311,7 +314,7 @@ __device__ Spans prepare_piece(BwdSmem& sm, const TokRows& rows, const uint4& bi
     }
   }
 #pragma unroll
-  for (int e = 0; e < 8; ++e) G[e] = prefix16_mul(wr[e]);
+  for (int e = 0; e < 8; ++e) G[e] = prefix16_mul(wr[e], n);
   if (n == 15) {
     *reinterpret_cast<float4*>(&sm.blk[p][f0]) = make_float4(G[0], G[1], G[2], G[3]);
     *reinterpret_cast<float4*>(&sm.blk[p][f0 + 4]) = make_float4(G[4], G[5], G[6], G[7]);
@@ -350,7 +353,7 @@ __device__ Spans prepare_piece(BwdSmem& sm, const TokRows& rows, const uint4& bi
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float g = G[e] * carry[e];
-    const float gp = exclusive16(G[e]) * carry[e];
+    const float gp = exclusive16(G[e], n) * carry[e];
     up[e] = on ? g : 0.0f;
     upp[e] = on ? gp : 0.0f;
     dn[e] = on ? __builtin_amdgcn_rcpf(g) : 0.0f;
@@ -817,9 +820,9 @@ __device__ void run_backward_step(BwdSmem& sm, const ChunkBwdParams& p, const To
       float xin = raw(cur.w, e);
       if constexpr (M == DecayMode::kLogits) xin += raw(bias, e);
       const float wv = on ? clamped_retention<M>(xin) : 1.0f;
-      const float Gi = prefix16_mul(wv);
+      const float Gi = prefix16_mul(wv, n);
       const float g = Gi * carry[jj];
-      const float gp = exclusive16(Gi) * carry[jj];
+      const float gp = exclusive16(Gi, n) * carry[jj];
       up[jj] = on ? g : 0.0f;
       upp[jj] = on ? gp : 0.0f;
       dn[jj] = on ? __builtin_amdgcn_rcpf(g) : 0.0f;
