@@ -75,6 +75,10 @@ __device__ __forceinline__ const uint16_t* tri_block(const ChunkSmem& sm, int m,
 
 struct ChunkFwdParams {
   int32_t num_heads;
+  // Packed varlen batches of at most 64 sequences (cu_seqlens mode) run
+  // their sequences longest first: workgroup b takes the sequence of length
+  // rank b / H. 0 keeps the natural order.
+  int32_t longest_first_sequences;
   int32_t total_tokens;
   int32_t state_slots;
   const int32_t* cu_seqlens;    // sequence token ranges when seg_offsets == null
@@ -611,6 +615,23 @@ __device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const uint16_t* v
   }
 }
 
+// The sequence of the given rank in order of decreasing length (ties in
+// index order), for batches of at most 64 sequences: lane s holds sequence
+// s's length, counts the sequences ahead of it, and the lane whose count is
+// the rank names the sequence. Wave-uniform; every wave computes it alike.
+__device__ __forceinline__ int sequence_by_length_rank(const ChunkFwdParams& p, int rank,
+                                                       int lane) {
+  const int count = p.longest_first_sequences;
+  const int len = lane < count ? p.cu_seqlens[lane + 1] - p.cu_seqlens[lane] : -1;
+  int ahead = 0;
+  for (int j = 0; j < count; ++j) {
+    const int lj = __builtin_amdgcn_readlane(len, j);
+    ahead += (lj > len || (lj == len && j < lane)) ? 1 : 0;
+  }
+  const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < count && ahead == rank);
+  return hit != 0 ? static_cast<int>(__builtin_ctzll(hit)) : rank;
+}
+
 template <typename T, DecayMode M, typename PoolT>
 __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdParams p) {
   __shared__ ChunkSmem sm;
@@ -628,7 +649,8 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
   const int tp = lane & 7;   // token pair
   const int kg = lane >> 3;  // feature group
   const int heads = p.num_heads;
-  const int seq = blockIdx.x / heads;
+  int seq = blockIdx.x / heads;
+  if (p.longest_first_sequences > 0) seq = sequence_by_length_rank(p, seq, lane);
   const int head = blockIdx.x % heads;
   // Metadata values are workgroup-uniform; readfirstlane keeps them (and
   // every buffer descriptor derived from them) in scalar registers.
@@ -969,6 +991,7 @@ extern "C" int frwkv_chunk_forward(
   }
   ChunkFwdParams p{};
   p.num_heads = num_heads;
+  p.longest_first_sequences = num_sequences <= 64 ? num_sequences : 0;
   p.total_tokens = total_tokens;
   p.state_slots = state_pool_size;
   p.cu_seqlens = cu_seqlens;
