@@ -41,26 +41,52 @@ BF16_PEAK_TFLOPS = 2516.6
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, mean KiB per dispatch of each
 # kernel at its bench workload (the traffic summaries under profiles/ give the
 # runs and their commands). Calibration: a 256 MiB device copy (--workload copy) reads
-# FETCH_SIZE 131085.3 KiB and WRITE_SIZE 262144.0 KiB per dispatch, so fetched
-# bytes are FETCH_SIZE * 1024 * (262144 / 131085.3) and written bytes
+# FETCH_SIZE 131084.4 KiB and WRITE_SIZE 262144.0 KiB per dispatch, so fetched
+# bytes are FETCH_SIZE * 1024 * (262144 / 131084.4) and written bytes
 # WRITE_SIZE * 1024.
 _COPY_KIB = 262144.0
-_COPY_FETCH_KIB = 131085.3
+_COPY_FETCH_KIB = 131084.4
 _COPY_WRITE_KIB = 262144.0
 PMC_KIB = {  # kernel -> (FETCH_SIZE, WRITE_SIZE)
-    "recurrent_fp32_kernel<64,64,64,Bf16,kRawW>": (85812.5, 165181.9),
-    "chunk_fwd_kernel<Bf16,kRawW,float>": (790726.8, 270851.7),
-    "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": (803353.1, 1319761.2),
-    "chunk_bwd_kernel<Bf16,kRawW>": (1988333.6, 2456509.8),
-    "recurrent_fp32_kernel<64,64,64,F16,kLogits,kFp16>": (44896.8, 83200.7),
+    "recurrent_fp32_kernel<64,64,64,Bf16,kRawW>": (85811.4, 165210.7),
+    "chunk_fwd_kernel<Bf16,kRawW,float>": (790713.2, 270341.6),
+    "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": (790727.9, 1319388.2),
+    "chunk_bwd_kernel<Bf16,kRawW>": (1187648.9, 1636895.4),
+    "recurrent_fp16_decode_kernel": (44891.9, 83212.9),
 }
 
+# The kernel sources PMC_KIB was measured on: sha256 over these files, in
+# order. When the tree's sources differ, the constants describe other kernels
+# and pmc_traffic reports None instead of a stale figure.
+PMC_SOURCES = ("flashrwkv_amd/csrc/recurrent.hip", "flashrwkv_amd/csrc/chunk_fwd.hip",
+               "flashrwkv_amd/csrc/chunk_bwd.hip", "flashrwkv_amd/csrc/chunk_common.h",
+               "flashrwkv_amd/csrc/wkv7_device.h", "flashrwkv_amd/csrc/wkv7_mfma.h")
+PMC_SOURCES_SHA = "eb75bacfd38ceb85216cd09806eb59a531cf1e613a52b84cc279a3ef4ab80499"
 
-def pmc_traffic(kernel: str) -> int:
-    """Measured HBM bytes per dispatch of ``kernel`` (calibrated counters)."""
+
+def kernel_sources_sha() -> str:
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in PMC_SOURCES:
+        h.update((ROOT / rel).read_bytes())
+    return h.hexdigest()
+
+
+def pmc_traffic(kernel: str) -> int | None:
+    """Measured HBM bytes per dispatch of ``kernel`` (calibrated counters), or
+    None when the kernel sources changed since the measurement."""
+    if kernel not in PMC_KIB or kernel_sources_sha() != PMC_SOURCES_SHA:
+        return None
     fetch, write = PMC_KIB[kernel]
     return int(round(fetch * 1024 * _COPY_KIB / _COPY_FETCH_KIB
                      + write * 1024 * _COPY_KIB / _COPY_WRITE_KIB))
+
+
+def _sum_or_none(*xs):
+    return None if any(x is None for x in xs) else sum(xs)
+
+
 METRIC = "WKV7 tokens/s + % roofline (HBM GB/s decode, MFMA TFLOP/s chunked), h32d64"
 
 
@@ -353,7 +379,7 @@ def bench_decode(args, fp16_state=False):
     achieved = nbytes / (cold_ms * 1e-3) / 1e9
     tok_s = batch / (cold_ms * 1e-3)
     if fp16_state:
-        kernel = "recurrent_fp32_kernel<64,64,64,F16,kLogits,kFp16>"
+        kernel = "recurrent_fp16_decode_kernel"
         return {
             "workload": f"wkv7_decode_fp16_state: B=256, H=40, D=64, T=1 per step, fp16 io, "
                         f"fp16 state pool in place, decay logits, {n_pools} rotating pool "
@@ -363,7 +389,7 @@ def bench_decode(args, fp16_state=False):
             "roofline": {
                 "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                "traffic": pmc_traffic(kernel) if kernel in PMC_KIB else None,
+                "traffic": pmc_traffic(kernel),
                 "kernel": kernel, "algorithmic_bytes_per_launch": nbytes,
             },
             "inplace_single_pool": {
@@ -837,8 +863,8 @@ def bench_training(args):
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
                      "algorithmic_flops_per_step": flops,
-                     "traffic": pmc_traffic("chunk_fwd_kernel<Bf16,kRawW,float>/statetune")
-                     + pmc_traffic("chunk_bwd_kernel<Bf16,kRawW>"),
+                     "traffic": _sum_or_none(pmc_traffic("chunk_fwd_kernel<Bf16,kRawW,float>/statetune"),
+                                             pmc_traffic("chunk_bwd_kernel<Bf16,kRawW>")),
                      "kernel": "chunk_fwd_kernel<Bf16,kRawW,float> + chunk_bwd_kernel<Bf16,kRawW>"},
         "hbm": {"achieved_GBps": round(gbps, 1), "peak": HBM_PEAK_GBPS,
                 "frac": round(gbps / HBM_PEAK_GBPS, 4), "algorithmic_bytes_per_step": nbytes},
