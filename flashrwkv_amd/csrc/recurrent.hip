@@ -450,12 +450,20 @@ __global__ __launch_bounds__(64) void recurrent_fp16_decode_kernel(
   }
   uint16_t* sbase = static_cast<uint16_t*>(p.state) +
                     ((static_cast<int64_t>(slot) * num_heads + head) * D) * D;
-  float s[8][8];
+  // The state stays fp16 in registers (it is fp16 at every rounding point);
+  // products read it through mixed-precision fmas, which take an fp16
+  // operand exactly, so no separate conversion to fp32 is needed.
+  _Float16 s[8][8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const u32x4 q = __builtin_nontemporal_load(
         reinterpret_cast<const u32x4*>(sbase + (row0 + j) * D + col));
-    unpack_f16x8(make_uint4(q.x, q.y, q.z, q.w), s[j]);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s[j][2 * i] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] & 0xffffu));
+      s[j][2 * i + 1] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] >> 16));
+    }
   }
   float bias[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (bias_ptr != nullptr) unpack_f16x8(load_x8(bias_ptr + head * D + row0), bias);
@@ -476,7 +484,7 @@ __global__ __launch_bounds__(64) void recurrent_fp16_decode_kernel(
     for (int c = 0; c < 8; ++c) {
       float acc = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc = fmaf(aa[j], s[j][c], acc);
+      for (int j = 0; j < 8; ++j) acc = fmaf(aa[j], static_cast<float>(s[j][c]), acc);
       sa[c] = sum_row_groups8(acc);
     }
     float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -487,8 +495,9 @@ __global__ __launch_bounds__(64) void recurrent_fp16_decode_kernel(
           round_f16(w - 1.0f + phase_dither(phase0 + static_cast<uint32_t>(j + t)));
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
-        s[j][c] = round_f16(fmaf(kk[j], vv[c], fmaf(bb[j], sa[c], fmaf(s[j][c], delta, s[j][c]))));
-        y[c] = fmaf(rr[j], s[j][c], y[c]);
+        const float sj = static_cast<float>(s[j][c]);
+        s[j][c] = static_cast<_Float16>(fmaf(kk[j], vv[c], fmaf(bb[j], sa[c], fmaf(sj, delta, sj))));
+        y[c] = fmaf(rr[j], static_cast<float>(s[j][c]), y[c]);
       }
     }
 #pragma unroll
@@ -504,11 +513,13 @@ __global__ __launch_bounds__(64) void recurrent_fp16_decode_kernel(
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    u32x4 q;
-    q.x = pack2<F16>(s[j][0], s[j][1]);
-    q.y = pack2<F16>(s[j][2], s[j][3]);
-    q.z = pack2<F16>(s[j][4], s[j][5]);
-    q.w = pack2<F16>(s[j][6], s[j][7]);
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[i] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, s[j][2 * i])) |
+             (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, s[j][2 * i + 1])) << 16);
+    }
+    const u32x4 q = {w[0], w[1], w[2], w[3]};
     __builtin_nontemporal_store(q, reinterpret_cast<u32x4*>(sbase + (row0 + j) * D + col));
   }
 }

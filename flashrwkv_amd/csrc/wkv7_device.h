@@ -22,10 +22,15 @@ constexpr float kLog2E = 1.4426950408889634f;
 // Retention and its natural log from a pre-transform decay input.
 // Logits: log w = -e^{-1/2} * sigmoid(x); computing log w directly keeps full
 // precision for w close to 1, which the chunked kernels need.
+// The sigmoid and the exponential use the hardware reciprocal and exp2
+// (v_rcp_f32, v_exp_f32, about 1 ulp): exp2 of a large positive argument is
+// +inf and its reciprocal 0, so sigmoid(x) -> 0 for x -> -inf without a
+// special case, and log w lies in [-e^{-1/2}, 0], far from exp2's denormal
+// range.
 template <DecayMode M>
 __device__ __forceinline__ float decay_log(float x) {
   if constexpr (M == DecayMode::kLogits) {
-    const float sig = 1.0f / (1.0f + exp2f(-kLog2E * x));
+    const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-kLog2E * x));
     return -kExpNegHalf * sig;
   } else {
     return __logf(x);
@@ -35,7 +40,7 @@ __device__ __forceinline__ float decay_log(float x) {
 template <DecayMode M>
 __device__ __forceinline__ float decay_retention(float x) {
   if constexpr (M == DecayMode::kLogits) {
-    return exp2f(kLog2E * decay_log<M>(x));
+    return __builtin_amdgcn_exp2f(kLog2E * decay_log<M>(x));
   } else {
     return x;
   }
