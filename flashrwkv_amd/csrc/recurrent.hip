@@ -35,6 +35,7 @@
 // measured fastest (6.07 TB/s at B=256, H=40, above a plain 168 MB copy).
 #include "capi_internal.h"
 #include "wkv7_device.h"
+#include "wkv7_mfma.h"
 
 namespace frwkv {
 namespace {
@@ -165,7 +166,7 @@ struct RecurrentKernelParams {
   float scale;
 };
 
-template <int D, int CW, int WG, typename T, DecayMode M, StateKind SK>
+template <int D, int CW, int WG, typename T, DecayMode M, StateKind SK, bool kBuf = false>
 __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
     RecurrentKernelParams p,
     const typename IoTraits<T>::storage* __restrict__ r_ptr,
@@ -249,14 +250,41 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
     RawRow<T, kRpl> a, w, b, k, r;
     RawRow<T, 4> v;
   };
+  // kBuf (prefetching shapes, tensors under 2 GiB): buffer loads whose
+  // per-lane offset is fixed and whose token offset is one scalar, so a
+  // token's six row loads need no address arithmetic in the vector unit.
+  constexpr uint32_t kEsize = IoTraits<T>::kBytes;
+  const uint32_t tensor_bytes =
+      kBuf ? static_cast<uint32_t>(total_tokens) * static_cast<uint32_t>(num_heads * D) * kEsize
+           : 0u;
+  const auto rs_a = buffer_rsrc(a_ptr, tensor_bytes);
+  const auto rs_w = buffer_rsrc(decay_ptr, tensor_bytes);
+  const auto rs_b = buffer_rsrc(b_ptr, tensor_bytes);
+  const auto rs_k = buffer_rsrc(k_ptr, tensor_bytes);
+  const auto rs_r = buffer_rsrc(r_ptr, tensor_bytes);
+  const auto rs_v = buffer_rsrc(v_ptr, tensor_bytes);
+  const auto rs_out = buffer_rsrc(out_ptr, tensor_bytes);
+  const uint32_t vo_rows = static_cast<uint32_t>(head * D + row0) * kEsize;
+  const uint32_t vo_cols = static_cast<uint32_t>(head * D + col) * kEsize;
+  const uint32_t token_bytes = static_cast<uint32_t>(num_heads * D) * kEsize;
   auto load_token = [&](TokenRows& dst, int32_t t) {
-    const int64_t base = (static_cast<int64_t>(t) * num_heads + head) * D;
-    load_raw<T, kRpl>(a_ptr + base + row0, dst.a);
-    load_raw<T, kRpl>(decay_ptr + base + row0, dst.w);
-    load_raw<T, kRpl>(b_ptr + base + row0, dst.b);
-    load_raw<T, kRpl>(k_ptr + base + row0, dst.k);
-    load_raw<T, kRpl>(r_ptr + base + row0, dst.r);
-    load_raw<T, 4>(v_ptr + base + col, dst.v);
+    if constexpr (kBuf) {
+      const int so = static_cast<int>(static_cast<uint32_t>(t) * token_bytes);
+      load_raw_buf<T, kRpl>(rs_a, vo_rows, so, dst.a);
+      load_raw_buf<T, kRpl>(rs_w, vo_rows, so, dst.w);
+      load_raw_buf<T, kRpl>(rs_b, vo_rows, so, dst.b);
+      load_raw_buf<T, kRpl>(rs_k, vo_rows, so, dst.k);
+      load_raw_buf<T, kRpl>(rs_r, vo_rows, so, dst.r);
+      load_raw_buf<T, 4>(rs_v, vo_cols, so, dst.v);
+    } else {
+      const int64_t base = (static_cast<int64_t>(t) * num_heads + head) * D;
+      load_raw<T, kRpl>(a_ptr + base + row0, dst.a);
+      load_raw<T, kRpl>(decay_ptr + base + row0, dst.w);
+      load_raw<T, kRpl>(b_ptr + base + row0, dst.b);
+      load_raw<T, kRpl>(k_ptr + base + row0, dst.k);
+      load_raw<T, kRpl>(r_ptr + base + row0, dst.r);
+      load_raw<T, 4>(v_ptr + base + col, dst.v);
+    }
   };
   // About 96 registers of ring; the one-wave decode shape loads in place.
   constexpr int kTokenWords = 5 * RawRow<T, kRpl>::kWords + RawRow<T, 4>::kWords;
@@ -284,7 +312,9 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
       decode_raw<T, kRpl>(ring[jp].r, rr);
       decode_raw<T, 4>(ring[jp].v, vv);
       if constexpr (kPrefetch > 1) {
-        if (t + kPrefetch < t_end) load_token(ring[jp], t + kPrefetch);
+        // Unconditional (the last token again past the end): a skipped load
+        // would make the ring registers a join of two paths, copied per token.
+        load_token(ring[jp], min(t + kPrefetch, t_end - 1));
       }
 
       float4 sa = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -307,7 +337,11 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
       float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
       for (int j = 0; j < kRpl; ++j) {
-        const float w = decay_retention<M>(ww[j] + bias[j]);
+        // (The raw-retention prefetch path skips the zero bias; the decode
+        // shape keeps the add: without it the compiler reorders the
+        // one-token body and the HBM-bound launch runs 1.6% slower.)
+        const float w = decay_retention<M>(
+            (kPrefetch > 1 && M != DecayMode::kLogits) ? ww[j] : ww[j] + bias[j]);
         if constexpr (SK == StateKind::kFp32) {
           s[j].x = fmaf(w, s[j].x, fmaf(bb[j], sa.x, kk[j] * vv[0]));
           s[j].y = fmaf(w, s[j].y, fmaf(bb[j], sa.y, kk[j] * vv[1]));
@@ -331,9 +365,14 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
       y.z = sum_row_groups<kNg, kLowRows>(y.z);
       y.w = sum_row_groups<kNg, kLowRows>(y.w);
       if (rg == 0) {
-        const int64_t base = (static_cast<int64_t>(t) * num_heads + head) * D;
-        store4<T>(out_ptr + base + col, scale * y.x, scale * y.y, scale * y.z,
-                  scale * y.w);
+        if constexpr (kBuf) {
+          store4_buf<T>(rs_out, vo_cols, static_cast<int>(static_cast<uint32_t>(t) * token_bytes),
+                        scale * y.x, scale * y.y, scale * y.z, scale * y.w);
+        } else {
+          const int64_t base = (static_cast<int64_t>(t) * num_heads + head) * D;
+          store4<T>(out_ptr + base + col, scale * y.x, scale * y.y, scale * y.z,
+                    scale * y.w);
+        }
       }
     }
   }
@@ -362,7 +401,7 @@ struct RecurrentArgs {
   const int32_t* elapsed = nullptr;
 };
 
-template <int D, int CW, int WG, typename T, DecayMode M, StateKind SK>
+template <int D, int CW, int WG, typename T, DecayMode M, StateKind SK, bool kBuf = false>
 int launch_recurrent(const RecurrentArgs& p) {
   using S = typename IoTraits<T>::storage;
   const int units = p.num_sequences * p.num_heads;
@@ -384,7 +423,7 @@ int launch_recurrent(const RecurrentArgs& p) {
   kp.state_dot_a = p.state_dot_a;
   kp.read_only_state = p.read_only_state;
   kp.scale = p.scale;
-  hipLaunchKernelGGL((recurrent_fp32_kernel<D, CW, WG, T, M, SK>), dim3(blocks),
+  hipLaunchKernelGGL((recurrent_fp32_kernel<D, CW, WG, T, M, SK, kBuf>), dim3(blocks),
                      dim3(WG), 0, p.stream, kp, static_cast<const S*>(p.r),
                      static_cast<const S*>(p.decay), static_cast<const S*>(p.bias),
                      static_cast<const S*>(p.k), static_cast<const S*>(p.v),
@@ -547,6 +586,13 @@ int launch_fp16_decode(const RecurrentArgs& p) {
   return check_launch("recurrent_fp16_decode_kernel");
 }
 
+// Token tensors small enough for 32-bit buffer offsets (below 2 GiB).
+template <int D, typename T>
+bool buffer_addressable(const RecurrentArgs& p) {
+  return static_cast<int64_t>(p.total_tokens) * p.num_heads * D * IoTraits<T>::kBytes <
+         (int64_t{1} << 31);
+}
+
 template <typename T, DecayMode M, StateKind SK = StateKind::kFp32>
 int dispatch_head_size(const RecurrentArgs& p) {
   switch (p.head_size) {
@@ -557,10 +603,13 @@ int dispatch_head_size(const RecurrentArgs& p) {
         if constexpr (SK == StateKind::kFp16) return launch_fp16_decode(p);
         return launch_recurrent<64, 64, 64, T, M, SK>(p);
       }
+      if (buffer_addressable<64, T>(p)) return launch_recurrent<64, 16, 256, T, M, SK, true>(p);
       return launch_recurrent<64, 16, 256, T, M, SK>(p);
     case 128:
+      if (buffer_addressable<128, T>(p)) return launch_recurrent<128, 16, 256, T, M, SK, true>(p);
       return launch_recurrent<128, 16, 256, T, M, SK>(p);
     case 256:
+      if (buffer_addressable<256, T>(p)) return launch_recurrent<256, 16, 256, T, M, SK, true>(p);
       return launch_recurrent<256, 16, 256, T, M, SK>(p);
     default:
       return set_error(FRWKV_ERR_UNSUPPORTED,

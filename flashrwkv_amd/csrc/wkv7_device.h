@@ -195,6 +195,33 @@ __device__ __forceinline__ void load_raw(const typename IoTraits<T>::storage* p,
   }
 }
 
+// load_raw through a buffer resource: byte offsets voffset (per lane) and
+// soffset (uniform) into the resource.
+template <typename T, int N>
+__device__ __forceinline__ void load_raw_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voffset,
+                                             int soffset, RawRow<T, N>& out) {
+  constexpr int kWords = RawRow<T, N>::kWords;
+  if constexpr (kWords % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < kWords / 4; ++i) {
+      typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+      const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(rs, voffset + 16 * i, soffset, 0);
+      out.w[4 * i + 0] = q.x;
+      out.w[4 * i + 1] = q.y;
+      out.w[4 * i + 2] = q.z;
+      out.w[4 * i + 3] = q.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kWords / 2; ++i) {
+      typedef uint32_t u32x2_t2 __attribute__((ext_vector_type(2)));
+      const u32x2_t2 q = __builtin_amdgcn_raw_buffer_load_b64(rs, voffset + 8 * i, soffset, 0);
+      out.w[2 * i + 0] = q.x;
+      out.w[2 * i + 1] = q.y;
+    }
+  }
+}
+
 template <typename T, int N>
 __device__ __forceinline__ void decode_raw(const RawRow<T, N>& in, float (&out)[N]) {
   if constexpr (__is_same(T, float)) {
@@ -220,6 +247,24 @@ __device__ __forceinline__ void store4(typename IoTraits<T>::storage* p, float x
     q.x = pack2<T>(x0, x1);
     q.y = pack2<T>(x2, x3);
     *reinterpret_cast<uint2*>(p) = q;
+  }
+}
+
+// store4 through a buffer resource (byte offsets voffset per lane, soffset
+// uniform).
+template <typename T>
+__device__ __forceinline__ void store4_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voffset,
+                                           int soffset, float x0, float x1, float x2, float x3) {
+  if constexpr (__is_same(T, float)) {
+    typedef float f32x4_b __attribute__((ext_vector_type(4)));
+    const f32x4_b q = {x0, x1, x2, x3};
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(
+                                               uint32_t __attribute__((ext_vector_type(4))), q),
+                                           rs, voffset, soffset, 0);
+  } else {
+    typedef uint32_t u32x2_b __attribute__((ext_vector_type(2)));
+    const u32x2_b q = {pack2<T>(x0, x1), pack2<T>(x2, x3)};
+    __builtin_amdgcn_raw_buffer_store_b64(q, rs, voffset, soffset, 0);
   }
 }
 
