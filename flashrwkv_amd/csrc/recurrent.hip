@@ -257,12 +257,16 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
   const uint32_t tensor_bytes =
       kBuf ? static_cast<uint32_t>(total_tokens) * static_cast<uint32_t>(num_heads * D) * kEsize
            : 0u;
+  // The ranges differ by a few bytes past each tensor's end (no access goes
+  // there): with identical upper descriptor words the compiler shares them
+  // between the descriptors and copies them back into place before every
+  // load, ten scalar moves per token.
   const auto rs_a = buffer_rsrc(a_ptr, tensor_bytes);
-  const auto rs_w = buffer_rsrc(decay_ptr, tensor_bytes);
-  const auto rs_b = buffer_rsrc(b_ptr, tensor_bytes);
-  const auto rs_k = buffer_rsrc(k_ptr, tensor_bytes);
-  const auto rs_r = buffer_rsrc(r_ptr, tensor_bytes);
-  const auto rs_v = buffer_rsrc(v_ptr, tensor_bytes);
+  const auto rs_w = buffer_rsrc(decay_ptr, tensor_bytes + 4);
+  const auto rs_b = buffer_rsrc(b_ptr, tensor_bytes + 8);
+  const auto rs_k = buffer_rsrc(k_ptr, tensor_bytes + 12);
+  const auto rs_r = buffer_rsrc(r_ptr, tensor_bytes + 16);
+  const auto rs_v = buffer_rsrc(v_ptr, tensor_bytes + 20);
   const auto rs_out = buffer_rsrc(out_ptr, tensor_bytes);
   const uint32_t vo_rows = static_cast<uint32_t>(head * D + row0) * kEsize;
   const uint32_t vo_cols = static_cast<uint32_t>(head * D + col) * kEsize;
