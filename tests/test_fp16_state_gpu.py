@@ -247,6 +247,46 @@ def test_fp16_long_sequences_and_scale():
     _check("state", state.cpu()[active], pool_ref[_np(active)])
 
 
+def test_fp16_decode_long_run_in_place():
+    """The fp16 decode kernel stepped 512 times in place (B=64, H=8, one token
+    per sequence per call, the elapsed pool advanced after each call) against
+    the oracle run over the same tokens as one 512-token sequence per sampled
+    slot: every step's output and the end state."""
+    print("case fp16 decode B=64 H=8, 512 in-place steps", flush=True)
+    batch, heads, steps = 64, 8, 512
+    sampled = (0, 29, 63)
+    g = torch.Generator(device=DEV).manual_seed(20260811)
+    scales = (0.12, 3.5, 0.06, 0.06, 0.06, 0.06)
+    pool0 = (torch.randn((batch, heads, 64, 64), generator=g, device=DEV) * 0.03).half()
+    bias = (torch.randn((heads, 64), generator=g, device=DEV) * 0.2).half()
+    elapsed0 = torch.arange(batch, dtype=torch.int32, device=DEV) * 11
+    state, elapsed = pool0.clone(), elapsed0.clone()
+    cu = torch.arange(batch + 1, dtype=torch.int32, device=DEV)
+    slots = torch.arange(batch, dtype=torch.int32, device=DEV)
+    pick = torch.tensor(sampled, device=DEV)
+    taken = [[] for _ in range(7)]
+    for _ in range(steps):
+        tokens = [(torch.randn((batch, heads, 64), generator=g, device=DEV) * s).half()
+                  for s in scales]
+        y = infer_recurrent_fp16_forward_varlen(
+            *tokens, state_pool=state, elapsed_state_pool=elapsed, cu_seqlens=cu,
+            state_indices=slots, decay_bias=bias, max_seqlen=1)
+        infer_recurrent_fp16_advance_i32_varlen(elapsed, cu, slots, total_tokens=batch)
+        for store, t in zip(taken, (*tokens, y)):
+            store.append(t[pick])
+    torch.cuda.synchronize()
+    series = [torch.stack(v).cpu().numpy() for v in taken]
+    assert torch.equal(elapsed.cpu(), elapsed0.cpu() + steps)
+    for i, slot in enumerate(sampled):
+        tokens = [s[:, i] for s in series[:6]]
+        y_ref, pool_ref = oracle.forward_fp16_state(
+            *tokens, _np(pool0[slot:slot + 1]), _np(elapsed0[slot:slot + 1]),
+            np.array([0, steps], dtype=np.int32), np.zeros(1, dtype=np.int32),
+            bias=_np(bias))
+        _check(f"slot {slot} output", torch.from_numpy(series[6][:, i]), y_ref)
+        _check(f"slot {slot} state", state[slot:slot + 1], pool_ref)
+
+
 def test_fp16_phase_continues_across_calls_bitwise():
     """Tokens split over two calls, the elapsed pool advanced in between, give
     bitwise the one-call result (same launch shape)."""

@@ -310,6 +310,27 @@ def test_fp16_dither_known_answers():
     assert np.max(np.abs(oracle.fp16_dither(np.arange(-5000, 5000)))) <= 2.0**-10
 
 
+def test_fp16_delta_known_answers():
+    """fp16(w - 1 + dither) at two logits with a closed-form retention, worked
+    by hand. x = 30 saturates the sigmoid: w = exp(-e^-1/2) = 0.545239212;
+    x = 0 halves it: w = exp(-e^-1/2 / 2) = 0.738403150. The fp16 grid on
+    [-0.5, -0.25) has step 2^-12 and on [-0.25, 0) step 2^-13:
+      x=30, p=0: -0.454760788 -> -1863 * 2^-12
+      x=30, p=1: -0.454760788 - 7.460e-4 = -0.455506815 -> -1866 * 2^-12
+      x=30, p=2: -0.454760788 + 4.611e-4 = -0.454299718 -> -1861 * 2^-12
+      x=0,  p=0: -0.261596850 -> -1072 * 2^-12
+      x=0,  p=1: -0.262342877 -> -1075 * 2^-12
+    Flipping the dither's sign moves p=1 to -1860 * 2^-12 and p=2 to
+    -1865 * 2^-12; dropping it moves both to -1863 * 2^-12."""
+    x = np.array([30.0, 30.0, 30.0, 0.0, 0.0])
+    phases = np.array([0, 1, 2, 0, 1], dtype=np.int64)
+    expected = np.array([-1863, -1866, -1861, -1072, -1075]) * 2.0**-12
+    assert np.array_equal(oracle.fp16_delta(x, phases), expected)
+    # The bias is added to the logits before the sigmoid.
+    assert np.array_equal(oracle.fp16_delta(x - 30.0, phases, bias=np.full(5, 30.0))[:3],
+                          expected[:3])
+
+
 def _fp16_case(lengths, h, d, *, seed, slots=None, pool_slots=None):
     rng = np.random.default_rng(seed)
     n = sum(lengths)

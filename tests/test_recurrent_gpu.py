@@ -173,6 +173,51 @@ def test_config1_decode_full_shape_three_steps():
         assert oracle.max_rel_error(_np(pool_dev), pool_ref) <= TOL_STATE_16
 
 
+def test_config1_decode_long_run_sampled_heads():
+    """Config 1's decode shape (B=256, H=40, bf16 tokens, fp32 pool) stepped
+    1000 times in place, one token per sequence per call. The state carried
+    across 1000 launches must match the fp64 oracle run over the same tokens
+    as one 1000-token sequence, checked on sampled (sequence, head) pairs at
+    every step's output and at the end state."""
+    print("case config1 decode B=256 H=40, 1000 in-place steps", flush=True)
+    b, h, steps = 256, 40, 1000
+    pairs = ((0, 0), (77, 13), (200, 39), (255, 21))
+    first = _baseline_case([1] * b, h, torch.bfloat16, seed=20260808, state_std=0.1)
+    pool = first["state_pool"].to(DEV)
+    initial = [_np(first["state_pool"][s, hd]) for s, hd in pairs]
+    cu = torch.arange(b + 1, dtype=torch.int32, device=DEV)
+    slots = torch.arange(b, dtype=torch.int32, device=DEV)
+    names = ("r", "w", "k", "v", "a", "b")
+    seq_idx = torch.tensor([s for s, _ in pairs], device=DEV)
+    head_idx = torch.tensor([hd for _, hd in pairs], device=DEV)
+    taken = {n: [] for n in (*names, "y")}
+    for step in range(steps):
+        tok = workloads.make_tokens(b, h, 64, dtype=torch.bfloat16, seed=20260900 + step,
+                                    device=DEV)
+        y = recurrent_forward_internal(
+            tok["r"], tok["w"], tok["k"], tok["v"], tok["a"], tok["b"], state_pool=pool,
+            cu_seqlens=cu, state_indices=slots, decay_mode=DECAY_RAW_W, max_seqlen=1)
+        for n in names:
+            taken[n].append(tok[n][seq_idx, head_idx])
+        taken["y"].append(y[seq_idx, head_idx])
+    torch.cuda.synchronize()
+    series = {n: torch.stack(v).double().cpu().numpy() for n, v in taken.items()}
+    final = _np(pool)
+    assert np.isfinite(final).all()
+    for i, (seq, head) in enumerate(pairs):
+        tokens = [series[n][:, i:i + 1] for n in names]
+        y_ref, s_ref = oracle.forward_varlen(
+            *tokens, initial[i][None, None], np.array([0, steps], dtype=np.int32),
+            np.zeros(1, dtype=np.int32))
+        mine = series["y"][:, i:i + 1]
+        err, rmse = oracle.max_rel_error(mine, y_ref), oracle.relative_rmse(mine, y_ref)
+        state_err = oracle.max_rel_error(final[seq, head][None, None], s_ref)
+        print(f"seq {seq} head {head}: y max-rel {err:.3e} rel-rmse {rmse:.3e} "
+              f"state max-rel {state_err:.3e}", flush=True)
+        assert err <= TOL_Y[torch.bfloat16] and rmse <= REF_RMSE
+        assert state_err <= TOL_STATE_16
+
+
 def test_config2_per_token_kernel_subset_of_batch():
     """The per-token kernel itself at config 2's length (the C entry with
     max_seqlen unknown keeps 16-bit tokens on it): two of the eight sequences
