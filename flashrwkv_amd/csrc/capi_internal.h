@@ -66,3 +66,14 @@ int frwkv_train_recurrent_backward(int io_dtype, int decay_mode, int32_t num_seq
 // Bytes of the fp32 gradient slices the per-token backward needs at this head
 // size (0 when a unit fits one workgroup, i.e. head size 128).
 size_t frwkv_train_slice_bytes(int32_t head_size, int32_t num_heads, int32_t total_tokens);
+
+// The recurrent operator's route for long sequences (chunk_fwd.hip): the
+// split-precision chunk kernel on bf16 tokens, head size 64, fp32 pool.
+// Arguments as frwkv_recurrent_forward's, already checked by it.
+int frwkv_recurrent_chunked_forward(int decay_mode, int32_t num_sequences, int32_t num_heads,
+                                    int32_t total_tokens, int32_t state_pool_size,
+                                    const int32_t* cu_seqlens, const int32_t* state_indices,
+                                    const int32_t* metadata_status, float* state_pool,
+                                    const void* r, const void* decay, const void* decay_bias,
+                                    const void* k, const void* v, const void* a, const void* b,
+                                    void* output, float scale, void* stream);

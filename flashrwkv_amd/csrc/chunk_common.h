@@ -108,6 +108,19 @@ __device__ __forceinline__ void store8_bf16(uint16_t* dst, const float (&x)[8]) 
   reinterpret_cast<uint2*>(dst)[1] = hi;
 }
 
+// store8_bf16 of the split pairs x = hi + lo: hi to dst_hi, lo to dst_lo.
+__device__ __forceinline__ void store8_bf16_split(uint16_t* dst_hi, uint16_t* dst_lo,
+                                                  const float (&x)[8]) {
+  const uint2 p0 = split_bf16x2(x[0], x[1]);
+  const uint2 p1 = split_bf16x2(x[2], x[3]);
+  const uint2 p2 = split_bf16x2(x[4], x[5]);
+  const uint2 p3 = split_bf16x2(x[6], x[7]);
+  reinterpret_cast<uint2*>(dst_hi)[0] = make_uint2(p0.x, p1.x);
+  reinterpret_cast<uint2*>(dst_hi)[1] = make_uint2(p2.x, p3.x);
+  reinterpret_cast<uint2*>(dst_lo)[0] = make_uint2(p0.y, p1.y);
+  reinterpret_cast<uint2*>(dst_lo)[1] = make_uint2(p2.y, p3.y);
+}
+
 // Inclusive-scan step over groups of 8 lanes: lane l adds lane l - N when
 // l % 8 >= N (DPP row shift; the groups never straddle a 16-lane row).
 template <int N>

@@ -69,6 +69,35 @@ struct ChunkSmem {
 };
 static_assert(sizeof(ChunkSmem) <= 80 * 1024, "two workgroups per CU need <= 80 KB of LDS");
 
+// Split-precision variant (the recurrent operator's long sequences): the
+// products whose bf16 rounding dominates the error against the per-token
+// fp32 recurrence are taken on split operands x = hi + lo (split_bf16x2),
+// which leaves about 2^-17 relative error per operand instead of 2^-9:
+//   Ark = Rt Kh^T   from Rt, Kh split (three products: hi hi, lo hi, hi lo),
+//                   stored split, so Ark V is two products;
+//   Lak = At Kh^T   with Kh split (two products);
+//   Rt S0           with Rt and S0 split (three products);
+//   Kh^T V          in the state update, Kh split (two products).
+// The remaining bf16 roundings (At, Bh, Lab, Arb, T, SA) enter through the
+// b sa^T term only. These tiles hold the low halves; the high halves stay in
+// ChunkSmem. The extra 23 KB of LDS leave one workgroup per CU.
+struct PreciseTiles {
+  uint16_t rt_lo[kOpTile];                  // [t][k]
+  uint16_t kh_lo[kOpTile];                  // [t][k]
+  uint16_t ark_lo[kTriBlocks * kTriBlock];  // [t][i]
+};
+struct NoPreciseTiles {};
+template <bool kPrecise>
+struct ExtraTilesOf {
+  using type = NoPreciseTiles;
+};
+template <>
+struct ExtraTilesOf<true> {
+  using type = PreciseTiles;
+};
+template <bool kPrecise>
+using ExtraTiles = typename ExtraTilesOf<kPrecise>::type;
+
 __device__ __forceinline__ const uint16_t* tri_block(const ChunkSmem& sm, int m, int p, int q) {
   return sm.tri[m] + tri_index(p, q) * kTriBlock;
 }
@@ -163,9 +192,9 @@ struct Spans {
 // Per feature, the thread's tokens t0 and t0 + 1 need 2^Gp(t0), 2^G(t0)
 // (= 2^Gp(t0 + 1)), 2^G(t0 + 1), 2^-G(t0), 2^-G(t0 + 1): two exponentials
 // and products with the retentions w = 2^lg (G(t) = Gp(t) + lg(t)).
-template <typename T, DecayMode M, bool kFull>
-__device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bias)[8],
-                         int lo, int hi) {
+template <typename T, DecayMode M, bool kFull, bool kPrecise>
+__device__ Spans prepare(ChunkSmem& sm, ExtraTiles<kPrecise>& ext, const ChunkRows& rows,
+                         const float (&bias)[8], int lo, int hi) {
   const int tid = threadIdx.x;
   const int wave = uniform(tid >> 6);
   const int lane = tid & 63;
@@ -281,10 +310,33 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
     store8_bf16(tile + t0 * kOpStride + 8 * kg, x0);
     store8_bf16(tile + (t0 + 1) * kOpStride + 8 * kg, x1);
   };
+  // Rt and Kh as split pairs in the precise variant.
+  auto split_rows = [&](uint16_t* tile, uint16_t* tile_lo, uint4 q0, uint4 q1,
+                        const float (&f0)[8], const float (&f1)[8]) {
+    float x0[8], x1[8];
+    unpack8<T>(q0, x0);
+    unpack8<T>(q1, x1);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x0[e] *= f0[e];
+      x1[e] *= f1[e];
+    }
+    const int o0 = t0 * kOpStride + 8 * kg, o1 = o0 + kOpStride;
+    store8_bf16_split(tile + o0, tile_lo + o0, x0);
+    store8_bf16_split(tile + o1, tile_lo + o1, x1);
+  };
   tile_rows(sm.at, rows.a[0], rows.a[1], fa0, fa1);
-  tile_rows(sm.rt, rows.r[0], rows.r[1], fr0, fr1);
+  if constexpr (kPrecise) {
+    split_rows(sm.rt, ext.rt_lo, rows.r[0], rows.r[1], fr0, fr1);
+  } else {
+    tile_rows(sm.rt, rows.r[0], rows.r[1], fr0, fr1);
+  }
   tile_rows(sm.bh, rows.b[0], rows.b[1], fd0, fd1);
-  tile_rows(sm.kh, rows.k[0], rows.k[1], fd0, fd1);
+  if constexpr (kPrecise) {
+    split_rows(sm.kh, ext.kh_lo, rows.k[0], rows.k[1], fd0, fd1);
+  } else {
+    tile_rows(sm.kh, rows.k[0], rows.k[1], fd0, fd1);
+  }
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     const int piece = tid + 256 * s;
@@ -319,8 +371,9 @@ __device__ Spans prepare(ChunkSmem& sm, const ChunkRows& rows, const float (&bia
 // issues one sixth of the next chunk's row loads there, so the loads enter
 // the memory system while the products run instead of stalling the wave on
 // a burst of 12 outstanding 16-byte loads.
-template <typename Issue>
-__device__ __forceinline__ void intra_chunk(ChunkSmem& sm, Issue&& issue) {
+template <bool kPrecise, typename Issue>
+__device__ __forceinline__ void intra_chunk(ChunkSmem& sm, ExtraTiles<kPrecise>& ext,
+                                            Issue&& issue) {
   // MFMA phases run at raised wave priority: the other workgroup on the CU
   // is then usually in its VALU-heavy prepare, and the arbiter keeps the
   // matrix pipe fed from this one.
@@ -345,6 +398,7 @@ __device__ __forceinline__ void intra_chunk(ChunkSmem& sm, Issue&& issue) {
 
   auto group = [&](int p, int q, bool with_b, bool with_k, bool diag) {
     f32x4 lab = zero4(), lak = zero4(), arb = zero4(), ark = zero4();
+    f32x4 lak_c = zero4(), ark_c = zero4();  // precise: the low-half products
 #pragma unroll
     for (int c = 0; c < 64; c += 32) {
       const i16x8 xa = lds_operand32<kOpStride>(sm.at, 16 * p + n, c, g);
@@ -358,6 +412,13 @@ __device__ __forceinline__ void intra_chunk(ChunkSmem& sm, Issue&& issue) {
         const i16x8 yk = lds_operand32<kOpStride>(sm.kh, 16 * q + n, c, g);
         lak = mfma32(yk, xa, lak);
         ark = mfma32(yk, xr, ark);
+        if constexpr (kPrecise) {
+          const i16x8 yk_lo = lds_operand32<kOpStride>(ext.kh_lo, 16 * q + n, c, g);
+          const i16x8 xr_lo = lds_operand32<kOpStride>(ext.rt_lo, 16 * p + n, c, g);
+          lak_c = mfma32(yk_lo, xa, lak_c);
+          ark_c = mfma32(yk_lo, xr, ark_c);
+          ark_c = mfma32(yk, xr_lo, ark_c);
+        }
       }
     }
     if (with_b) {
@@ -365,8 +426,22 @@ __device__ __forceinline__ void intra_chunk(ChunkSmem& sm, Issue&& issue) {
       store(kArb, p, q, arb, false, diag);
     }
     if (with_k) {
+      if constexpr (kPrecise) {
+        lak += lak_c;
+        ark += ark_c;
+      }
       store(kLak, p, q, lak, true, diag);
-      store(kArk, p, q, ark, false, diag);
+      if constexpr (kPrecise) {
+        if (diag) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) ark[j] = (4 * g + j <= n) ? ark[j] : 0.0f;
+        }
+        lds_store_transposed_split(sm.tri[kArk] + tri_index(p, q) * kTriBlock,
+                                   ext.ark_lo + tri_index(p, q) * kTriBlock, kTriStride, g, n,
+                                   ark);
+      } else {
+        store(kArk, p, q, ark, false, diag);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -435,11 +510,12 @@ __device__ __forceinline__ void intra_chunk(ChunkSmem& sm, Issue&& issue) {
 // sub_rs / nsub: the first nsub (at most 3) 16-token boundary states of the
 // chunk (after tokens 15, 31, 47) go to sub_rs, one [D][D] fp32 block each;
 // nsub is 0 except for whole-chunk passes of the every-16-tokens layout.
-template <typename T>
-__device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const uint16_t* vtile,
-                           __amdgpu_buffer_rsrc_t out_rs, __amdgpu_buffer_rsrc_t sda_rs,
-                           bool with_sda, uint32_t row_bytes, float scale, int lo, int hi,
-                           __amdgpu_buffer_rsrc_t sub_rs, int nsub) {
+template <typename T, bool kPrecise>
+__device__ void state_pass(const ChunkSmem& sm, const ExtraTiles<kPrecise>& ext, f32x4 (&S)[4],
+                           const uint16_t* vtile, __amdgpu_buffer_rsrc_t out_rs,
+                           __amdgpu_buffer_rsrc_t sda_rs, bool with_sda, uint32_t row_bytes,
+                           float scale, int lo, int hi, __amdgpu_buffer_rsrc_t sub_rs,
+                           int nsub) {
   __builtin_amdgcn_s_setprio(1);  // MFMA phase (see intra_chunk)
   const int tid = threadIdx.x;
   const int w = tid >> 6;
@@ -455,7 +531,16 @@ __device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const uint16_t* v
   // the transposed output product), V slice, then SA as it is solved. A
   // 32-wide K step concatenates two 16-blocks (see mfma32).
   i16x8 s01, s23;
-  {
+  i16x8 s01_lo, s23_lo;  // precise: S0 = hi + lo for the output product
+  if constexpr (kPrecise) {
+    i16x4 h[4], l[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) to_operand_split(S[kb], h[kb], l[kb]);
+    s01 = cat(h[0], h[1]);
+    s23 = cat(h[2], h[3]);
+    s01_lo = cat(l[0], l[1]);
+    s23_lo = cat(l[2], l[3]);
+  } else {
     const i16x4 s0 = to_operand(S[0]), s1 = to_operand(S[1]);
     const i16x4 s2 = to_operand(S[2]), s3 = to_operand(S[3]);
     s01 = cat(s0, s1);
@@ -549,6 +634,10 @@ __device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const uint16_t* v
                         lo32(sab[q]), sn[kb]);
         sn[kb] = mfma32(lo32(lds_operand_tr<kOpStride>(sm.kh, 16 * q, 16 * kb, g, n)),
                         lo32(vs[q]), sn[kb]);
+        if constexpr (kPrecise) {
+          sn[kb] = mfma32(lo32(lds_operand_tr<kOpStride>(ext.kh_lo, 16 * q, 16 * kb, g, n)),
+                          lo32(vs[q]), sn[kb]);
+        }
       }
       if (q < 3 && q < nsub) {
 #pragma unroll
@@ -572,6 +661,12 @@ __device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const uint16_t* v
     for (int kb = 0; kb < 4; ++kb) sn[kb] = mfma32(tr32(sm.kh, kb, 0), v01, sn[kb]);
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) sn[kb] = mfma32(tr32(sm.kh, kb, 32), v23, sn[kb]);
+    if constexpr (kPrecise) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) sn[kb] = mfma32(tr32(ext.kh_lo, kb, 0), v01, sn[kb]);
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) sn[kb] = mfma32(tr32(ext.kh_lo, kb, 32), v23, sn[kb]);
+    }
   }
 #pragma unroll
   for (int pb = 0; pb < 4; ++pb) {
@@ -580,6 +675,29 @@ __device__ void state_pass(const ChunkSmem& sm, f32x4 (&S)[4], const uint16_t* v
 #pragma unroll
   for (int pb = 0; pb < 4; ++pb) {
     y[pb] = mfma32(s23, lds_operand32<kOpStride>(sm.rt, 16 * pb + n, 32, g), y[pb]);
+  }
+  if constexpr (kPrecise) {
+    // Rt S0 = Rt_hi S0_hi + Rt_hi S0_lo + Rt_lo S0_hi.
+#pragma unroll
+    for (int pb = 0; pb < 4; ++pb) {
+      const i16x8 r01 = lds_operand32<kOpStride>(sm.rt, 16 * pb + n, 0, g);
+      const i16x8 r23 = lds_operand32<kOpStride>(sm.rt, 16 * pb + n, 32, g);
+      y[pb] = mfma32(s01_lo, r01, y[pb]);
+      y[pb] = mfma32(s23_lo, r23, y[pb]);
+      y[pb] = mfma32(s01, lds_operand32<kOpStride>(ext.rt_lo, 16 * pb + n, 0, g), y[pb]);
+      y[pb] = mfma32(s23, lds_operand32<kOpStride>(ext.rt_lo, 16 * pb + n, 32, g), y[pb]);
+    }
+    // Ark V with the low half of Ark.
+    auto ark16 = [&](int p, int q) {
+      return lds_operand<kTriStride>(ext.ark_lo + tri_index(p, q) * kTriBlock, n, 4 * g);
+    };
+    auto ark32 = [&](int p, int q) { return cat(ark16(p, q), ark16(p, q + 1)); };
+    y[0] = mfma32(lo32(vs[0]), lo32(ark16(0, 0)), y[0]);
+    y[1] = mfma32(v01, ark32(1, 0), y[1]);
+    y[2] = mfma32(v01, ark32(2, 0), y[2]);
+    y[3] = mfma32(v01, ark32(3, 0), y[3]);
+    y[2] = mfma32(lo32(vs[2]), lo32(ark16(2, 2)), y[2]);
+    y[3] = mfma32(v23, ark32(3, 2), y[3]);
   }
   y[0] = mfma32(lo32(sab[0]), lo32(tri16(kArb, 0, 0)), y[0]);
   y[1] = mfma32(sa01, tri32(kArb, 1, 0), y[1]);
@@ -632,9 +750,11 @@ __device__ __forceinline__ int sequence_by_length_rank(const ChunkFwdParams& p, 
   return hit != 0 ? static_cast<int>(__builtin_ctzll(hit)) : rank;
 }
 
-template <typename T, DecayMode M, typename PoolT>
-__global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdParams p) {
+template <typename T, DecayMode M, typename PoolT, bool kPrecise>
+__global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_kernel(
+    ChunkFwdParams p) {
   __shared__ ChunkSmem sm;
+  __shared__ ExtraTiles<kPrecise> ext;
   using S16 = typename IoTraits<T>::storage;
 
   if (p.status != nullptr && p.status[0] != 0) {
@@ -853,8 +973,9 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
       bool whole = true, first = true;
       int lo = 0, hi = ntok;
       for (;;) {
-        const Spans cur = (lo == 0 && hi == kChunk) ? prepare<T, M, true>(sm, rows, bias, lo, hi)
-                                                    : prepare<T, M, false>(sm, rows, bias, lo, hi);
+        const Spans cur = (lo == 0 && hi == kChunk)
+                              ? prepare<T, M, true, kPrecise>(sm, ext, rows, bias, lo, hi)
+                              : prepare<T, M, false, kPrecise>(sm, ext, rows, bias, lo, hi);
         if (first) {
           first = false;
           spans = cur;
@@ -869,12 +990,12 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
         // chunk the range is empty and the loads return zeros (a skipped
         // load would make the compiler's in-order wait counts too strict).
         if (whole) {
-          intra_chunk(sm, [&](int piece) {
+          intra_chunk<kPrecise>(sm, ext, [&](int piece) {
             load_piece(rows, has_next ? nc0 : c0, has_next ? min(kChunk, nend - nc0) : 0,
                        piece);
           });
         } else {
-          intra_chunk(sm, [](int) {});
+          intra_chunk<kPrecise>(sm, ext, [](int) {});
         }
         {
           const int64_t base = (static_cast<int64_t>(c0) * heads + head) * kHead;
@@ -885,8 +1006,9 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
               p.state_dot_a != nullptr ? p.state_dot_a + base : nullptr,
               p.state_dot_a != nullptr ? 2u * static_cast<uint32_t>(ntok) * row_bytes : 0u);
           const int nsub = (p.boundary16 && whole) ? (ntok - 1) / 16 : 0;
-          state_pass<T>(sm, S, sm.vt, out_rs, sda_rs, p.state_dot_a != nullptr, row_bytes,
-                        p.scale, lo, hi, b16_rs(16, nsub), nsub);
+          state_pass<T, kPrecise>(sm, ext, S, sm.vt, out_rs, sda_rs,
+                                  p.state_dot_a != nullptr, row_bytes, p.scale, lo, hi,
+                                  b16_rs(16, nsub), nsub);
         }
         if (whole) break;
         if (p.boundary16 && hi % 16 == 0 && hi < ntok) store_b16(hi);
@@ -914,10 +1036,10 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_fwd_kernel(ChunkFwdPar
   }
 }
 
-template <typename T, DecayMode M, typename PoolT>
+template <typename T, DecayMode M, typename PoolT, bool kPrecise = false>
 int launch_chunk(const ChunkFwdParams& p, int units, hipStream_t stream) {
-  hipLaunchKernelGGL((chunk_fwd_kernel<T, M, PoolT>), dim3(units), dim3(kChunkThreads), 0,
-                     stream, p);
+  hipLaunchKernelGGL((chunk_fwd_kernel<T, M, PoolT, kPrecise>), dim3(units),
+                     dim3(kChunkThreads), 0, stream, p);
   return check_launch("chunk_fwd_kernel");
 }
 
@@ -1238,4 +1360,50 @@ extern "C" int frwkv_chunk_replay(int io_dtype, int decay_mode, int32_t num_chun
   p.out_elems = static_cast<int64_t>(total_tokens) * num_heads * head_size;
   return dispatch_chunk_io<float>(p, io_dtype, decay_mode, num_chunks * num_heads,
                                   static_cast<hipStream_t>(stream));
+}
+
+// The recurrent operator's route for long sequences (called by
+// frwkv_recurrent_forward): bf16 tokens, head size 64, fp32 pool, the
+// split-precision variant of the chunk kernel. Arguments as there; the
+// caller has checked pointers and sizes.
+int frwkv_recurrent_chunked_forward(int decay_mode, int32_t num_sequences, int32_t num_heads,
+                                    int32_t total_tokens, int32_t state_pool_size,
+                                    const int32_t* cu_seqlens, const int32_t* state_indices,
+                                    const int32_t* metadata_status, float* state_pool,
+                                    const void* r, const void* decay, const void* decay_bias,
+                                    const void* k, const void* v, const void* a, const void* b,
+                                    void* output, float scale, void* stream) {
+  using namespace frwkv;
+  ChunkFwdParams p{};
+  p.num_heads = num_heads;
+  p.longest_first_sequences = num_sequences <= 64 ? num_sequences : 0;
+  p.total_tokens = total_tokens;
+  p.state_slots = state_pool_size;
+  p.cu_seqlens = cu_seqlens;
+  p.slots = state_indices;
+  p.status = metadata_status;
+  p.state = state_pool;
+  p.r = r;
+  p.decay = decay;
+  p.bias = decay_bias;
+  p.k = k;
+  p.v = v;
+  p.a = a;
+  p.b = b;
+  p.out = output;
+  p.scale = scale;
+  p.out_elems = static_cast<int64_t>(total_tokens) * num_heads * kHead;
+  const int units = num_sequences * num_heads;
+  auto s = static_cast<hipStream_t>(stream);
+  if (decay_mode == FRWKV_DECAY_LOGITS) {
+    return launch_chunk<Bf16, DecayMode::kLogits, float, true>(p, units, s);
+  }
+  if (decay_mode == FRWKV_DECAY_RAW_W) {
+    if (decay_bias != nullptr) {
+      return set_error(FRWKV_ERR_INVALID_ARGUMENT,
+                       "decay_bias is only defined for the logits decay mode");
+    }
+    return launch_chunk<Bf16, DecayMode::kRawW, float, true>(p, units, s);
+  }
+  return set_error(FRWKV_ERR_INVALID_ARGUMENT, "unknown decay mode %d", decay_mode);
 }

@@ -590,6 +590,9 @@ int launch_fp16_decode(const RecurrentArgs& p) {
   return check_launch("recurrent_fp16_decode_kernel");
 }
 
+// Smallest max_seqlen that the recurrent operator routes to the chunk kernel.
+constexpr int32_t kChunkedMinSeqlen = 64;
+
 // Token tensors small enough for 32-bit buffer offsets (below 2 GiB).
 template <int D, typename T>
 bool buffer_addressable(const RecurrentArgs& p) {
@@ -879,6 +882,16 @@ extern "C" int frwkv_recurrent_forward(
   }
   if (!__builtin_isfinite(scale)) {
     return set_error(FRWKV_ERR_INVALID_ARGUMENT, "scale must be finite");
+  }
+  // Long bf16 sequences at head size 64 take the split-precision chunk
+  // kernel: its products keep about 2^-17 relative error per operand, so the
+  // outputs stay within the per-token kernel's tolerances, at several times
+  // its speed once sequences span a few chunks.
+  if (io_dtype == FRWKV_DTYPE_BF16 && head_size == 64 && max_seqlen >= kChunkedMinSeqlen) {
+    return frwkv_recurrent_chunked_forward(decay_mode, num_sequences, num_heads, total_tokens,
+                                           state_pool_size, cu_seqlens, state_indices,
+                                           metadata_status, state_pool, r, decay, decay_bias,
+                                           k, v, a, b, output, scale, stream);
   }
   RecurrentArgs p{num_sequences, num_heads, head_size, total_tokens, max_seqlen,
                   state_pool_size, cu_seqlens, state_indices, metadata_status,

@@ -92,12 +92,31 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
+// Two fp32 split into bf16 pairs x = hi + lo: .x packs hi = bf16(x), .y packs
+// lo = bf16(x - hi) (x - hi is exact in fp32), leaving a relative error of
+// about 2^-17 where bf16 alone leaves 2^-9.
+__device__ __forceinline__ uint2 split_bf16x2(float x0, float x1) {
+  const uint32_t hi = pack_bf16x2(x0, x1);
+  const float h0 = __uint_as_float(hi << 16);
+  const float h1 = __uint_as_float(hi & 0xffff0000u);
+  return make_uint2(hi, pack_bf16x2(x0 - h0, x1 - h1));
+}
+
 // C-layout accumulator -> bf16 operand registers (two packed conversions;
 // a single 4-wide vector conversion is split into per-value conversions plus
 // byte permutes when its result feeds an MFMA operand directly).
 __device__ __forceinline__ i16x4 to_operand(f32x4 c) {
   const u32x2 q = {pack_bf16x2(c[0], c[1]), pack_bf16x2(c[2], c[3])};
   return __builtin_bit_cast(i16x4, q);
+}
+
+// The same as a split pair of operands, c = hi + lo (see split_bf16x2).
+__device__ __forceinline__ void to_operand_split(f32x4 c, i16x4& hi, i16x4& lo) {
+  const uint2 p01 = split_bf16x2(c[0], c[1]);
+  const uint2 p23 = split_bf16x2(c[2], c[3]);
+  const u32x2 h = {p01.x, p23.x}, l = {p01.y, p23.y};
+  hi = __builtin_bit_cast(i16x4, h);
+  lo = __builtin_bit_cast(i16x4, l);
 }
 
 // Operand read from an LDS tile: 4 consecutive bf16 of row `row` starting at
@@ -147,6 +166,15 @@ __device__ __forceinline__ void lds_store_transposed(uint16_t* dst, int stride,
   q.x = pack_bf16x2(c[0], c[1]);
   q.y = pack_bf16x2(c[2], c[3]);
   *reinterpret_cast<uint2*>(dst + n * stride + 4 * g) = q;
+}
+
+// lds_store_transposed of the split pair c = hi + lo into two tiles.
+__device__ __forceinline__ void lds_store_transposed_split(uint16_t* dst_hi, uint16_t* dst_lo,
+                                                           int stride, int g, int n, f32x4 c) {
+  const uint2 p01 = split_bf16x2(c[0], c[1]);
+  const uint2 p23 = split_bf16x2(c[2], c[3]);
+  *reinterpret_cast<uint2*>(dst_hi + n * stride + 4 * g) = make_uint2(p01.x, p23.x);
+  *reinterpret_cast<uint2*>(dst_lo + n * stride + 4 * g) = make_uint2(p01.y, p23.y);
 }
 
 }  // namespace frwkv

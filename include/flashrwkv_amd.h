@@ -96,9 +96,15 @@ int frwkv_metadata_validate(const int32_t* cu_seqlens,
  * [H*D] of io_dtype (logits mode only). metadata_status is the status word of
  * frwkv_metadata_validate: when it is non-zero at run time the kernels fill
  * output with NaN and leave the pool untouched. max_seqlen is the longest
- * sequence (<= 0: unknown); it selects the launch shape of the per-token
- * kernel (one wave per state for decode, four for longer sequences), never
- * the result. The arithmetic stays fp32 per token whatever the length.
+ * sequence (<= 0: unknown). It selects the kernel:
+ *   - unknown, or below 64, or tokens other than bf16, or head size other
+ *     than 64: the per-token kernel, fp32 arithmetic per token (one wave per
+ *     state for decode, four for longer sequences);
+ *   - bf16 tokens, head size 64, max_seqlen >= 64: the chunked form on
+ *     split-bf16 MFMA products (about 2^-17 relative error per split
+ *     operand). Outputs and states then stay within the reference's
+ *     relative-RMSE gate for this operator (0.002, reference
+ *     tests/fixtures/tolerances-v1.json:9-12), at several times the speed.
  */
 int frwkv_recurrent_forward(int io_dtype, int decay_mode, int32_t num_sequences,
                             int32_t num_heads, int32_t head_size,
