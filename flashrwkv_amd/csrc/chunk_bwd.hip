@@ -686,34 +686,36 @@ __device__ __forceinline__ void adjoint_chain(BwdSmem& sm, const f32x4 (&S0)[4],
   }
 }
 
-// The four gradient matrices, 40 (matrix, block pair) items, five per wave
-// (item wave + 8 i): M[t][i] = sum_v X[t][v] Y[i][v] (X = dYs or dZ, Y = SA
-// or V, all four [t][v] tiles), computed as M^T in C layout and stored
-// [t][i]. The items differ only in their tile pointers, so the five are
-// unrolled without branches and their reads overlap. Ends with a barrier.
+// The four gradient matrices, 40 (matrix, block) items: M[t][i] = sum_v
+// X[t][v] Y[i][v] (X = dYs or dZ, Y = SA or V, all four [t][v] tiles),
+// computed as M^T in C layout and stored [t][i]. Wave w takes matrix w / 2
+// and the block rows {3, 0} (w even) or {2, 1} (w odd): five blocks, whose
+// operands are two row blocks of X and the four (three) row blocks of Y, each
+// read from LDS once (6 or 5 operand reads for 5 products, instead of 10).
+// Ends with a barrier.
 __device__ __forceinline__ void gradient_matrices(BwdSmem& sm) {
   const int tid = lane_tid();
   const int wave = uniform(tid >> 6);
   const int lane = tid & 63;
   const int g = lane >> 4, n = lane & 15;
+  const int m = wave >> 1;  // kGArb, kGArk, kGLab, kGLak
+  const bool odd = (wave & 1) != 0;
+  const bool from_dz = m >= 2;
+  const uint16_t* xt = from_dz ? sm.dz : sm.dy;
+  const uint16_t* yt = (m & 1) != 0 ? sm.vv : sm.sa;
+  const int pa = odd ? 2 : 3, pz = odd ? 1 : 0;
   __builtin_amdgcn_s_setprio(1);
+  i16x8 xa[2], xz[2], y[4][2];
 #pragma unroll
-  for (int i = 0; i < 5; ++i) {
-    const int item = wave + 8 * i;
-    const int m = item / 10;  // kGArb, kGArk, kGLab, kGLak
-    const int pair = item % 10;
-    const int pb = pair < 1 ? 0 : pair < 3 ? 1 : pair < 6 ? 2 : 3;
-    const int q = pair - (pb * (pb + 1)) / 2;
-    const bool from_dz = m >= 2;
-    const uint16_t* xt = from_dz ? sm.dz : sm.dy;
-    const uint16_t* yt = (m & 1) != 0 ? sm.vv : sm.sa;
-    f32x4 mt = zero4();
+  for (int h = 0; h < 2; ++h) {
+    xa[h] = lds_operand32<kOpStride>(xt, 16 * pa + n, 32 * h, g);
+    xz[h] = lds_operand32<kOpStride>(xt, 16 * pz + n, 32 * h, g);
 #pragma unroll
-    for (int c = 0; c < 64; c += 32) {
-      const i16x8 x = lds_operand32<kOpStride>(xt, 16 * pb + n, c, g);
-      const i16x8 y = lds_operand32<kOpStride>(yt, 16 * q + n, c, g);
-      mt = mfma32(y, x, mt);  // lane (g, n): M[t = 16 pb + n][i = 16 q + 4g + j]
-    }
+    for (int q = 0; q < 4; ++q) y[q][h] = lds_operand32<kOpStride>(yt, 16 * q + n, 32 * h, g);
+  }
+  auto block = [&](const i16x8 (&x)[2], int pb, int q) {
+    f32x4 mt = mfma32(y[q][0], x[0], zero4());  // lane (g, n): M[16 pb + n][16 q + 4g + j]
+    mt = mfma32(y[q][1], x[1], mt);
     if (pb == q) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -722,6 +724,14 @@ __device__ __forceinline__ void gradient_matrices(BwdSmem& sm) {
       }
     }
     lds_store_transposed(sm.u.grad[m] + tri_index(pb, q) * kTriBlock, kTriStride, g, n, mt);
+  };
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (q <= pa) block(xa, pa, q);
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    if (q <= pz) block(xz, pz, q);
   }
   __builtin_amdgcn_s_setprio(0);
   __syncthreads();
