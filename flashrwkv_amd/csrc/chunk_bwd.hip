@@ -778,10 +778,10 @@ __device__ void run_backward_step(BwdSmem& sm, const ChunkBwdParams& p, const To
   gradient_matrices(sm);
 
   // ----------------------------------------------------------- tokens --
-  // Each feature half u (features f0 + 4u .. +3 of the lane) in two passes
-  // that share no operand: pass A forms dRt, dAt (products with S0, Bh^T,
-  // Kh^T), pass B dBc = dBh + g dBt and dKc = dKh + g dKt (products with dS,
-  // At^T, Rt^T). Only one pass's four accumulators are live at a time.
+  // Two passes that share no operand: pass A forms dRt, dAt (products with
+  // S0, Bh^T, Kh^T), pass B dBc = dBh + g dBt and dKc = dKh + g dKt (products
+  // with dS, At^T, Rt^T), each for both of the lane's feature quarters u
+  // (features f0 + 4u .. +3). Only one pass's accumulators are live at a time.
   auto Gf = [&](int m, int pp, int q) {  // B[k = i][n = t]: block (pp, q) as stored
     return lds_operand<kTriStride>(tri_blk(sm.u.grad[m], pp, q), n, 4 * g);
   };
@@ -806,146 +806,179 @@ __device__ void run_backward_step(BwdSmem& sm, const ChunkBwdParams& p, const To
   // gradient's in-block suffix sum of e1 + e2 minus e2.
   uint32_t wr[4], wa[4], wb[4], wk[4];
   float sfx[8];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int c0 = 32 * hf + 4 * u;
-    const int fb = f0 + 4 * u;
-    // Decay factors of the lane's 4 features, recomputed exactly as in
-    // prepare: the row's product scan times the earlier blocks' products.
-    float carry[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+  // Decay factors of the lane's 8 features, recomputed exactly as in
+  // prepare: the row's product scan times the earlier blocks' products.
+  float up[8], upp[8];
+  {
+    float carry[8] = {1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       if (q < pt) {
-        const float4 c = *reinterpret_cast<const float4*>(&sm.blk[q][fb]);
-        carry[0] *= c.x;
-        carry[1] *= c.y;
-        carry[2] *= c.z;
-        carry[3] *= c.w;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const float4 c = *reinterpret_cast<const float4*>(&sm.blk[q][f0 + 4 * u]);
+          carry[4 * u + 0] *= c.x;
+          carry[4 * u + 1] *= c.y;
+          carry[4 * u + 2] *= c.z;
+          carry[4 * u + 3] *= c.w;
+        }
       }
     }
-    float upp[4], up[4], dn[4];
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int e = 4 * u + jj;
+    for (int e = 0; e < 8; ++e) {
       float xin = raw(cur.w, e);
       if constexpr (M == DecayMode::kLogits) xin += raw(bias, e);
       const float wv = on ? clamped_retention<M>(xin) : 1.0f;
+      // Both scans run in every lane: the lane before the first one of a
+      // sub-piece range holds the empty product that the exclusive scan reads.
       const float Gi = prefix16_mul(wv, n);
-      const float g = Gi * carry[jj];
-      const float gp = exclusive16(Gi, n) * carry[jj];
-      up[jj] = on ? g : 0.0f;
-      upp[jj] = on ? gp : 0.0f;
-      dn[jj] = on ? __builtin_amdgcn_rcpf(g) : 0.0f;
+      const float Ge = exclusive16(Gi, n);
+      up[e] = on ? Gi * carry[e] : 0.0f;
+      upp[e] = on ? Ge * carry[e] : 0.0f;
     }
-    float e12[4];
-
-    // ---- pass A: dRt = dYs S0^T + dArb Bh + dArk Kh, dAt = dZ S0^T + dLab Bh + dLak Kh.
-      __builtin_amdgcn_s_setprio(1);
-    {
-      f32x4 acc_r = zero4(), acc_a = zero4();
+  }
+  // Both feature quarters u (features f0 + 4u .. +3) in each pass: the
+  // operands that do not depend on u (dYs, dZ, SA, V rows and the gradient
+  // blocks) are read once for both.
+  float e12[8];
+  __builtin_amdgcn_s_setprio(1);
+  // ---- pass A: dRt = dYs S0^T + dArb Bh + dArk Kh, dAt = dZ S0^T + dLab Bh + dLak Kh.
+  {
+    f32x4 acc_r[2] = {zero4(), zero4()}, acc_a[2] = {zero4(), zero4()};
 #pragma unroll
-      for (int c = 0; c < 64; c += 32) {
-        const i16x8 s0a = tr32_q8<kOpStride>(sm.s0, c, c0, g, n);
-        acc_r = mfma32(s0a, lds_operand32<kOpStride>(sm.dy, t, c, g), acc_r);
-        acc_a = mfma32(s0a, lds_operand32<kOpStride>(sm.dz, t, c, g), acc_a);
+    for (int c = 0; c < 64; c += 32) {
+      const i16x8 dyo = lds_operand32<kOpStride>(sm.dy, t, c, g);
+      const i16x8 dzo = lds_operand32<kOpStride>(sm.dz, t, c, g);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const i16x8 s0a = tr32_q8<kOpStride>(sm.s0, c, 32 * hf + 4 * u, g, n);
+        acc_r[u] = mfma32(s0a, dyo, acc_r[u]);
+        acc_a[u] = mfma32(s0a, dzo, acc_a[u]);
       }
-      // Source blocks q <= pt: A = Bh^T / Kh^T (rows: features), B = the
-      // gradient blocks (pt, q) as stored.
-      auto src = [&](int q, bool pair) {
+    }
+    // Source blocks q <= pt: A = Bh^T / Kh^T (rows: features), B = the
+    // gradient blocks (pt, q) as stored.
+    auto src = [&](int q, bool pair) {
+      auto gb = [&](int m) {
+        return pair ? cat(Gf(m, pt, q), Gf(m, pt, q + 1)) : lo32(Gf(m, pt, q));
+      };
+      const i16x8 g_arb = gb(kGArb), g_ark = gb(kGArk), g_lab = gb(kGLab), g_lak = gb(kGLak);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int c0 = 32 * hf + 4 * u;
         const i16x8 bq = pair ? cat(lds_tr_q8<kOpStride>(sm.bh, 16 * q, c0, g, n),
                                     lds_tr_q8<kOpStride>(sm.bh, 16 * q + 16, c0, g, n))
                               : lo32(lds_tr_q8<kOpStride>(sm.bh, 16 * q, c0, g, n));
         const i16x8 kq = pair ? cat(lds_tr_q8<kOpStride>(sm.kh, 16 * q, c0, g, n),
                                     lds_tr_q8<kOpStride>(sm.kh, 16 * q + 16, c0, g, n))
                               : lo32(lds_tr_q8<kOpStride>(sm.kh, 16 * q, c0, g, n));
-        auto gb = [&](int m) {
-          return pair ? cat(Gf(m, pt, q), Gf(m, pt, q + 1)) : lo32(Gf(m, pt, q));
-        };
-        acc_r = mfma32(bq, gb(kGArb), acc_r);
-        acc_r = mfma32(kq, gb(kGArk), acc_r);
-        acc_a = mfma32(bq, gb(kGLab), acc_a);
-        acc_a = mfma32(kq, gb(kGLak), acc_a);
-      };
-      if (pt == 0) {
-        src(0, false);
-      } else if (pt == 1) {
-        src(0, true);
-      } else if (pt == 2) {
-        src(0, true);
-        src(2, false);
-      } else {
-        src(0, true);
-        src(2, true);
+        acc_r[u] = mfma32(bq, g_arb, acc_r[u]);
+        acc_r[u] = mfma32(kq, g_ark, acc_r[u]);
+        acc_a[u] = mfma32(bq, g_lab, acc_a[u]);
+        acc_a[u] = mfma32(kq, g_lak, acc_a[u]);
       }
+    };
+    if (pt == 0) {
+      src(0, false);
+    } else if (pt == 1) {
+      src(0, true);
+    } else if (pt == 2) {
+      src(0, true);
+      src(2, false);
+    } else {
+      src(0, true);
+      src(2, true);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int fb = f0 + 4 * u;
       const uint2 rt4 = tile4(sm.rt, fb), at4 = tile4(sm.at, fb);
       float gr4[4], ga4[4];
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        gr4[jj] = acc_r[jj] * up[jj];
-        ga4[jj] = acc_a[jj] * upp[jj];
-        const float e2 = acc_a[jj] * half(at4, jj);
-        e12[jj] = acc_r[jj] * half(rt4, jj) + e2;
-        sfx[4 * u + jj] = -e2;
+        const int e = 4 * u + jj;
+        gr4[jj] = acc_r[u][jj] * up[e];
+        ga4[jj] = acc_a[u][jj] * upp[e];
+        const float e2 = acc_a[u][jj] * half(at4, jj);
+        e12[e] = acc_r[u][jj] * half(rt4, jj) + e2;
+        sfx[e] = -e2;
       }
       wr[2 * u] = pack2<T>(gr4[0], gr4[1]);
       wr[2 * u + 1] = pack2<T>(gr4[2], gr4[3]);
       wa[2 * u] = pack2<T>(ga4[0], ga4[1]);
       wa[2 * u + 1] = pack2<T>(ga4[2], ga4[3]);
     }
+  }
 
-    // ---- pass B: dBc = dLab^T At + dArb^T Rt + g (SA dS^T), dKc likewise
-    // with dLak, dArk and V.
-      {
-      f32x4 acc_b = zero4(), acc_k = zero4(), acc_bt = zero4(), acc_kt = zero4();
+  // ---- pass B: dBc = dLab^T At + dArb^T Rt + g (SA dS^T), dKc likewise
+  // with dLak, dArk and V.
+  {
+    f32x4 acc_b[2] = {zero4(), zero4()}, acc_k[2] = {zero4(), zero4()};
+    f32x4 acc_bt[2] = {zero4(), zero4()}, acc_kt[2] = {zero4(), zero4()};
 #pragma unroll
-      for (int c = 0; c < 64; c += 32) {
-        const i16x8 dsa = tr32_q8<kOpStride>(sm.ds, c, c0, g, n);
-        acc_bt = mfma32(dsa, lds_operand32<kOpStride>(sm.sa, t, c, g), acc_bt);
-        acc_kt = mfma32(dsa, lds_operand32<kOpStride>(sm.vv, t, c, g), acc_kt);
+    for (int c = 0; c < 64; c += 32) {
+      const i16x8 sao = lds_operand32<kOpStride>(sm.sa, t, c, g);
+      const i16x8 vvo = lds_operand32<kOpStride>(sm.vv, t, c, g);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const i16x8 dsa = tr32_q8<kOpStride>(sm.ds, c, 32 * hf + 4 * u, g, n);
+        acc_bt[u] = mfma32(dsa, sao, acc_bt[u]);
+        acc_kt[u] = mfma32(dsa, vvo, acc_kt[u]);
       }
-      // Target blocks qt >= pt: A = At^T / Rt^T, B = the gradient blocks
-      // (qt, pt) transposed.
-      auto dst = [&](int qt, bool pair) {
+    }
+    // Target blocks qt >= pt: A = At^T / Rt^T, B = the gradient blocks
+    // (qt, pt) transposed.
+    auto dst = [&](int qt, bool pair) {
+      auto gb = [&](int m) {
+        return pair ? cat(Gt(m, qt, pt), Gt(m, qt + 1, pt)) : lo32(Gt(m, qt, pt));
+      };
+      const i16x8 g_lab = gb(kGLab), g_arb = gb(kGArb), g_lak = gb(kGLak), g_ark = gb(kGArk);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int c0 = 32 * hf + 4 * u;
         const i16x8 aq = pair ? cat(lds_tr_q8<kOpStride>(sm.at, 16 * qt, c0, g, n),
                                     lds_tr_q8<kOpStride>(sm.at, 16 * qt + 16, c0, g, n))
                               : lo32(lds_tr_q8<kOpStride>(sm.at, 16 * qt, c0, g, n));
         const i16x8 rq = pair ? cat(lds_tr_q8<kOpStride>(sm.rt, 16 * qt, c0, g, n),
                                     lds_tr_q8<kOpStride>(sm.rt, 16 * qt + 16, c0, g, n))
                               : lo32(lds_tr_q8<kOpStride>(sm.rt, 16 * qt, c0, g, n));
-        auto gb = [&](int m) {
-          return pair ? cat(Gt(m, qt, pt), Gt(m, qt + 1, pt)) : lo32(Gt(m, qt, pt));
-        };
-        acc_b = mfma32(aq, gb(kGLab), acc_b);
-        acc_b = mfma32(rq, gb(kGArb), acc_b);
-        acc_k = mfma32(aq, gb(kGLak), acc_k);
-        acc_k = mfma32(rq, gb(kGArk), acc_k);
-      };
-      if (pt == 0) {
-        dst(0, true);
-        dst(2, true);
-      } else if (pt == 1) {
-        dst(1, false);
-        dst(2, true);
-      } else if (pt == 2) {
-        dst(2, true);
-      } else {
-        dst(3, false);
+        acc_b[u] = mfma32(aq, g_lab, acc_b[u]);
+        acc_b[u] = mfma32(rq, g_arb, acc_b[u]);
+        acc_k[u] = mfma32(aq, g_lak, acc_k[u]);
+        acc_k[u] = mfma32(rq, g_ark, acc_k[u]);
       }
-      __builtin_amdgcn_s_setprio(0);
+    };
+    if (pt == 0) {
+      dst(0, true);
+      dst(2, true);
+    } else if (pt == 1) {
+      dst(1, false);
+      dst(2, true);
+    } else if (pt == 2) {
+      dst(2, true);
+    } else {
+      dst(3, false);
+    }
+    __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int fb = f0 + 4 * u;
       const float4 gc4 = *reinterpret_cast<const float4*>(&sm.gc[fb]);
       const float gcv[4] = {gc4.x, gc4.y, gc4.z, gc4.w};
       const uint2 bh4 = tile4(sm.bh, fb), kh4 = tile4(sm.kh, fb);
       float gb4[4], gk4[4];
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        const float dBc = acc_b[jj] + gcv[jj] * acc_bt[jj];
-        const float dKc = acc_k[jj] + gcv[jj] * acc_kt[jj];
-        gb4[jj] = dn[jj] * dBc;
-        gk4[jj] = dn[jj] * dKc;
+        const int e = 4 * u + jj;
+        const float dn = on ? __builtin_amdgcn_rcpf(up[e]) : 0.0f;
+        const float dBc = acc_b[u][jj] + gcv[jj] * acc_bt[u][jj];
+        const float dKc = acc_k[u][jj] + gcv[jj] * acc_kt[u][jj];
+        gb4[jj] = dn * dBc;
+        gk4[jj] = dn * dKc;
         const float bh_v = half(bh4, jj), kh_v = half(kh4, jj);
-        const float suf = suffix16(e12[jj] - dBc * bh_v - dKc * kh_v);
-        const float tot3 = suffix16(gcv[jj] * (acc_bt[jj] * bh_v + acc_kt[jj] * kh_v));
-        sfx[4 * u + jj] += suf;
+        const float suf = suffix16(e12[e] - dBc * bh_v - dKc * kh_v);
+        const float tot3 = suffix16(gcv[jj] * (acc_bt[u][jj] * bh_v + acc_kt[u][jj] * kh_v));
+        sfx[e] += suf;
         if (n == 0) {
           sm.car1[pt][fb + jj] = suf;
           sm.car3[pt][fb + jj] = tot3;
