@@ -613,6 +613,35 @@ __device__ __forceinline__ void adjoint_chain(BwdSmem& sm, const f32x4 (&S0)[4],
   dsa[2] = mfma32(cat(Lt(kArb, 2, 2), Lt(kArb, 3, 2)), dy23, dsa[2]);
   dsa[3] = mfma32(lo32(Lt(kArb, 3, 3)), lo32(dys[3]), dsa[3]);
 
+  // The parts of dV and dS0 that do not need dZ first, so their products
+  // fill the latencies of the dZ chain:
+  //   dV^T  <- (g o dS)^T Kh^T + sum_{q>=pb} dYs_q^T Ark(q, pb),
+  //   dS0   <- g o dS + Rt^T dYs.
+  auto Lb = [&](int m, int q, int pb) {  // B[k = t][n = i] = M[t][i] of block (q, pb)
+    return lds_operand_tr<kTriStride>(tri_blk(sm.u.f.tri[m], q, pb), 0, 0, g, n);
+  };
+  f32x4 dvt[4];
+#pragma unroll
+  for (int pb = 0; pb < 4; ++pb)
+    dvt[pb] = mfma32(gds01, lds_operand32<kOpStride>(sm.kh, 16 * pb + n, 0, g), zero4());
+#pragma unroll
+  for (int pb = 0; pb < 4; ++pb)
+    dvt[pb] = mfma32(gds23, lds_operand32<kOpStride>(sm.kh, 16 * pb + n, 32, g), dvt[pb]);
+  dvt[0] = mfma32(dy01, cat(Lb(kArk, 0, 0), Lb(kArk, 1, 0)), dvt[0]);
+  dvt[0] = mfma32(dy23, cat(Lb(kArk, 2, 0), Lb(kArk, 3, 0)), dvt[0]);
+  dvt[1] = mfma32(lo32(dys[1]), lo32(Lb(kArk, 1, 1)), dvt[1]);
+  dvt[1] = mfma32(dy23, cat(Lb(kArk, 2, 1), Lb(kArk, 3, 1)), dvt[1]);
+  dvt[2] = mfma32(dy23, cat(Lb(kArk, 2, 2), Lb(kArk, 3, 2)), dvt[2]);
+  dvt[3] = mfma32(lo32(dys[3]), lo32(Lb(kArk, 3, 3)), dvt[3]);
+  f32x4 ds0[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    const float4 gc4 = *reinterpret_cast<const float4*>(&sm.gc[16 * kb + 4 * g]);
+    f32x4 acc = {gc4.x * dS[kb][0], gc4.y * dS[kb][1], gc4.z * dS[kb][2], gc4.w * dS[kb][3]};
+    acc = mfma32(tr32<kOpStride>(sm.rt, 0, 16 * kb, g, n), dy01, acc);
+    ds0[kb] = mfma32(tr32<kOpStride>(sm.rt, 32, 16 * kb, g, n), dy23, acc);
+  }
+
   // dZ = T^T dSA: dZ_p = T_pp^T (dSA_p + sum_{q>p} Lab^T(q, p) dZ_q).
   auto Tt = [&](int pb) {
     return lds_operand_tr<kTriStride>(sm.u.f.tinv[pb], 0, 0, g, n);
@@ -637,50 +666,26 @@ __device__ __forceinline__ void adjoint_chain(BwdSmem& sm, const f32x4 (&S0)[4],
   for (int pb = 0; pb < 4; ++pb)
     lds_store_rows(sm.dz + (16 * pb) * kOpStride + 16 * cs, kOpStride, g, n, dz[pb]);
 
-  // dV^T (rows v of this slab, cols t of block pb):
-  //   (g o dS)^T Kh^T + sum_{q>=pb} (dYs_q^T Ark(q, pb) + dZ_q^T Lak(q, pb)).
-  // The C-layout operands of (g o dS), dYs and dZ serve as A operands of their
-  // transposes; lane (g, n) ends with dV[16 pb + n][16 cs + 4g .. +3].
-  {
-    auto Lb = [&](int m, int q, int pb) {  // B[k = t][n = i] = M[t][i] of block (q, pb)
-      return lds_operand_tr<kTriStride>(tri_blk(sm.u.f.tri[m], q, pb), 0, 0, g, n);
-    };
-    f32x4 dvt[4];
+  // dV^T (rows v of this slab, cols t of block pb): the dZ terms
+  // sum_{q>=pb} dZ_q^T Lak(q, pb); lane (g, n) ends with dV[16 pb + n][16 cs + 4g .. +3].
+  dvt[0] = mfma32(dz01, cat(Lb(kLak, 0, 0), Lb(kLak, 1, 0)), dvt[0]);
+  dvt[0] = mfma32(dz23, cat(Lb(kLak, 2, 0), Lb(kLak, 3, 0)), dvt[0]);
+  dvt[1] = mfma32(lo32(dzb[1]), lo32(Lb(kLak, 1, 1)), dvt[1]);
+  dvt[1] = mfma32(dz23, cat(Lb(kLak, 2, 1), Lb(kLak, 3, 1)), dvt[1]);
+  dvt[2] = mfma32(dz23, cat(Lb(kLak, 2, 2), Lb(kLak, 3, 2)), dvt[2]);
+  dvt[3] = mfma32(lo32(dzb[3]), lo32(Lb(kLak, 3, 3)), dvt[3]);
 #pragma unroll
-    for (int pb = 0; pb < 4; ++pb)
-      dvt[pb] = mfma32(gds01, lds_operand32<kOpStride>(sm.kh, 16 * pb + n, 0, g), zero4());
-#pragma unroll
-    for (int pb = 0; pb < 4; ++pb)
-      dvt[pb] = mfma32(gds23, lds_operand32<kOpStride>(sm.kh, 16 * pb + n, 32, g), dvt[pb]);
-    dvt[0] = mfma32(dy01, cat(Lb(kArk, 0, 0), Lb(kArk, 1, 0)), dvt[0]);
-    dvt[0] = mfma32(dy23, cat(Lb(kArk, 2, 0), Lb(kArk, 3, 0)), dvt[0]);
-    dvt[0] = mfma32(dz01, cat(Lb(kLak, 0, 0), Lb(kLak, 1, 0)), dvt[0]);
-    dvt[0] = mfma32(dz23, cat(Lb(kLak, 2, 0), Lb(kLak, 3, 0)), dvt[0]);
-    dvt[1] = mfma32(lo32(dys[1]), lo32(Lb(kArk, 1, 1)), dvt[1]);
-    dvt[1] = mfma32(dy23, cat(Lb(kArk, 2, 1), Lb(kArk, 3, 1)), dvt[1]);
-    dvt[1] = mfma32(lo32(dzb[1]), lo32(Lb(kLak, 1, 1)), dvt[1]);
-    dvt[1] = mfma32(dz23, cat(Lb(kLak, 2, 1), Lb(kLak, 3, 1)), dvt[1]);
-    dvt[2] = mfma32(dy23, cat(Lb(kArk, 2, 2), Lb(kArk, 3, 2)), dvt[2]);
-    dvt[2] = mfma32(dz23, cat(Lb(kLak, 2, 2), Lb(kLak, 3, 2)), dvt[2]);
-    dvt[3] = mfma32(lo32(dys[3]), lo32(Lb(kArk, 3, 3)), dvt[3]);
-    dvt[3] = mfma32(lo32(dzb[3]), lo32(Lb(kLak, 3, 3)), dvt[3]);
-#pragma unroll
-    for (int pb = 0; pb < 4; ++pb) {
-      uint2 q;
-      q.x = pack2<T>(dvt[pb][0], dvt[pb][1]);
-      q.y = pack2<T>(dvt[pb][2], dvt[pb][3]);
-      *reinterpret_cast<uint2*>(sm.dv + (16 * pb + n) * kOpStride + 16 * cs + 4 * g) = q;
-    }
+  for (int pb = 0; pb < 4; ++pb) {
+    uint2 q;
+    q.x = pack2<T>(dvt[pb][0], dvt[pb][1]);
+    q.y = pack2<T>(dvt[pb][2], dvt[pb][3]);
+    *reinterpret_cast<uint2*>(sm.dv + (16 * pb + n) * kOpStride + 16 * cs + 4 * g) = q;
   }
 
   // dS0 = g o dS + Rt^T dYs + At^T dZ.
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
-    const float4 gc4 = *reinterpret_cast<const float4*>(&sm.gc[16 * kb + 4 * g]);
-    f32x4 acc = {gc4.x * dS[kb][0], gc4.y * dS[kb][1], gc4.z * dS[kb][2], gc4.w * dS[kb][3]};
-    acc = mfma32(tr32<kOpStride>(sm.rt, 0, 16 * kb, g, n), dy01, acc);
-    acc = mfma32(tr32<kOpStride>(sm.rt, 32, 16 * kb, g, n), dy23, acc);
-    acc = mfma32(tr32<kOpStride>(sm.at, 0, 16 * kb, g, n), dz01, acc);
+    f32x4 acc = mfma32(tr32<kOpStride>(sm.at, 0, 16 * kb, g, n), dz01, ds0[kb]);
     acc = mfma32(tr32<kOpStride>(sm.at, 32, 16 * kb, g, n), dz23, acc);
     sm.dstash[cs][kb][lane] = acc;
   }
