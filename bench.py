@@ -48,11 +48,12 @@ _COPY_KIB = 262144.0
 _COPY_FETCH_KIB = 131084.4
 _COPY_WRITE_KIB = 262144.0
 PMC_KIB = {  # kernel -> (FETCH_SIZE, WRITE_SIZE)
-    "recurrent_fp32_kernel<64,64,64,Bf16,kRawW>": (85811.4, 165210.7),
-    "chunk_fwd_kernel<Bf16,kRawW,float>": (790713.2, 270341.6),
-    "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": (790727.9, 1319388.2),
-    "chunk_bwd_kernel<Bf16,kRawW>": (1187648.9, 1636895.4),
-    "recurrent_fp16_decode_kernel": (44891.9, 83212.9),
+    "recurrent_fp32_kernel<64,64,64,Bf16,kRawW>": (85811.4, 165208.9),
+    "chunk_fwd_kernel<Bf16,kRawW,float>": (790711.1, 270341.0),
+    "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": (790727.5, 1319370.2),
+    "chunk_fwd_kernel<Bf16,kRawW,float>/precise": (395464.6, 135168.0),
+    "chunk_bwd_kernel<Bf16,kRawW>": (1187909.2, 1637060.8),
+    "recurrent_fp16_decode_kernel": (44876.3, 83226.3),
 }
 
 # The kernel sources PMC_KIB was measured on: sha256 over these files, in
@@ -61,7 +62,7 @@ PMC_KIB = {  # kernel -> (FETCH_SIZE, WRITE_SIZE)
 PMC_SOURCES = ("flashrwkv_amd/csrc/recurrent.hip", "flashrwkv_amd/csrc/chunk_fwd.hip",
                "flashrwkv_amd/csrc/chunk_bwd.hip", "flashrwkv_amd/csrc/chunk_common.h",
                "flashrwkv_amd/csrc/wkv7_device.h", "flashrwkv_amd/csrc/wkv7_mfma.h")
-PMC_SOURCES_SHA = "eb75bacfd38ceb85216cd09806eb59a531cf1e613a52b84cc279a3ef4ab80499"
+PMC_SOURCES_SHA = "dfd9acbcc1552d3ed685f365f5e16b5c1cd15c070c11e9a44136c4e0afd2555f"
 
 
 def kernel_sources_sha() -> str:
@@ -998,7 +999,7 @@ def bench_recurrent_long(args):
 
     import flashrwkv_amd
     from flashrwkv_amd import workloads
-    from flashrwkv_amd.tmix.wkv7 import DECAY_RAW_W
+    from flashrwkv_amd.tmix.wkv7 import DECAY_RAW_W, prepare_recurrent_metadata
 
     if flashrwkv_amd._C is None:
         raise SystemExit("flashrwkv_amd native library is not built")
@@ -1026,8 +1027,12 @@ def bench_recurrent_long(args):
         end.synchronize()
         return start.elapsed_time(end) / reps
 
+    # The operator with a validated-metadata ticket (no per-call validation
+    # launch), as a serving loop calls it.
+    ticket = prepare_recurrent_metadata(cu, slots, total_tokens=n_tok, state_pool_size=batch,
+                                        max_seqlen=t_len)
     op_ms = timed(lambda: ops.recurrent_fp32_forward_internal(
-        cu, slots, pool, *args_tok, out, 1.0, DECAY_RAW_W, None, None, t_len), 10)
+        cu, slots, pool, *args_tok, out, 1.0, DECAY_RAW_W, None, ticket, t_len), 10)
     token_ms = timed(lambda: ops.recurrent_fp32_forward_internal(
         cu, slots, pool, *args_tok, out, 1.0, DECAY_RAW_W, None, None, -1), 3)
     chunk_ms = timed(lambda: ops.chunk_forward_internal(
@@ -1039,9 +1044,16 @@ def bench_recurrent_long(args):
                 "tokens_per_s": round(n_tok / (ms * 1e-3), 1),
                 "achieved_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
 
+    op = leg(op_ms, "chunk_fwd_kernel, split-bf16 products")
+    kernel = "chunk_fwd_kernel<Bf16,kRawW,float>/precise"
+    op["roofline"] = {
+        "bound": "hbm", "achieved": op["achieved_GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+        "frac": round(op["achieved_GBps"] / HBM_PEAK_GBPS, 4), "traffic": pmc_traffic(kernel),
+        "kernel": kernel, "algorithmic_bytes_per_launch": nbytes,
+    }
     return {
         "workload": "wkv7_recurrent_long_cfg2: B=8, T=4096, H=32, D=64, bf16 io, fp32 state",
-        "recurrent_op": leg(op_ms, "chunk_fwd_kernel, split-bf16 products"),
+        "recurrent_op": op,
         "per_token_kernel": leg(token_ms, "recurrent_fp32_kernel"),
         "bf16_chunk_op": leg(chunk_ms, "chunk_fwd_kernel, bf16 products"),
         "algorithmic_bytes": nbytes,
