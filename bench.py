@@ -1205,8 +1205,15 @@ def bench_matrix(args):
                                   and gate["deterministic"]
                                   and gate["output_relative_rmse"] <= MATRIX_RMSE_LIMIT
                                   and gate["state_relative_rmse"] <= MATRIX_RMSE_LIMIT)
+            # The operator's kernel for this call (its rule in frwkv_recurrent_forward:
+            # bf16 tokens at head size 64 with max_seqlen >= 64 take the split-bf16
+            # chunk kernel).
+            chunked = args.matrix_dtype == "bfloat16" and max(lengths) >= 64
             row = {"operator_shape": shape_name, "case": label, "B": bsz,
                    "T": lengths[0] if len(set(lengths)) == 1 else None,
+                   "max_seqlen": max(lengths),
+                   "kernel": "chunk_fwd_kernel (split-bf16)" if chunked
+                   else "recurrent_fp32_kernel",
                    "total_tokens": n_tok, "dtype": args.matrix_dtype, "correctness": gate}
             if gate["passed"]:
                 out = torch.empty_like(v)
