@@ -15,6 +15,12 @@ constexpr int kChunkThreads = 256;
 constexpr float kSpanLimit = 80.0f;   // log2 units
 constexpr float kSpanFloor = 0x1p-80f; // 2^-kSpanLimit: the same limit as a decay product
 constexpr float kLog2Min = -20.0f;    // per-token clamp of log2 retention
+// A buffer offset past every resource's range (resources here are under
+// 2 GiB): a store there is dropped and a load returns zero. Masked lanes use
+// it instead of a branch around the access, so every pass issues the same
+// number of memory instructions and the compiler's in-order wait counts stay
+// exact.
+constexpr uint32_t kDropOffset = 0x80000000u;
 
 // Operand tiles: 64 rows x 64 bf16, row stride 68 elements (136 B = 34
 // dwords): the 16 rows of an 8-byte operand read hit 16 distinct dword pairs.

@@ -503,7 +503,8 @@ __device__ __forceinline__ void intra_chunk(ChunkSmem& sm, ExtraTiles<kPrecise>&
 
 // State-dependent part of one prepared (sub-)chunk for wave w's value
 // columns. Tokens outside [lo, hi) are zero rows of every operand; their
-// outputs are not stored.
+// output stores go to kDropOffset and are dropped (no branch around them, so
+// every pass issues the same stores).
 // out_rs / sda_rs cover the chunk's rows of the output and of state_dot_a
 // (row t at byte t * row_bytes, resp. 2 * t * row_bytes); sda_rs is unused
 // when with_sda is false.
@@ -602,11 +603,9 @@ __device__ void state_pass(const ChunkSmem& sm, const ExtraTiles<kPrecise>& ext,
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int t = 16 * pb + 4 * g + j;
-        if (t >= lo && t < hi) {
-          __builtin_amdgcn_raw_buffer_store_b32(
-              __float_as_uint(sa[pb][j]), sda_rs, off,
-              static_cast<int>((16 * pb + j) * 2 * row_bytes), 0);
-        }
+        __builtin_amdgcn_raw_buffer_store_b32(
+            __float_as_uint(sa[pb][j]), sda_rs, (t >= lo && t < hi) ? off : kDropOffset,
+            static_cast<int>((16 * pb + j) * 2 * row_bytes), 0);
       }
     }
   }
@@ -723,13 +722,11 @@ __device__ void state_pass(const ChunkSmem& sm, const ExtraTiles<kPrecise>& ext,
 #pragma unroll
   for (int pb = 0; pb < 4; ++pb) {
     const int t = 16 * pb + n;
-    if (t >= lo && t < hi) {
-      u32x2 q;
-      q.x = pack2<T>(scale * y[pb][0], scale * y[pb][1]);
-      q.y = pack2<T>(scale * y[pb][2], scale * y[pb][3]);
-      __builtin_amdgcn_raw_buffer_store_b64(q, out_rs, y_off,
-                                            static_cast<int>(16 * pb * row_bytes), 0);
-    }
+    u32x2 q;
+    q.x = pack2<T>(scale * y[pb][0], scale * y[pb][1]);
+    q.y = pack2<T>(scale * y[pb][2], scale * y[pb][3]);
+    __builtin_amdgcn_raw_buffer_store_b64(q, out_rs, (t >= lo && t < hi) ? y_off : kDropOffset,
+                                          static_cast<int>(16 * pb * row_bytes), 0);
   }
 }
 
@@ -897,17 +894,36 @@ __global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_ker
 #pragma unroll
     for (int piece = 0; piece < 6; ++piece) load_piece(rows, c0, ntok, piece);
   };
+  // The main path issues the state pass's output stores between a chunk's
+  // row loads and the prepare that reads them. Paths that load rows without
+  // a state pass after them issue as many dropped stores, so that on every
+  // path into the prepare the compiler counts them and waits for the loads
+  // alone (the memory counter retires in order; at a join the compiler keeps
+  // the path with the fewest instructions after the loads).
+  auto pad_after_rows = [&]() {
+    const auto nrs = buffer_rsrc(static_cast<float*>(nullptr), 0u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_raw_buffer_store_b32(0u, nrs, kDropOffset, 4 * i, 0);
+    }
+  };
 
   ChunkRows rows;
   {
     int seg = seg_lo, c0 = 0, c_end = 0;
     if (seg < seg_hi) seg_range(seg, c0, c_end);
     if (seg < seg_hi && c0 < c_end) load_rows(rows, c0, min(kChunk, c_end - c0));
+    pad_after_rows();
   }
   for (int seg = seg_lo; seg < seg_hi; ++seg) {
     int t_begin, t_end;
     seg_range(seg, t_begin, t_end);
-    if (p.boundary != nullptr && !p.boundary16) {
+    // The state at the segment start, written after the first chunk's
+    // prepare: stores issued here, between the row loads of that chunk
+    // (made during the previous chunk) and their first use, would be waited
+    // for with them (the memory counter retires in order). Segments that
+    // reach no prepare (empty, or skipped by fill_only) store it here.
+    auto store_boundary = [&]() {
       const auto brs = buffer_rsrc(
           p.boundary + (static_cast<int64_t>(seg) * heads + head) * kHead * kHead,
           kHead * kHead * 4);
@@ -920,7 +936,10 @@ __global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_ker
                                                 (16 * kb + j) * kHead * 4, 0);
         }
       }
-    }
+    };
+    const bool want_boundary = p.boundary != nullptr && !p.boundary16;
+    const bool defer_boundary = t_end > t_begin && !p.fill_only;
+    if (want_boundary && !defer_boundary) store_boundary();
     if (p.fill_only && t_end - t_begin <= kChunk) continue;
     for (int c0 = t_begin; c0 < t_end; c0 += kChunk) {
       const int ntok = min(kChunk, t_end - c0);
@@ -977,6 +996,7 @@ __global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_ker
                               ? prepare<T, M, true, kPrecise>(sm, ext, rows, bias, lo, hi)
                               : prepare<T, M, false, kPrecise>(sm, ext, rows, bias, lo, hi);
         if (first) {
+          if (want_boundary && defer_boundary && c0 == t_begin) store_boundary();
           first = false;
           spans = cur;
           whole = cur.whole;
@@ -1017,7 +1037,10 @@ __global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_ker
         const int q = lo >> 4;
         hi = min(lo + (spans.block_ok(q) ? 16 : 4), min(16 * q + 16, ntok));
       }
-      if (!whole) load_rows(rows, has_next ? nc0 : c0, has_next ? min(kChunk, nend - nc0) : 0);
+      if (!whole) {
+        load_rows(rows, has_next ? nc0 : c0, has_next ? min(kChunk, nend - nc0) : 0);
+        pad_after_rows();
+      }
     }
   }
 
