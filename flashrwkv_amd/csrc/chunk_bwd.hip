@@ -556,12 +556,16 @@ __device__ __forceinline__ void state_step(const BwdSmem& sm, f32x4 (&S)[4], int
   }
 }
 
-// Adjoint chain of value columns 16 cs .. 16 cs + 15: dSA, dZ (written to the
-// dz tile), dV (written to the dv tile), the partial dg of these columns, and
-// dS <- dS0. S0 is the piece-start state slab (fp32, C layout).
+// Adjoint chain of value columns 16 cs .. 16 cs + 15, first part: dSA, dZ
+// (written to the dz tile and returned as operands), the partial dg of these
+// columns, and dS0 without its dZ term (ds0). S0 is the piece-start state
+// slab (fp32, C layout). adjoint_finish completes dS0 after the columns
+// phase's mid barrier; the forward waves form dV meanwhile (dv_partial,
+// dv_finish).
 template <typename T>
 __device__ __forceinline__ void adjoint_chain(BwdSmem& sm, const f32x4 (&S0)[4], int cs, int g,
-                                              int n, int lane) {
+                                              int n, int lane, f32x4 (&ds0)[4], i16x8& dz01,
+                                              i16x8& dz23) {
   lane = lane_tid() & 63;
   g = lane >> 4;
   n = lane & 15;
@@ -613,27 +617,8 @@ __device__ __forceinline__ void adjoint_chain(BwdSmem& sm, const f32x4 (&S0)[4],
   dsa[2] = mfma32(cat(Lt(kArb, 2, 2), Lt(kArb, 3, 2)), dy23, dsa[2]);
   dsa[3] = mfma32(lo32(Lt(kArb, 3, 3)), lo32(dys[3]), dsa[3]);
 
-  // The parts of dV and dS0 that do not need dZ first, so their products
-  // fill the latencies of the dZ chain:
-  //   dV^T  <- (g o dS)^T Kh^T + sum_{q>=pb} dYs_q^T Ark(q, pb),
-  //   dS0   <- g o dS + Rt^T dYs.
-  auto Lb = [&](int m, int q, int pb) {  // B[k = t][n = i] = M[t][i] of block (q, pb)
-    return lds_operand_tr<kTriStride>(tri_blk(sm.u.f.tri[m], q, pb), 0, 0, g, n);
-  };
-  f32x4 dvt[4];
-#pragma unroll
-  for (int pb = 0; pb < 4; ++pb)
-    dvt[pb] = mfma32(gds01, lds_operand32<kOpStride>(sm.kh, 16 * pb + n, 0, g), zero4());
-#pragma unroll
-  for (int pb = 0; pb < 4; ++pb)
-    dvt[pb] = mfma32(gds23, lds_operand32<kOpStride>(sm.kh, 16 * pb + n, 32, g), dvt[pb]);
-  dvt[0] = mfma32(dy01, cat(Lb(kArk, 0, 0), Lb(kArk, 1, 0)), dvt[0]);
-  dvt[0] = mfma32(dy23, cat(Lb(kArk, 2, 0), Lb(kArk, 3, 0)), dvt[0]);
-  dvt[1] = mfma32(lo32(dys[1]), lo32(Lb(kArk, 1, 1)), dvt[1]);
-  dvt[1] = mfma32(dy23, cat(Lb(kArk, 2, 1), Lb(kArk, 3, 1)), dvt[1]);
-  dvt[2] = mfma32(dy23, cat(Lb(kArk, 2, 2), Lb(kArk, 3, 2)), dvt[2]);
-  dvt[3] = mfma32(lo32(dys[3]), lo32(Lb(kArk, 3, 3)), dvt[3]);
-  f32x4 ds0[4];
+  // The part of dS0 that does not need dZ first, so its products fill the
+  // latencies of the dZ chain: dS0 <- g o dS + Rt^T dYs.
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
     const float4 gc4 = *reinterpret_cast<const float4*>(&sm.gc[16 * kb + 4 * g]);
@@ -653,7 +638,7 @@ __device__ __forceinline__ void adjoint_chain(BwdSmem& sm, const f32x4 (&S0)[4],
   dsa[2] = mfma32(lo32(Lt(kLab, 3, 2)), lo32(dzb[3]), dsa[2]);
   dz[2] = mfma32(lo32(Tt(2)), lo32(to_operand(dsa[2])), zero4());
   dzb[2] = to_operand(dz[2]);
-  const i16x8 dz23 = cat(dzb[2], dzb[3]);
+  dz23 = cat(dzb[2], dzb[3]);
   dsa[1] = mfma32(cat(Lt(kLab, 2, 1), Lt(kLab, 3, 1)), dz23, dsa[1]);
   dsa[0] = mfma32(cat(Lt(kLab, 2, 0), Lt(kLab, 3, 0)), dz23, dsa[0]);
   dz[1] = mfma32(lo32(Tt(1)), lo32(to_operand(dsa[1])), zero4());
@@ -661,13 +646,80 @@ __device__ __forceinline__ void adjoint_chain(BwdSmem& sm, const f32x4 (&S0)[4],
   dsa[0] = mfma32(lo32(Lt(kLab, 1, 0)), lo32(dzb[1]), dsa[0]);
   dz[0] = mfma32(lo32(Tt(0)), lo32(to_operand(dsa[0])), zero4());
   dzb[0] = to_operand(dz[0]);
-  const i16x8 dz01 = cat(dzb[0], dzb[1]);
+  dz01 = cat(dzb[0], dzb[1]);
 #pragma unroll
   for (int pb = 0; pb < 4; ++pb)
     lds_store_rows(sm.dz + (16 * pb) * kOpStride + 16 * cs, kOpStride, g, n, dz[pb]);
+}
 
-  // dV^T (rows v of this slab, cols t of block pb): the dZ terms
-  // sum_{q>=pb} dZ_q^T Lak(q, pb); lane (g, n) ends with dV[16 pb + n][16 cs + 4g .. +3].
+// Second part, after the mid barrier: dS0 = g o dS + Rt^T dYs + At^T dZ into
+// the stash (dS for the range before).
+__device__ __forceinline__ void adjoint_finish(BwdSmem& sm, int cs, f32x4 (&ds0)[4],
+                                               const i16x8& dz01, const i16x8& dz23) {
+  const int lane = lane_tid() & 63;
+  const int g = lane >> 4, n = lane & 15;
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    f32x4 acc = mfma32(tr32<kOpStride>(sm.at, 0, 16 * kb, g, n), dz01, ds0[kb]);
+    acc = mfma32(tr32<kOpStride>(sm.at, 32, 16 * kb, g, n), dz23, acc);
+    sm.dstash[cs][kb][lane] = acc;
+  }
+}
+
+// dV^T of value columns 16 cs .. 16 cs + 15 on the forward waves (lane (g, n)
+// ends with dV[16 pb + n][16 cs + 4g .. +3]). dv_partial, before the mid
+// barrier: the terms without dZ, (g o dS)^T Kh^T + sum_{q>=pb} dYs_q^T
+// Ark(q, pb), with dS read from the adjoint waves' stash (same slab and lane,
+// read before they overwrite it). dv_finish, after it: the dZ terms
+// sum_{q>=pb} dZ_q^T Lak(q, pb) from the dz tile, then the dv tile.
+__device__ __forceinline__ void dv_partial(const BwdSmem& sm, int cs, f32x4 (&dvt)[4]) {
+  const int lane = lane_tid() & 63;
+  const int g = lane >> 4, n = lane & 15;
+  i16x4 gds[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    const f32x4 dS = sm.dstash[cs][kb][lane];
+    const float4 gc4 = *reinterpret_cast<const float4*>(&sm.gc[16 * kb + 4 * g]);
+    f32x4 x;
+    x[0] = gc4.x * dS[0];
+    x[1] = gc4.y * dS[1];
+    x[2] = gc4.z * dS[2];
+    x[3] = gc4.w * dS[3];
+    gds[kb] = to_operand(x);
+  }
+  const i16x8 gds01 = cat(gds[0], gds[1]), gds23 = cat(gds[2], gds[3]);
+  i16x4 dys[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) dys[q] = lds_operand_tr<kOpStride>(sm.dy, 16 * q, 16 * cs, g, n);
+  const i16x8 dy01 = cat(dys[0], dys[1]), dy23 = cat(dys[2], dys[3]);
+  auto Lb = [&](int m, int q, int pb) {  // B[k = t][n = i] = M[t][i] of block (q, pb)
+    return lds_operand_tr<kTriStride>(tri_blk(sm.u.f.tri[m], q, pb), 0, 0, g, n);
+  };
+#pragma unroll
+  for (int pb = 0; pb < 4; ++pb)
+    dvt[pb] = mfma32(gds01, lds_operand32<kOpStride>(sm.kh, 16 * pb + n, 0, g), zero4());
+#pragma unroll
+  for (int pb = 0; pb < 4; ++pb)
+    dvt[pb] = mfma32(gds23, lds_operand32<kOpStride>(sm.kh, 16 * pb + n, 32, g), dvt[pb]);
+  dvt[0] = mfma32(dy01, cat(Lb(kArk, 0, 0), Lb(kArk, 1, 0)), dvt[0]);
+  dvt[0] = mfma32(dy23, cat(Lb(kArk, 2, 0), Lb(kArk, 3, 0)), dvt[0]);
+  dvt[1] = mfma32(lo32(dys[1]), lo32(Lb(kArk, 1, 1)), dvt[1]);
+  dvt[1] = mfma32(dy23, cat(Lb(kArk, 2, 1), Lb(kArk, 3, 1)), dvt[1]);
+  dvt[2] = mfma32(dy23, cat(Lb(kArk, 2, 2), Lb(kArk, 3, 2)), dvt[2]);
+  dvt[3] = mfma32(lo32(dys[3]), lo32(Lb(kArk, 3, 3)), dvt[3]);
+}
+
+template <typename T>
+__device__ __forceinline__ void dv_finish(BwdSmem& sm, int cs, f32x4 (&dvt)[4]) {
+  const int lane = lane_tid() & 63;
+  const int g = lane >> 4, n = lane & 15;
+  i16x4 dzb[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) dzb[q] = lds_operand_tr<kOpStride>(sm.dz, 16 * q, 16 * cs, g, n);
+  const i16x8 dz01 = cat(dzb[0], dzb[1]), dz23 = cat(dzb[2], dzb[3]);
+  auto Lb = [&](int m, int q, int pb) {
+    return lds_operand_tr<kTriStride>(tri_blk(sm.u.f.tri[m], q, pb), 0, 0, g, n);
+  };
   dvt[0] = mfma32(dz01, cat(Lb(kLak, 0, 0), Lb(kLak, 1, 0)), dvt[0]);
   dvt[0] = mfma32(dz23, cat(Lb(kLak, 2, 0), Lb(kLak, 3, 0)), dvt[0]);
   dvt[1] = mfma32(lo32(dzb[1]), lo32(Lb(kLak, 1, 1)), dvt[1]);
@@ -680,14 +732,6 @@ __device__ __forceinline__ void adjoint_chain(BwdSmem& sm, const f32x4 (&S0)[4],
     q.x = pack2<T>(dvt[pb][0], dvt[pb][1]);
     q.y = pack2<T>(dvt[pb][2], dvt[pb][3]);
     *reinterpret_cast<uint2*>(sm.dv + (16 * pb + n) * kOpStride + 16 * cs + 4 * g) = q;
-  }
-
-  // dS0 = g o dS + Rt^T dYs + At^T dZ.
-#pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
-    f32x4 acc = mfma32(tr32<kOpStride>(sm.at, 0, 16 * kb, g, n), dz01, ds0[kb]);
-    acc = mfma32(tr32<kOpStride>(sm.at, 32, 16 * kb, g, n), dz23, acc);
-    sm.dstash[cs][kb][lane] = acc;
   }
 }
 
@@ -763,7 +807,12 @@ __device__ void run_backward_step(BwdSmem& sm, const ChunkBwdParams& p, const To
   const bool on = t >= lo && t < hi;
 
   // ---------------------------------------------------------- columns --
+  // Two parts around a mid barrier. Forward waves: the SA chain and the
+  // dZ-free part of dV, then dV's dZ terms. Adjoint waves: dSA, the dZ chain
+  // (dz tile) and dS0 without its dZ term, then that term.
   __builtin_amdgcn_s_setprio(1);
+  f32x4 dvt[4], ds0[4];
+  i16x8 dz01, dz23;
   if (wave < 4) {
     f32x4 sa[4];
     i16x4 sab[4], vs[4];
@@ -773,8 +822,15 @@ __device__ void run_backward_step(BwdSmem& sm, const ChunkBwdParams& p, const To
       lds_store_rows(sm.sa + (16 * q) * kOpStride + 16 * cs, kOpStride, g, n, sa[q]);
       lds_store_transposed(sm.s0 + (16 * cs) * kOpStride + 16 * q, kOpStride, g, n, S0[q]);
     }
+    dv_partial(sm, cs, dvt);
   } else {
-    adjoint_chain<T>(sm, S0, cs, g, n, lane);
+    adjoint_chain<T>(sm, S0, cs, g, n, lane, ds0, dz01, dz23);
+  }
+  __syncthreads();
+  if (wave < 4) {
+    dv_finish<T>(sm, cs, dvt);
+  } else {
+    adjoint_finish(sm, cs, ds0, dz01, dz23);
   }
   __builtin_amdgcn_s_setprio(0);
   __syncthreads();
@@ -1003,18 +1059,22 @@ __device__ void run_backward_step(BwdSmem& sm, const ChunkBwdParams& p, const To
     return buffer_rsrc(static_cast<S16*>(x) + (static_cast<int64_t>(pc.c0) * heads + head) * kHead,
                        static_cast<uint32_t>(pc.ntok) * row_bytes);
   };
-  if (on) {
+  // Lanes of tokens outside [lo, hi) store to kDropOffset (dropped): no
+  // branch, so every pass issues the same stores and the compiler's in-order
+  // wait counts for the next piece's row loads stay exact.
+  const uint32_t st_off = on ? tok_off : kDropOffset;
+  {
     __builtin_amdgcn_raw_buffer_store_b128(u32x4{wr[0], wr[1], wr[2], wr[3]}, rsrc(args().dr),
-                                           tok_off, 0, 0);
+                                           st_off, 0, 0);
     __builtin_amdgcn_raw_buffer_store_b128(u32x4{wa[0], wa[1], wa[2], wa[3]}, rsrc(args().da),
-                                           tok_off, 0, 0);
+                                           st_off, 0, 0);
     __builtin_amdgcn_raw_buffer_store_b128(u32x4{wb[0], wb[1], wb[2], wb[3]}, rsrc(args().db),
-                                           tok_off, 0, 0);
+                                           st_off, 0, 0);
     __builtin_amdgcn_raw_buffer_store_b128(u32x4{wk[0], wk[1], wk[2], wk[3]}, rsrc(args().dk),
-                                           tok_off, 0, 0);
+                                           st_off, 0, 0);
     const uint2 d0 = *reinterpret_cast<const uint2*>(sm.dv + t * kOpStride + f0);
     const uint2 d1 = *reinterpret_cast<const uint2*>(sm.dv + t * kOpStride + f0 + 4);
-    __builtin_amdgcn_raw_buffer_store_b128(u32x4{d0.x, d0.y, d1.x, d1.y}, rsrc(args().dv), tok_off,
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{d0.x, d0.y, d1.x, d1.y}, rsrc(args().dv), st_off,
                                            0, 0);
   }
   __syncthreads();  // block carries of the decay gradient
@@ -1055,7 +1115,7 @@ __device__ void run_backward_step(BwdSmem& sm, const ChunkBwdParams& p, const To
       }
     }
   }
-  if (on) __builtin_amdgcn_raw_buffer_store_b128(pack8<T>(dw), rsrc(args().ddecay), tok_off, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b128(pack8<T>(dw), rsrc(args().ddecay), st_off, 0, 0);
 }
 
 template <typename T, DecayMode M>
@@ -1205,6 +1265,19 @@ __global__ __launch_bounds__(kBwdThreads, 1) void chunk_bwd_kernel(ChunkBwdParam
     }
     return false;
   };
+  // A whole piece issues the six gradient stores between its loads of the
+  // next piece's rows and that piece's prepare; paths that load rows without
+  // them issue as many dropped stores, so that on every path into the prepare
+  // the compiler counts them and waits for the row loads alone (the memory
+  // counter retires in order; at a join the compiler keeps the path with the
+  // fewest instructions after the loads).
+  auto pad_after_rows = [&]() {
+    const auto nrs = buffer_rsrc(static_cast<float*>(nullptr), 0u);
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      __builtin_amdgcn_raw_buffer_store_b32(0u, nrs, kDropOffset, 4 * i, 0);
+    }
+  };
   int seg = seg_hi, tb = 0, te = 0, j = 0;
   bool have = advance(seg, tb, te, j);
   TokRows nxt;
@@ -1213,6 +1286,7 @@ __global__ __launch_bounds__(kBwdThreads, 1) void chunk_bwd_kernel(ChunkBwdParam
 #pragma unroll
     for (int grp = 0; grp < 3; ++grp) load_group(first, nxt, grp);
   }
+  pad_after_rows();
 
   while (have) {
     const Piece pc = piece_of(seg, tb, te, j);
@@ -1256,6 +1330,7 @@ __global__ __launch_bounds__(kBwdThreads, 1) void chunk_bwd_kernel(ChunkBwdParam
       }
 #pragma unroll
       for (int grp = 0; grp < 3; ++grp) load_group(prev, nxt, grp);
+      pad_after_rows();
     }
     seg = pseg;
     tb = ptb;
