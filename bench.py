@@ -48,12 +48,12 @@ _COPY_KIB = 262144.0
 _COPY_FETCH_KIB = 131084.4
 _COPY_WRITE_KIB = 262144.0
 PMC_KIB = {  # kernel -> (FETCH_SIZE, WRITE_SIZE)
-    "recurrent_fp32_kernel<64,64,64,Bf16,kRawW>": (85811.4, 165208.9),
-    "chunk_fwd_kernel<Bf16,kRawW,float>": (790711.1, 270341.0),
-    "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": (790727.5, 1319370.2),
-    "chunk_fwd_kernel<Bf16,kRawW,float>/precise": (395464.6, 135168.0),
-    "chunk_bwd_kernel<Bf16,kRawW>": (1187909.2, 1637060.8),
-    "recurrent_fp16_decode_kernel": (44876.3, 83226.3),
+    "recurrent_fp32_kernel<64,64,64,Bf16,kRawW>": (85811.4, 165206.2),
+    "chunk_fwd_kernel<Bf16,kRawW,float>": (790712.8, 270342.3),
+    "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": (790726.1, 1318932.4),
+    "chunk_fwd_kernel<Bf16,kRawW,float>/precise": (395468.7, 135168.0),
+    "chunk_bwd_kernel<Bf16,kRawW>": (1185180.4, 1657188.7),
+    "recurrent_fp16_decode_kernel": (44876.3, 83232.2),
 }
 
 # The kernel sources PMC_KIB was measured on: sha256 over these files, in
@@ -62,7 +62,7 @@ PMC_KIB = {  # kernel -> (FETCH_SIZE, WRITE_SIZE)
 PMC_SOURCES = ("flashrwkv_amd/csrc/recurrent.hip", "flashrwkv_amd/csrc/chunk_fwd.hip",
                "flashrwkv_amd/csrc/chunk_bwd.hip", "flashrwkv_amd/csrc/chunk_common.h",
                "flashrwkv_amd/csrc/wkv7_device.h", "flashrwkv_amd/csrc/wkv7_mfma.h")
-PMC_SOURCES_SHA = "dfd9acbcc1552d3ed685f365f5e16b5c1cd15c070c11e9a44136c4e0afd2555f"
+PMC_SOURCES_SHA = "08cbe2f61139a6f82c84ec58c8df9db7911c3fd2d8f4871b08b28f5d8a98b93a"
 
 
 def kernel_sources_sha() -> str:
