@@ -59,10 +59,10 @@ struct ChunkSmem {
   uint16_t bh[kOpTile];   // [t][k]
   uint16_t kh[kOpTile];   // [t][k]
   uint16_t vt[kOpTile];   // V [t][v]
-  union {
-    uint16_t tri[4][kTriBlocks * kTriBlock];  // Lab, Lak, Arb, Ark: [t][i]
-    float wave_tot[4][kHead];                 // decay scan carry (prepare only)
-  };
+  uint16_t tri[4][kTriBlocks * kTriBlock];  // Lab, Lak, Arb, Ark: [t][i]
+  // Decay scan carry (prepare only). Not shared with the tiles: the scan
+  // writes it before the barrier after which the tiles may be overwritten.
+  float wave_tot[4][kHead];
   uint16_t tinv[4][kTriBlock];  // (I - Lab_pp)^{-1}, [t][i]
   float gc[kHead];              // 2^GC per key feature
   float gsub[3][kHead];         // 2^G at tokens 15, 31, 47 (16-token boundaries)
@@ -204,8 +204,6 @@ __device__ Spans prepare(ChunkSmem& sm, ExtraTiles<kPrecise>& ext, const ChunkRo
   const bool on0 = kFull || (t0 >= lo && t0 < hi);
   const bool on1 = kFull || (t0 + 1 >= lo && t0 + 1 < hi);
 
-  __syncthreads();  // earlier readers of the tiles are done
-
   // Retentions; tokens outside [lo, hi) get w = 1 (no decay, and their operand
   // rows are zero below).
   float w0[8], w1[8];
@@ -244,6 +242,8 @@ __device__ Spans prepare(ChunkSmem& sm, ExtraTiles<kPrecise>& ext, const ChunkRo
 #pragma unroll
     for (int e = 0; e < 8; ++e) sm.wave_tot[wave][8 * kg + e] = incl[e];
   }
+  // The carries are in LDS, and every reader of the previous pass's tiles
+  // (its state pass) is done: the tiles below may be overwritten.
   __syncthreads();
 
   // Block products x_q (q = 0..3, one per wave's 16 tokens); the carry into
