@@ -1356,6 +1356,10 @@ __global__ __launch_bounds__(kBwdThreads, 1) void chunk_bwd_kernel(ChunkBwdParam
 
 template <typename T, DecayMode M>
 int launch_bwd(const ChunkBwdParams& p, int units, hipStream_t stream) {
+  if (p.num_heads > kMaxChunkHeads) {
+    return set_error(FRWKV_ERR_UNSUPPORTED, "chunked kernels take at most %d heads, got %d",
+                     kMaxChunkHeads, p.num_heads);
+  }
   hipLaunchKernelGGL((chunk_bwd_kernel<T, M>), dim3(units), dim3(kBwdThreads), 0, stream, p);
   return check_launch("chunk_bwd_kernel");
 }

@@ -21,6 +21,10 @@ constexpr float kLog2Min = -20.0f;    // per-token clamp of log2 retention
 // number of memory instructions and the compiler's in-order wait counts stay
 // exact.
 constexpr uint32_t kDropOffset = 0x80000000u;
+// Head count limit of the chunked kernels: a chunk's row offsets (at most
+// 2 x 64 rows of H x 64 x 2 bytes) then stay below 2^30, so neither an
+// in-range offset nor kDropOffset plus a row offset wraps in 32 bits.
+constexpr int32_t kMaxChunkHeads = 65536;
 
 // Operand tiles: 64 rows x 64 bf16, row stride 68 elements (136 B = 34
 // dwords): the 16 rows of an 8-byte operand read hit 16 distinct dword pairs.

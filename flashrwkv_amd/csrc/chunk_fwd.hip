@@ -1061,6 +1061,10 @@ __global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_ker
 
 template <typename T, DecayMode M, typename PoolT, bool kPrecise = false>
 int launch_chunk(const ChunkFwdParams& p, int units, hipStream_t stream) {
+  if (p.num_heads > kMaxChunkHeads) {
+    return set_error(FRWKV_ERR_UNSUPPORTED, "chunked kernels take at most %d heads, got %d",
+                     kMaxChunkHeads, p.num_heads);
+  }
   hipLaunchKernelGGL((chunk_fwd_kernel<T, M, PoolT, kPrecise>), dim3(units),
                      dim3(kChunkThreads), 0, stream, p);
   return check_launch("chunk_fwd_kernel");

@@ -19,6 +19,8 @@
  *            FRWKV_DECAY_RAW_W: the retention w itself (bias must be NULL).
  *   recurrence per token: sa = S^T a; S = diag(w) S + b sa^T + k v^T;
  *            y = scale S^T r.
+ *   The chunked (head size 64) kernels take at most 65536 heads; a call
+ *   routed to them with more returns FRWKV_ERR_UNSUPPORTED.
  *
  * Each entry point cites the reference native interface it replaces
  * (paths relative to the rwkv-rs/FlashRWKV2 source tree).

@@ -190,3 +190,18 @@ def test_noalloc_backward_rejects_oversized_need_without_a_gpu():
     rc = lib.frwkv_statetune_backward_noalloc(2, 1, 1, 1, 256, 4096, 1, *([fake] * 21), 1.0,
                                               None)
     assert rc == 1 and b"bytes of scratch" in lib.frwkv_last_error()
+
+
+def test_chunk_forward_rejects_too_many_heads_without_a_gpu(lib):
+    """The chunked kernels' 32-bit row offsets bound the head count (65536);
+    a larger one is refused before any launch."""
+    lib.frwkv_last_error.restype = ctypes.c_char_p
+    fake = ctypes.c_void_p(256)  # never dereferenced: the call fails first
+    null = ctypes.c_void_p()
+    i32 = ctypes.c_int32
+    common = [i32(1), i32(1 << 17), i32(64), i32(64), i32(1)]
+    ptrs = [fake] * 4 + [fake, fake, null, fake, fake, fake, fake, fake]
+    rc = lib.frwkv_chunk_forward(ctypes.c_int(2), ctypes.c_int(1), ctypes.c_int(0), *common,
+                                 *ptrs, ctypes.c_float(1.0), null)
+    assert rc == 2
+    assert b"at most 65536 heads" in lib.frwkv_last_error()
