@@ -62,7 +62,7 @@ PMC_KIB = {  # kernel -> (FETCH_SIZE, WRITE_SIZE)
 PMC_SOURCES = ("flashrwkv_amd/csrc/recurrent.hip", "flashrwkv_amd/csrc/chunk_fwd.hip",
                "flashrwkv_amd/csrc/chunk_bwd.hip", "flashrwkv_amd/csrc/chunk_common.h",
                "flashrwkv_amd/csrc/wkv7_device.h", "flashrwkv_amd/csrc/wkv7_mfma.h")
-PMC_SOURCES_SHA = "08cbe2f61139a6f82c84ec58c8df9db7911c3fd2d8f4871b08b28f5d8a98b93a"
+PMC_SOURCES_SHA = "1826cbec9ec0358cc7c6a071dd795fa13504ac851d340ee2516f4f92b5de9030"
 
 
 def kernel_sources_sha() -> str:
