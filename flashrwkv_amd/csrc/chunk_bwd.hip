@@ -809,8 +809,14 @@ __device__ void run_backward_step(BwdSmem& sm, const ChunkBwdParams& p, const To
   // ---------------------------------------------------------- columns --
   // Two parts around a mid barrier. Forward waves: the SA chain and the
   // dZ-free part of dV, then dV's dZ terms. Adjoint waves: dSA, the dZ chain
-  // (dz tile) and dS0 without its dZ term, then that term.
-  __builtin_amdgcn_s_setprio(1);
+  // (dz tile) and dS0 without its dZ term, then that term. The adjoint
+  // waves' dZ chain is the phase's critical path: they run at a higher wave
+  // priority than the forward waves sharing their SIMDs.
+  if (wave < 4) {
+    __builtin_amdgcn_s_setprio(1);
+  } else {
+    __builtin_amdgcn_s_setprio(2);
+  }
   f32x4 dvt[4], ds0[4];
   i16x8 dz01, dz23;
   if (wave < 4) {
