@@ -105,6 +105,12 @@ class _StateTune(torch.autograd.Function):
         ctx.save_for_backward(offsets, starts, ends, r, decay, k, v, a, b, boundary, interior)
         ctx.scale, ctx.decay_mode = float(scale), int(decay_mode)
         ctx.mark_non_differentiable(boundary, state_dot_a)
+        # Outputs without a gradient reach backward as None instead of zero
+        # tensors: boundary and state_dot_a are 16 KiB per chunk-head and 256 B
+        # per token-head, whose zero fills would cost more HBM traffic than the
+        # backward's own gradient writes; a None dY or dS_T is a zero input
+        # of the backward kernel.
+        ctx.set_materialize_grads(False)
         return output, state, boundary, state_dot_a
 
     @staticmethod
