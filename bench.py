@@ -84,6 +84,26 @@ def pmc_traffic(kernel: str) -> int | None:
                      + write * 1024 * _COPY_KIB / _COPY_WRITE_KIB))
 
 
+# MFMA busy share per SIMD of the chunked kernels on the same sources
+# (SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs over SQ_BUSY_CU_CYCLES / 256 CUs, in
+# %), from the counter passes of the bench workloads.
+PMC_MFMA_BUSY_PCT = {
+    "chunk_fwd_kernel<Bf16,kRawW,float>": 19.2,
+    "chunk_fwd_kernel<Bf16,kRawW,float>/varlen": 19.0,
+    "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": 15.3,
+    "chunk_fwd_kernel<Bf16,kRawW,float>/precise": 13.8,
+    "chunk_bwd_kernel<Bf16,kRawW>": 12.3,
+}
+
+
+def pmc_mfma_busy(kernel: str) -> float | None:
+    """Measured MFMA busy % per SIMD of ``kernel``, or None when the kernel
+    sources changed since the measurement."""
+    if kernel not in PMC_MFMA_BUSY_PCT or kernel_sources_sha() != PMC_SOURCES_SHA:
+        return None
+    return PMC_MFMA_BUSY_PCT[kernel]
+
+
 def _sum_or_none(*xs):
     return None if any(x is None for x in xs) else sum(xs)
 
@@ -688,6 +708,7 @@ def bench_prefill(args):
                      "frac_of_attainable": round(tflops / attainable, 4),
                      "attainable": round(attainable, 1),
                      "traffic": pmc_traffic("chunk_fwd_kernel<Bf16,kRawW,float>"),
+                     "mfma_busy_pct": pmc_mfma_busy("chunk_fwd_kernel<Bf16,kRawW,float>"),
                      "kernel": "chunk_fwd_kernel<Bf16,kRawW,float>",
                      "algorithmic_flops_per_launch": flops},
         "hbm": {"achieved_GBps": round(gbps, 1), "peak": HBM_PEAK_GBPS,
@@ -767,6 +788,7 @@ def bench_prefill_varlen(args):
         "kernel_ms": round(kernel_ms, 4),
         "achieved_TFLOPs": round(tflops, 2),
         "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+        "mfma_busy_pct": pmc_mfma_busy("chunk_fwd_kernel<Bf16,kRawW,float>/varlen"),
         "achieved_GBps": round(gbps, 1),
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "algorithmic_flops": flops,
@@ -866,6 +888,9 @@ def bench_training(args):
                      "algorithmic_flops_per_step": flops,
                      "traffic": _sum_or_none(pmc_traffic("chunk_fwd_kernel<Bf16,kRawW,float>/statetune"),
                                              pmc_traffic("chunk_bwd_kernel<Bf16,kRawW>")),
+                     "mfma_busy_pct": {
+                         "forward": pmc_mfma_busy("chunk_fwd_kernel<Bf16,kRawW,float>/statetune"),
+                         "backward": pmc_mfma_busy("chunk_bwd_kernel<Bf16,kRawW>")},
                      "kernel": "chunk_fwd_kernel<Bf16,kRawW,float> + chunk_bwd_kernel<Bf16,kRawW>"},
         "hbm": {"achieved_GBps": round(gbps, 1), "peak": HBM_PEAK_GBPS,
                 "frac": round(gbps / HBM_PEAK_GBPS, 4), "algorithmic_bytes_per_step": nbytes},
@@ -1049,6 +1074,7 @@ def bench_recurrent_long(args):
     op["roofline"] = {
         "bound": "hbm", "achieved": op["achieved_GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
         "frac": round(op["achieved_GBps"] / HBM_PEAK_GBPS, 4), "traffic": pmc_traffic(kernel),
+        "mfma_busy_pct": pmc_mfma_busy(kernel),
         "kernel": kernel, "algorithmic_bytes_per_launch": nbytes,
     }
     return {
