@@ -977,6 +977,27 @@ __device__ void run_backward_step(BwdSmem& sm, const ChunkBwdParams& p, const To
       wa[2 * u + 1] = pack2<T>(ga4[2], ga4[3]);
     }
   }
+  // Token rows of the piece: the buffer range ends at its last token; inside
+  // the piece only tokens of [lo, hi) are written.
+  using S16 = typename IoTraits<T>::storage;
+  auto rsrc = [&](void* x) {
+    return buffer_rsrc(static_cast<S16*>(x) + (static_cast<int64_t>(pc.c0) * heads + head) * kHead,
+                       static_cast<uint32_t>(pc.ntok) * row_bytes);
+  };
+  // Lanes of tokens outside [lo, hi) store to kDropOffset (dropped): no
+  // branch, so every pass issues the same stores and the compiler's in-order
+  // wait counts for the next piece's row loads stay exact.
+  const uint32_t st_off = on ? tok_off : kDropOffset;
+  __builtin_amdgcn_raw_buffer_store_b128(u32x4{wr[0], wr[1], wr[2], wr[3]}, rsrc(args().dr),
+                                         st_off, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b128(u32x4{wa[0], wa[1], wa[2], wa[3]}, rsrc(args().da),
+                                         st_off, 0, 0);
+  {
+    const uint2 d0 = *reinterpret_cast<const uint2*>(sm.dv + t * kOpStride + f0);
+    const uint2 d1 = *reinterpret_cast<const uint2*>(sm.dv + t * kOpStride + f0 + 4);
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{d0.x, d0.y, d1.x, d1.y}, rsrc(args().dv), st_off,
+                                           0, 0);
+  }
 
   // ---- pass B: dBc = dLab^T At + dArb^T Rt + g (SA dS^T), dKc likewise
   // with dLak, dArk and V.
@@ -1058,31 +1079,10 @@ __device__ void run_backward_step(BwdSmem& sm, const ChunkBwdParams& p, const To
     }
   }
 
-  // Token rows of the piece: the buffer range ends at its last token; inside
-  // the piece only tokens of [lo, hi) are written.
-  using S16 = typename IoTraits<T>::storage;
-  auto rsrc = [&](void* x) {
-    return buffer_rsrc(static_cast<S16*>(x) + (static_cast<int64_t>(pc.c0) * heads + head) * kHead,
-                       static_cast<uint32_t>(pc.ntok) * row_bytes);
-  };
-  // Lanes of tokens outside [lo, hi) store to kDropOffset (dropped): no
-  // branch, so every pass issues the same stores and the compiler's in-order
-  // wait counts for the next piece's row loads stay exact.
-  const uint32_t st_off = on ? tok_off : kDropOffset;
-  {
-    __builtin_amdgcn_raw_buffer_store_b128(u32x4{wr[0], wr[1], wr[2], wr[3]}, rsrc(args().dr),
-                                           st_off, 0, 0);
-    __builtin_amdgcn_raw_buffer_store_b128(u32x4{wa[0], wa[1], wa[2], wa[3]}, rsrc(args().da),
-                                           st_off, 0, 0);
-    __builtin_amdgcn_raw_buffer_store_b128(u32x4{wb[0], wb[1], wb[2], wb[3]}, rsrc(args().db),
-                                           st_off, 0, 0);
-    __builtin_amdgcn_raw_buffer_store_b128(u32x4{wk[0], wk[1], wk[2], wk[3]}, rsrc(args().dk),
-                                           st_off, 0, 0);
-    const uint2 d0 = *reinterpret_cast<const uint2*>(sm.dv + t * kOpStride + f0);
-    const uint2 d1 = *reinterpret_cast<const uint2*>(sm.dv + t * kOpStride + f0 + 4);
-    __builtin_amdgcn_raw_buffer_store_b128(u32x4{d0.x, d0.y, d1.x, d1.y}, rsrc(args().dv), st_off,
-                                           0, 0);
-  }
+  __builtin_amdgcn_raw_buffer_store_b128(u32x4{wb[0], wb[1], wb[2], wb[3]}, rsrc(args().db),
+                                         st_off, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b128(u32x4{wk[0], wk[1], wk[2], wk[3]}, rsrc(args().dk),
+                                         st_off, 0, 0);
   __syncthreads();  // block carries of the decay gradient
 
   float dw[8];
