@@ -48,12 +48,12 @@ _COPY_KIB = 262144.0
 _COPY_FETCH_KIB = 131084.4
 _COPY_WRITE_KIB = 262144.0
 PMC_KIB = {  # kernel -> (FETCH_SIZE, WRITE_SIZE)
-    "recurrent_fp32_kernel<64,64,64,Bf16,kRawW>": (85811.5, 165205.0),
-    "chunk_fwd_kernel<Bf16,kRawW,float>": (790717.0, 270339.4),
-    "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": (790731.3, 1318937.3),
-    "chunk_fwd_kernel<Bf16,kRawW,float>/precise": (395470.9, 135168.0),
-    "chunk_bwd_kernel<Bf16,kRawW>": (1185127.1, 1655218.4),
-    "recurrent_fp16_decode_kernel": (44876.3, 83239.0),
+    "recurrent_fp32_kernel<64,64,64,Bf16,kRawW>": (85811.4, 165204.9),
+    "chunk_fwd_kernel<Bf16,kRawW,float>": (790716.1, 270343.8),
+    "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": (790731.7, 1318935.7),
+    "chunk_fwd_kernel<Bf16,kRawW,float>/precise": (395471.0, 135168.0),
+    "chunk_bwd_kernel<Bf16,kRawW>": (1184918.9, 1581062.2),
+    "recurrent_fp16_decode_kernel": (44876.2, 83231.4),
 }
 
 # The kernel sources PMC_KIB was measured on: sha256 over these files, in
@@ -62,7 +62,7 @@ PMC_KIB = {  # kernel -> (FETCH_SIZE, WRITE_SIZE)
 PMC_SOURCES = ("flashrwkv_amd/csrc/recurrent.hip", "flashrwkv_amd/csrc/chunk_fwd.hip",
                "flashrwkv_amd/csrc/chunk_bwd.hip", "flashrwkv_amd/csrc/chunk_common.h",
                "flashrwkv_amd/csrc/wkv7_device.h", "flashrwkv_amd/csrc/wkv7_mfma.h")
-PMC_SOURCES_SHA = "7f869e4101f2c8feba9244a797171537cf2ea7f705e9c74fab2005fe760ac14a"
+PMC_SOURCES_SHA = "f5c5779111d5bdeff6970984e3a6d47c5915718b64579f3b02dde3fd7b14d433"
 
 
 def kernel_sources_sha() -> str:
@@ -90,9 +90,9 @@ def pmc_traffic(kernel: str) -> int | None:
 PMC_MFMA_BUSY_PCT = {
     "chunk_fwd_kernel<Bf16,kRawW,float>": 19.2,
     "chunk_fwd_kernel<Bf16,kRawW,float>/varlen": 19.0,
-    "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": 15.3,
+    "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": 15.4,
     "chunk_fwd_kernel<Bf16,kRawW,float>/precise": 13.8,
-    "chunk_bwd_kernel<Bf16,kRawW>": 12.3,
+    "chunk_bwd_kernel<Bf16,kRawW>": 12.7,
 }
 
 
