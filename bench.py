@@ -48,21 +48,23 @@ _COPY_KIB = 262144.0
 _COPY_FETCH_KIB = 131084.4
 _COPY_WRITE_KIB = 262144.0
 PMC_KIB = {  # kernel -> (FETCH_SIZE, WRITE_SIZE)
-    "recurrent_fp32_kernel<64,64,64,Bf16,kRawW>": (85811.4, 165204.9),
-    "chunk_fwd_kernel<Bf16,kRawW,float>": (790716.1, 270343.8),
-    "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": (790731.7, 1318935.7),
-    "chunk_fwd_kernel<Bf16,kRawW,float>/precise": (395471.0, 135168.0),
-    "chunk_bwd_kernel<Bf16,kRawW>": (1184918.9, 1581062.2),
-    "recurrent_fp16_decode_kernel": (44876.2, 83231.4),
+    "recurrent_fp32_kernel<64,64,64,Bf16,kRawW>": (85811.4, 165206.6),
+    "chunk_fwd_kernel<Bf16,kRawW,float>": (790716.3, 270344.9),
+    "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": (790730.2, 1318942.7),
+    "chunk_fwd_kernel<Bf16,kRawW,float>/precise": (395469.2, 135168.0),
+    "chunk_bwd_kernel<Bf16,kRawW>": (1186686.9, 1581074.4),
+    "recurrent_fp16_decode_kernel": (44876.3, 83224.2),
 }
 
 # The kernel sources PMC_KIB was measured on: sha256 over these files, in
-# order. When the tree's sources differ, the constants describe other kernels
-# and pmc_traffic reports None instead of a stale figure.
+# order (the build script carries the compile flags). When the tree's sources
+# differ, the constants describe other kernels and pmc_traffic reports None
+# instead of a stale figure.
 PMC_SOURCES = ("flashrwkv_amd/csrc/recurrent.hip", "flashrwkv_amd/csrc/chunk_fwd.hip",
                "flashrwkv_amd/csrc/chunk_bwd.hip", "flashrwkv_amd/csrc/chunk_common.h",
-               "flashrwkv_amd/csrc/wkv7_device.h", "flashrwkv_amd/csrc/wkv7_mfma.h")
-PMC_SOURCES_SHA = "f5c5779111d5bdeff6970984e3a6d47c5915718b64579f3b02dde3fd7b14d433"
+               "flashrwkv_amd/csrc/wkv7_device.h", "flashrwkv_amd/csrc/wkv7_mfma.h",
+               "flashrwkv_amd/_build.py")
+PMC_SOURCES_SHA = "c24e19da539215f3d36b3e66b6baa2f8117e6ce71f2789434535e2501fdb29b5"
 
 
 def kernel_sources_sha() -> str:
@@ -89,10 +91,10 @@ def pmc_traffic(kernel: str) -> int | None:
 # %), from the counter passes of the bench workloads.
 PMC_MFMA_BUSY_PCT = {
     "chunk_fwd_kernel<Bf16,kRawW,float>": 19.2,
-    "chunk_fwd_kernel<Bf16,kRawW,float>/varlen": 19.0,
-    "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": 15.4,
-    "chunk_fwd_kernel<Bf16,kRawW,float>/precise": 13.8,
-    "chunk_bwd_kernel<Bf16,kRawW>": 12.7,
+    "chunk_fwd_kernel<Bf16,kRawW,float>/varlen": 18.9,
+    "chunk_fwd_kernel<Bf16,kRawW,float>/statetune": 15.2,
+    "chunk_fwd_kernel<Bf16,kRawW,float>/precise": 13.5,
+    "chunk_bwd_kernel<Bf16,kRawW>": 12.9,
 }
 
 
