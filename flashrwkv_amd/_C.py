@@ -61,6 +61,16 @@ def recurrent_fp32_forward_internal(query_start_loc, state_indices, state, r,
         int(max_seqlen))
 
 
+def set_recurrent_long_route(route):
+    """Route of long bf16 sequences in the fp32-state op (0 split-precision
+    chunk kernel, 1 per-token fp32 kernel); returns the previous route."""
+    return int(ops.set_recurrent_long_route(int(route)))
+
+
+def recurrent_long_route():
+    return int(ops.recurrent_long_route())
+
+
 def loaded_libraries() -> list[str]:
     """Absolute paths of the native libraries this facade loaded."""
     return [str(HIP_LIBRARY), str(OPS_LIBRARY)]

@@ -15,6 +15,9 @@
 #include <torch/custom_class.h>
 #include <torch/library.h>
 
+#include <hip/hip_runtime_api.h>
+
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <limits>
@@ -36,6 +39,37 @@ void check_rc(int rc) {
 void* current_stream(const Tensor& t) {
   return c10::hip::getCurrentHIPStream(t.device().index()).stream();
 }
+
+// True while the current stream of t's device is being captured into a HIP
+// graph. A query that fails (the legacy stream during another thread's
+// global-mode capture) counts as capturing; its error is cleared so that the
+// next launch check does not report it.
+bool stream_is_capturing(const Tensor& t) {
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  const hipError_t err =
+      hipStreamIsCapturing(static_cast<hipStream_t>(current_stream(t)), &status);
+  if (err != hipSuccess) {
+    (void)hipGetLastError();
+    return true;
+  }
+  return status != hipStreamCaptureStatusNone;
+}
+
+// The chunked MFMA kernels (prefill, training forward and backward, replay)
+// have not been run inside a captured HIP graph: the one capture of an
+// autograd training step that held them ended in a host segmentation fault
+// while the capture closed, cause not found. Ops that would launch them
+// under capture therefore refuse with this error instead.
+void refuse_capture(const Tensor& t, const char* op) {
+  TORCH_CHECK(!stream_is_capturing(t), op,
+              " does not run under HIP graph capture: its chunked kernels are not validated "
+              "inside a captured graph; run it eagerly");
+}
+
+// Route of long bf16 sequences (head size 64, max_seqlen >= 64) in the
+// fp32-state recurrent op: 0 the split-precision chunk kernel (default), 1
+// the per-token fp32 kernel for every call, as the reference computes it.
+std::atomic<int> g_recurrent_long_route{0};
 
 void check_device_contiguous(const Tensor& t, const char* name) {
   TORCH_CHECK(t.is_cuda(), name, " must be CUDA");
@@ -320,6 +354,14 @@ void recurrent_impl(const Tensor& cu, const Tensor& slots, Tensor& state,
     // bad metadata fails closed inside the kernel.
     launch = device_prepare(cu, slots, r.size(0), state.size(0));
   }
+  // A max_seqlen the library does not know sends every sequence to the
+  // per-token fp32 kernel (the shape it uses for any max_seqlen above 2): when
+  // the caller asked for that route, and under graph capture, where the chunk
+  // kernels do not run.
+  if (max_seqlen > 2 &&
+      (g_recurrent_long_route.load(std::memory_order_relaxed) == 1 || stream_is_capturing(state))) {
+    max_seqlen = -1;
+  }
   check_rc(frwkv_recurrent_forward(
       io_code(r.scalar_type()), decay_mode, static_cast<int32_t>(slots.numel()),
       static_cast<int32_t>(state.size(1)), static_cast<int32_t>(state.size(2)),
@@ -331,6 +373,17 @@ void recurrent_impl(const Tensor& cu, const Tensor& slots, Tensor& state,
       v.data_ptr(), a.data_ptr(), b.data_ptr(), output.data_ptr(),
       static_cast<float>(scale), current_stream(state)));
 }
+
+// Process-wide route of long bf16 sequences in the fp32-state op (not a
+// reference op): 0 split-precision chunk kernel, 1 per-token fp32 kernel.
+// Returns the previous route.
+int64_t set_recurrent_long_route(int64_t route) {
+  TORCH_CHECK(route == 0 || route == 1,
+              "route must be 0 (split-precision chunk kernel) or 1 (per-token fp32 kernel)");
+  return g_recurrent_long_route.exchange(static_cast<int>(route));
+}
+
+int64_t recurrent_long_route() { return g_recurrent_long_route.load(); }
 
 // Public op: raw decay logits, fp16/bf16 tokens.
 void recurrent_fp32_from_decay_logits(
@@ -426,6 +479,7 @@ void chunk_impl(const Tensor& r, const Tensor& decay, const Tensor& k, const Ten
                                                               : -1;
   TORCH_CHECK(pool_code >= 0, "state_pool must be float32 or bfloat16");
   c10::DeviceGuard guard(r.device());
+  refuse_capture(r, "the chunked WKV7 forward");
   Prepared launch = device_prepare(cu, slots, r.size(0), pool.size(0));
   check_rc(frwkv_chunk_forward(
       io_code(r.scalar_type()), decay_mode, pool_code, static_cast<int32_t>(slots.numel()),
@@ -542,6 +596,7 @@ void statetune_forward_impl(const Tensor& offsets, const Tensor& starts, const T
               "state_dot_a must have shape [total_tokens,H,D] float32");
   float* interior_ptr = checked_interior(interior, r, d);
   c10::DeviceGuard guard(state.device());
+  refuse_capture(r, "the StateTune forward");
   check_rc(frwkv_statetune_forward(
       io_code(r.scalar_type()), decay_mode, static_cast<int32_t>(state.size(0)),
       static_cast<int32_t>(state.size(1)), static_cast<int32_t>(d), static_cast<int32_t>(r.size(0)),
@@ -644,6 +699,7 @@ void statetune_backward_impl(const Tensor& offsets, const Tensor& starts, const 
               "grad_initial_state must have shape [B,H,D,D] float32");
   const float* interior_ptr = checked_interior(interior, r, d);
   c10::DeviceGuard guard(r.device());
+  refuse_capture(r, "the StateTune backward");
   const bool has_dy = grad_output.has_value() && grad_output->defined();
   const bool has_ds = grad_final_state.has_value() && grad_final_state->defined();
   // Without the forward's interior states the call recomputes them into the
@@ -744,6 +800,7 @@ void clampw_forward(Tensor r, Tensor w, Tensor k, Tensor v, Tensor a, Tensor b, 
                        {&y, "y"}}, head_size);
   check_clampw_side(r, s, sa);
   c10::DeviceGuard guard(r.device());
+  refuse_capture(r, "the clampw-v3 pretraining forward");
   check_rc(frwkv_pretrain_forward(
       io_code(r.scalar_type()), FRWKV_DECAY_LOGITS, static_cast<int32_t>(r.size(0)),
       static_cast<int32_t>(r.size(1)), static_cast<int32_t>(r.size(2)),
@@ -763,6 +820,7 @@ void clampw_backward(Tensor r, Tensor w, Tensor k, Tensor v, Tensor a, Tensor b,
   const size_t ws_bytes = frwkv_pretrain_backward_workspace_bytes(
       static_cast<int32_t>(r.size(0)), static_cast<int32_t>(r.size(1)),
       static_cast<int32_t>(r.size(2)), static_cast<int32_t>(head_size));
+  refuse_capture(r, "the clampw-v3 pretraining backward");
   Tensor ws = workspace_like(r, ws_bytes);
   check_rc(frwkv_pretrain_backward(
       io_code(r.scalar_type()), FRWKV_DECAY_LOGITS, static_cast<int32_t>(r.size(0)),
@@ -911,6 +969,7 @@ void rl_infctx_replay(Tensor starts, Tensor ends, Tensor boundary, Tensor r, Ten
                 "decay_bias must have shape [H*D] or [H,D]");
   }
   c10::DeviceGuard guard(r.device());
+  refuse_capture(r, "the RL/Infctx replay");
   check_rc(frwkv_chunk_replay(
       io_code(r.scalar_type()), FRWKV_DECAY_LOGITS, static_cast<int32_t>(starts.numel()),
       static_cast<int32_t>(r.size(1)), static_cast<int32_t>(r.size(2)),
@@ -1265,6 +1324,8 @@ TORCH_LIBRARY(flashrwkv2, m) {
       "__torch__.torch.classes.flashrwkv2.MetadataTicket? "
       "validated_metadata=None, int max_seqlen=-1) -> ()",
       &recurrent_fp32_forward_internal);
+  m.def("set_recurrent_long_route(int route) -> int", &set_recurrent_long_route);
+  m.def("recurrent_long_route() -> int", &recurrent_long_route);
   m.def(
       "infer_chunk_bf16_forward_varlen(Tensor r, Tensor decay_logits, Tensor k, "
       "Tensor v, Tensor a, Tensor b, Tensor(a!) state_pool, Tensor cu_seqlens, "

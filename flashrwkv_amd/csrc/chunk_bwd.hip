@@ -1439,11 +1439,13 @@ extern "C" int frwkv_statetune_backward(
                      head_size);
   }
   // Workspace: the gradient slices (head size 256), then, when interior is
-  // null, the interior states this call recomputes from the boundaries.
+  // null, the interior states this call recomputes from the boundaries. A
+  // call without interior states always needs the workspace: whether some
+  // chunk is longer than one piece is only known on the device.
   const size_t slice_bytes = frwkv_train_slice_bytes(head_size, num_heads, total_tokens);
   const size_t need = frwkv_statetune_backward_workspace_bytes(head_size, num_heads,
                                                                total_tokens, interior != nullptr);
-  const bool fill = interior == nullptr && workspace != nullptr;
+  const bool fill = interior == nullptr;
   if ((slice_bytes > 0 || fill) && (workspace == nullptr || workspace_bytes < need)) {
     return set_error(FRWKV_ERR_INVALID_ARGUMENT,
                      "frwkv_statetune_backward: workspace of %zu bytes given, %zu needed",

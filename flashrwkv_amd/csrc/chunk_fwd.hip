@@ -786,6 +786,16 @@ __global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_ker
     seg_hi = min(seq + 1, p.num_segments);
   }
 
+  // Interior-state fill (replay layout, one segment per unit): a segment of
+  // at most one chunk has no interior state, so its unit ends before it
+  // loads the start state or any token row.
+  if (p.fill_only) {
+    if (seg_lo >= seg_hi) return;
+    const int tb = uniform(max(p.seg_starts[seg_lo], 0));
+    const int te = uniform(min(p.seg_ends[seg_lo], p.total_tokens));
+    if (te - tb <= kChunk) return;
+  }
+
   float bias[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) bias[e] = 0.0f;

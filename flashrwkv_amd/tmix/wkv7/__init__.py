@@ -172,6 +172,37 @@ def _recurrent_fp32(ns: dict, decay_mode: int | None) -> torch.Tensor:
     return output
 
 
+# Routes of long sequences in the fp32-state recurrent op (not reference API).
+LONG_ROUTE_CHUNKED = "chunked"
+LONG_ROUTE_PER_TOKEN = "per_token"
+_ROUTE_CODES = {LONG_ROUTE_CHUNKED: 0, LONG_ROUTE_PER_TOKEN: 1}
+
+
+def set_recurrent_long_route(route: str) -> str:
+    """Choose how ``infer_recurrent_fp32io16_forward_varlen`` runs long calls.
+
+    Not reference API. Calls with bf16 tokens, head size 64 and a longest
+    sequence of 64 tokens or more run, by default (``"chunked"``), on the
+    split-precision chunk kernel: its outputs meet the reference's
+    relative-RMSE gate of 0.002, but the pool it leaves differs from the
+    per-token fp32 recurrence by about 4e-4 relative RMSE (1e-7 on the
+    per-token kernel). ``"per_token"`` runs every call on the per-token fp32
+    kernel, as the reference computes it, at several times the time for long
+    sequences. Decode, short sequences, fp16 tokens and other head sizes run
+    the per-token kernel either way, and so does any call made under HIP
+    graph capture. The setting is process-wide; returns the previous route.
+    """
+    if route not in _ROUTE_CODES:
+        raise ValueError(f"route must be one of {sorted(_ROUTE_CODES)}, got {route!r}")
+    previous = C.native().set_recurrent_long_route(_ROUTE_CODES[route])
+    return LONG_ROUTE_PER_TOKEN if previous == 1 else LONG_ROUTE_CHUNKED
+
+
+def recurrent_long_route() -> str:
+    """The current route of long calls (see :func:`set_recurrent_long_route`)."""
+    return LONG_ROUTE_PER_TOKEN if C.native().recurrent_long_route() == 1 else LONG_ROUTE_CHUNKED
+
+
 def infer_recurrent_fp32io16_forward_varlen(
     r: torch.Tensor,
     decay_logits: torch.Tensor,

@@ -123,6 +123,9 @@ def pretrain_recurrent_bf16(r: torch.Tensor, w: torch.Tensor, k: torch.Tensor,
     """clampw v3 pretraining recurrence with autograd (reference ``pretrain.py:109-126``)."""
     layout = _Layout.of((r, w, k, v, a, b), head_size)
     C.native()
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("pretrain_recurrent_bf16 does not run under HIP graph capture: "
+                           "its chunked kernels are not validated inside a captured graph")
     return _ClampwV3.apply(layout, r, w, k, v, a, b)
 
 

@@ -10,8 +10,18 @@ decay.
 Caller chunks may have any length. The kernels walk a chunk in pieces of P
 tokens (P = 64 at head size 64, 16 at 128 and 256); the forward keeps the
 state at each interior piece start in a buffer indexed by (piece start) / P,
-which the backward reads. Nothing reads the chunk metadata on the host, so a
-training step never synchronises and can be captured in a HIP graph.
+which the backward reads. That buffer holds ceil(N / P) x H x D x D fp32
+values from the forward to the backward (16 KiB per 64 token-heads at D = 64,
+64 KiB per 16 token-heads at D = 128, 256 KiB at D = 256) whether or not a
+chunk is longer than P. Callers whose chunks never exceed P tokens pass
+``max_chunk_len`` to ``statetune_recurrent_internal``: the forward then keeps
+no buffer, and the backward recomputes any interior state it needs into a
+temporary workspace, so a wrong hint costs time, never correctness.
+
+Nothing reads the chunk metadata on the host, so a training step never
+synchronises. It does not run under HIP graph capture: the chunked kernels are
+not validated inside a captured graph, and the operator raises RuntimeError
+when called on a capturing stream.
 """
 
 from __future__ import annotations
@@ -77,9 +87,13 @@ def _piece_len(head_size: int) -> int:
     return 64 if head_size == 64 else 16
 
 
-def _interior(r: torch.Tensor, heads: int, d: int) -> torch.Tensor:
-    """Buffer for the interior piece-start states: ceil(N / P) slots."""
+def _interior(r: torch.Tensor, heads: int, d: int,
+              max_chunk_len: int | None) -> torch.Tensor | None:
+    """Buffer for the interior piece-start states: ceil(N / P) slots, or None
+    when the caller states that no chunk is longer than one piece."""
     p = _piece_len(d)
+    if max_chunk_len is not None and max_chunk_len <= p:
+        return None
     slots = (r.shape[0] + p - 1) // p
     return torch.empty((slots, heads, d, d), device=r.device, dtype=torch.float32)
 
@@ -91,12 +105,12 @@ class _StateTune(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, initial_state, offsets, starts, ends, r, decay, k, v, a, b, scale,
-                decay_mode):
+                decay_mode, max_chunk_len):
         state = initial_state.detach().contiguous().clone()
         heads, d = state.shape[1], state.shape[2]
         boundary = torch.empty((starts.numel(), heads, d, d), device=state.device,
                                dtype=torch.float32)
-        interior = _interior(r, heads, d)
+        interior = _interior(r, heads, d, max_chunk_len)
         output = torch.empty_like(v)
         state_dot_a = torch.empty_like(r, dtype=torch.float32)
         C.native().statetune_forward_internal(offsets, starts, ends, state, r, decay, k, v, a, b,
@@ -125,14 +139,24 @@ class _StateTune(torch.autograd.Function):
         C.native().statetune_backward_internal(offsets, starts, ends, r, decay, k, v, a, b, dy,
                                                ds, boundary, *grads, grad_state, interior,
                                                ctx.scale, ctx.decay_mode)
-        return (grad_state, None, None, None, *grads, None, None)
+        return (grad_state, None, None, None, *grads, None, None, None)
 
 
 def _run(ns: dict, decay_mode: int):
     C.enforce(TOKENS, ns)
     C.enforce(METADATA, ns)
+    max_chunk_len = ns.get("max_chunk_len")
+    if max_chunk_len is not None and not (isinstance(max_chunk_len, int)
+                                          and not isinstance(max_chunk_len, bool)
+                                          and max_chunk_len > 0):
+        raise ValueError("max_chunk_len must be a positive integer or None")
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("statetune_recurrent_fp32io16 does not run under HIP graph "
+                           "capture: its chunked kernels are not validated inside a "
+                           "captured graph; run the training step eagerly")
     return _StateTune.apply(ns["state"], *(ns[n] for n in _METADATA_NAMES),
-                            *(ns[n] for n in C.PACKED_TOKENS), float(ns["scale"]), decay_mode)
+                            *(ns[n] for n in C.PACKED_TOKENS), float(ns["scale"]), decay_mode,
+                            max_chunk_len)
 
 
 def statetune_recurrent_fp32io16(initial_state, sequence_chunk_offsets, chunk_token_starts,
@@ -150,9 +174,13 @@ def statetune_recurrent_fp32io16(initial_state, sequence_chunk_offsets, chunk_to
 
 def statetune_recurrent_internal(initial_state, sequence_chunk_offsets, chunk_token_starts,
                                  chunk_token_ends, r, decay, k, v, a, b, *,
-                                 scale: float = 1.0, decay_mode: int = DECAY_RAW_W):
+                                 scale: float = 1.0, decay_mode: int = DECAY_RAW_W,
+                                 max_chunk_len: int | None = None):
     """StateTune with an explicit decay mode (not reference API):
-    ``DECAY_RAW_W`` takes the retention itself, and its gradient is dL/dw."""
+    ``DECAY_RAW_W`` takes the retention itself, and its gradient is dL/dw.
+    ``max_chunk_len`` is an optional upper bound on the chunk lengths: at or
+    below the kernels' piece length (64 tokens at head size 64, 16 at 128 and
+    256) the forward keeps no interior-state buffer for the backward."""
     if decay_mode not in (DECAY_LOGITS, DECAY_RAW_W):
         raise ValueError("decay_mode must be DECAY_LOGITS or DECAY_RAW_W")
     ns = dict(locals())

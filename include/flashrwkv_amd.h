@@ -258,16 +258,17 @@ int frwkv_statetune_interior(int io_dtype, int decay_mode, int32_t num_heads,
  * adjoint in reverse; it never divides by the decay, and any chunk length
  * and any retention are supported (pieces whose decay span exceeds the
  * kernel's single-reference limit run as 16- and 4-token sub-pieces).
- * interior: the forward's interior states, or NULL; then, with a workspace,
- * the call first recomputes them into it (frwkv_statetune_interior), and
- * without one every chunk must span at most P tokens (a longer one makes its
- * sequence's gradients NaN). grad_output [total_tokens,H,D] (io dtype) and
+ * interior: the forward's interior states, or NULL; then the call first
+ * recomputes them into the workspace (frwkv_statetune_interior), which must
+ * be given (FRWKV_ERR_INVALID_ARGUMENT otherwise, before anything runs).
+ * grad_output [total_tokens,H,D] (io dtype) and
  * grad_final_state [B,H,D,D] fp32 may be NULL (zero). Writes every token
  * gradient (grad_decay is dL/d(decay input): logits or retention per
  * decay_mode) and grad_initial_state [B,H,D,D] fp32.
  * workspace: frwkv_statetune_backward_workspace_bytes(head_size, H,
  * total_tokens, interior != NULL) bytes of device memory, 256-byte aligned;
- * it may be NULL when that is 0 (head sizes 64 and 128 with interior given).
+ * it may be NULL only when that is 0 (head sizes 64 and 128 with interior
+ * given).
  * Replaces statetune_recurrent_fp32io16_backward_cuda
  * (csrc/sm90/tmix/wkv7/statetune_recurrent_fp32io16_backward.cu:49-676;
  * binding statetune_recurrent_fp32io16_backward.cpp:34-82). head_size 64

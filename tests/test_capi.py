@@ -205,3 +205,25 @@ def test_chunk_forward_rejects_too_many_heads_without_a_gpu(lib):
                                  *ptrs, ctypes.c_float(1.0), null)
     assert rc == 2
     assert b"at most 65536 heads" in lib.frwkv_last_error()
+
+
+def test_backward_without_interior_or_workspace_is_refused_without_a_gpu():
+    """frwkv_statetune_backward at head size 64 with neither the forward's
+    interior states nor a workspace is an argument error before any launch:
+    whether a chunk spans more than one 64-token piece is only known on the
+    device, and such a chunk needs the recomputed interior states (a 100-token
+    chunk here; the placeholder pointers are never used)."""
+    from flashrwkv_amd import capi
+
+    lib = capi.library()
+    fake = ctypes.c_void_p(256)
+    null = ctypes.c_void_p()
+    # io bf16, raw decay, B=1, H=1, D=64, N=100, one chunk.
+    head = [2, 1, 1, 1, 64, 100, 1]
+    metadata_and_boundary = [fake] * 4           # offsets, starts, ends, boundary
+    tensors = [fake, fake, null, fake, fake, fake, fake, fake, fake]  # r..b, dy, dS_T
+    grads = [fake] * 7
+    rc = lib.frwkv_statetune_backward(*head, *metadata_and_boundary, null, *tensors[:2],
+                                      *tensors[2:], *grads, null, 0, 1.0, None)
+    assert rc == 1
+    assert b"workspace of 0 bytes given" in lib.frwkv_last_error()

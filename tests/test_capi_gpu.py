@@ -17,6 +17,7 @@ import torch
 
 from flashrwkv_amd import capi, workloads
 from oracle import oracle
+from tests import parity
 
 pytestmark = pytest.mark.gpu
 
@@ -36,9 +37,11 @@ def _np(t):
 
 
 def _check(name, actual, expected, tol):
-    err = oracle.max_rel_error(_np(actual), expected)
-    print(f"{name}: max-rel {err:.3e}")
-    assert np.isfinite(err) and err <= tol, f"{name}: {err:.3e} > {tol}"
+    """Normwise ``tol``; per row (floor 1e-2) and elementwise (floor 0.1)
+    within 0.1 -- bf16 chunked forward and backward, measured at most 4.4e-2
+    and 3.0e-2."""
+    return parity.check(name, actual, expected, tol, row_tol=0.1, elem_tol=0.1,
+                        elem_floor=0.1)
 
 
 def _case(lengths, dtype, seed, heads=3):

@@ -27,6 +27,7 @@ from flashrwkv_amd.tmix.wkv7.chunk import (
     infer_chunk_bf16_forward_varlen,
 )
 from oracle import oracle
+from tests import parity
 
 pytestmark = pytest.mark.gpu
 
@@ -62,10 +63,10 @@ def _oracle(case, *, w=None, pool=None, scale=1.0):
 
 
 def _check(name, actual, expected, tol=TOL):
-    err = oracle.max_rel_error(_np(actual), expected)
-    print(f"{name}: max-rel {err:.3e}")
-    assert np.isfinite(err) and err <= tol, f"{name}: {err:.3e} > {tol}"
-    return err
+    """Normwise ``tol``; per row (floor 1e-2) and elementwise (floor 0.1)
+    within 8e-2 (measured at most 2.9e-2 and 3.9e-2)."""
+    return parity.check(name, actual, expected, tol, row_tol=8e-2, elem_tol=8e-2,
+                        elem_floor=0.1)
 
 
 @pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
@@ -279,3 +280,37 @@ def test_public_chunk_wrapper_rejects_bad_arguments_before_launch():
         infer_chunk_bf16_forward_varlen(*args, **{**kw, "state_pool": pool.float()})
     with pytest.raises(ValueError, match="finite"):
         infer_chunk_bf16_forward_varlen(*args, scale=float("inf"), **kw)
+
+
+def test_chunked_ops_refuse_graph_capture_before_launch():
+    """On a capturing stream the chunked forward (binding check) and the
+    StateTune training op (Python check) raise RuntimeError before they
+    launch anything; the capture holds only an elementwise add, and the pool
+    and the tokens are untouched."""
+    from flashrwkv_amd.tmix.wkv7.statetune import statetune_recurrent_internal
+
+    case = workloads.make_case(lengths=(70,), heads=1, head_size=64, dtype=torch.bfloat16,
+                               seed=5, state_std=0.1)
+    d = _dev(case)
+    pool = d["state_pool"].clone()
+    side = torch.cuda.Stream()
+    x = torch.zeros(4, device=DEV)
+    meta = [torch.from_numpy(m).to(DEV) for m in oracle.chunk_metadata((70,), 64)[:3]]
+    torch.cuda.synchronize()
+    graphs = []
+    for call in (
+        lambda: chunk_forward_internal(d["r"], d["w"], d["k"], d["v"], d["a"], d["b"],
+                                       state_pool=pool, cu_seqlens=d["cu_seqlens"],
+                                       state_indices=d["state_indices"],
+                                       decay_mode=DECAY_RAW_W),
+        lambda: statetune_recurrent_internal(pool, *meta, d["r"], d["w"], d["k"], d["v"],
+                                             d["a"], d["b"], decay_mode=DECAY_RAW_W),
+    ):
+        graph = torch.cuda.CUDAGraph()
+        graphs.append(graph)
+        with pytest.raises(RuntimeError, match="graph capture"):
+            with torch.cuda.graph(graph, stream=side):
+                x.add_(1.0)
+                call()
+    torch.cuda.synchronize()
+    assert torch.equal(pool, d["state_pool"])

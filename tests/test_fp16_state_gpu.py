@@ -28,6 +28,7 @@ from flashrwkv_amd.tmix.wkv7 import (
     prepare_recurrent_metadata,
 )
 from oracle import oracle
+from tests import parity
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda")
@@ -76,10 +77,11 @@ def _check(name, actual, expected):
     actual = _np(actual).astype(np.float64)
     expected = np.asarray(expected, dtype=np.float64)
     rmse = oracle.relative_rmse(actual, expected)
-    worst = oracle.max_rel_error(actual, expected)
-    print(f"{name}: rel-rmse {rmse:.2e} max-rel {worst:.2e}")
-    assert np.isfinite(actual).all()
-    assert rmse <= RMSE_TOL and worst <= MAX_TOL, f"{name}: rmse {rmse:.3e} max {worst:.3e}"
+    print(f"{name}: rel-rmse {rmse:.2e}")
+    assert rmse <= RMSE_TOL, f"{name}: rmse {rmse:.3e}"
+    # Per row (floor 1e-2) within 4e-3 and elementwise (floor 0.1) within
+    # 5e-3: measured at most 1.5e-3 and 2.3e-3 (fp16 state rounding).
+    parity.check(name, actual, expected, MAX_TOL, row_tol=4e-3, elem_tol=5e-3, elem_floor=0.1)
 
 
 def _run(tokens, cu, slots, pool, elapsed, decay_bias, **kw):

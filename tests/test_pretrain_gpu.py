@@ -22,6 +22,7 @@ import flashrwkv_amd
 from flashrwkv_amd import capi
 from flashrwkv_amd.tmix.wkv7 import pretrain_recurrent_bf16
 from oracle import oracle
+from tests import parity
 
 TOL = 2e-2
 NAMES = ("r", "w", "k", "v", "a", "b")
@@ -52,10 +53,15 @@ def _np(t):
 
 
 def _check(name, actual, expected, tol=TOL):
-    err = oracle.max_rel_error(_np(actual) if isinstance(actual, torch.Tensor) else actual,
-                               expected)
-    print(f"{name}: max-rel {err:.3e}")
-    assert np.isfinite(err) and err <= tol, f"{name}: {err:.3e} > {tol}"
+    """Normwise ``tol``; per row (floor 1e-2) within 0.5 and elementwise
+    (floor 0.1) within 0.2 (measured at most 0.29 and 0.11). These cases'
+    a and b are independent N(0, s^2) vectors (the reference test's recipe),
+    not RWKV-7's a = -kk, b = kk g with |kk| = 1: at s = 0.3, |a||b| is about
+    6, the chunk form's (I - Lab)^-1 has entries far above 1 and amplifies
+    the bf16 rounding of its operands, so low-norm rows carry relative errors
+    that the normalised inputs of the other tests (about 1e-2) do not."""
+    return parity.check(name, actual, expected, tol, row_tol=0.5, elem_tol=0.2,
+                        elem_floor=0.1)
 
 
 def _oracle(values, dy, batch, tokens, heads, d=64):

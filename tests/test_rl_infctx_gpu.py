@@ -26,6 +26,7 @@ from flashrwkv_amd.rl_infctx.wkv7 import (
     rl_infctx_chunk_fp32io16_factor_recompute,
 )
 from oracle import oracle
+from tests import parity
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda")
@@ -44,10 +45,10 @@ def _tol(d, dtype=torch.float16):
 
 
 def _check(name, actual, expected, tol):
-    err = oracle.max_rel_error(_np(actual) if isinstance(actual, torch.Tensor) else actual,
-                               expected)
-    print(f"{name}: max-rel {err:.3e}")
-    assert np.isfinite(err) and err <= tol, f"{name}: {err:.3e} > {tol}"
+    """Normwise ``tol``; per row (floor 1e-2) within 4e-2 and elementwise
+    (floor 0.1) within 5e-2 (measured at most 1.1e-2 and 2.5e-2)."""
+    return parity.check(name, actual, expected, tol, row_tol=4e-2, elem_tol=5e-2,
+                        elem_floor=0.1)
 
 
 def _oracle(inputs, pool, cu, slots, *, scale=1.0, bias=None):

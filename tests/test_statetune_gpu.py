@@ -23,6 +23,7 @@ from flashrwkv_amd.tmix.wkv7.statetune import (
     statetune_recurrent_internal,
 )
 from oracle import oracle
+from tests import parity
 
 pytestmark = pytest.mark.gpu
 
@@ -44,9 +45,12 @@ def _np(t):
 
 
 def _check(name, actual, expected, tol=TOL):
-    err = oracle.max_rel_error(_np(actual), expected)
-    print(f"{name}: max-rel {err:.3e}")
-    assert np.isfinite(err) and err <= tol, f"{name}: {err:.3e} > {tol}"
+    """Normwise ``tol``; per row (floor 1e-2) within 0.15 and elementwise
+    (floor 0.1) within 0.1. Measured at most 7.9e-2 (dv rows under strong
+    decay, where the recomputed sub-piece states are summed over many small
+    terms) and 5.2e-2."""
+    return parity.check(name, actual, expected, tol, row_tol=0.15, elem_tol=0.1,
+                        elem_floor=0.1)
 
 
 def _run(case, meta, *, scale, ds_std=0.01, seed=5, decay_mode=DECAY_RAW_W, public=False):
@@ -393,3 +397,31 @@ def test_large_heads_long_sequence(head_size):
     ref_out, ref_grads = _oracle(case, meta, _np(case["w"]), scale=1.0, dy=dy, ds=ds,
                                  batch=len(lengths))
     _compare(out, grads, ref_out, ref_grads)
+
+
+@pytest.mark.parametrize("lengths,chunk,hint", [((130, 64, 33), 64, 64), ((200, 50), 100, 64)])
+def test_max_chunk_len_hint_keeps_no_interior_and_changes_no_result(lengths, chunk, hint):
+    """statetune_recurrent_internal(max_chunk_len=...) at or below the piece
+    length keeps no interior buffer; the backward then recomputes what it
+    needs into its workspace, so the gradients equal the run without the hint
+    bit for bit even when the hint is wrong (chunks of 100 tokens here)."""
+    meta = oracle.chunk_metadata(lengths, chunk)
+    case = workloads.make_case(lengths=lengths, heads=2, head_size=64, dtype=torch.bfloat16,
+                               seed=400 + chunk, state_std=0.1)
+    offsets, starts, ends = (torch.from_numpy(x).to(DEV) for x in meta[:3])
+    batch = len(lengths)
+    g = torch.Generator().manual_seed(9)
+    dy = torch.randn(case["v"].shape, generator=g).to(torch.bfloat16).to(DEV)
+    ds = (torch.randn((batch, 2, 64, 64), generator=g) * 0.01).to(DEV)
+    results = []
+    for max_chunk_len in (None, hint):
+        toks = [case[nm].to(DEV).requires_grad_(True) for nm in NAMES]
+        s0 = case["state_pool"][:batch].to(DEV).requires_grad_(True)
+        y, st, _, _ = statetune_recurrent_internal(s0, offsets, starts, ends, *toks, scale=0.5,
+                                                   decay_mode=DECAY_RAW_W,
+                                                   max_chunk_len=max_chunk_len)
+        grads = torch.autograd.grad([y, st], [*toks, s0], [dy, ds])
+        results.append((y, st, *grads))
+    torch.cuda.synchronize()
+    for i, (x, e) in enumerate(zip(*results)):
+        assert torch.equal(x, e), i

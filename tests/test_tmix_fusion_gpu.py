@@ -36,6 +36,7 @@ from flashrwkv_amd.tmix.wkv7.fused import (
     tmix_fused_internal,
 )
 from oracle import oracle
+from tests import parity
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda")
@@ -54,9 +55,14 @@ def _np(t):
 
 
 def _check(actual, expected, tol, label):
-    err = oracle.max_rel_error(_np(actual), expected)
-    assert np.isfinite(err) and err <= tol, f"{label}: max-rel {err:.3e} > {tol}"
-    return err
+    """Normwise, per row (floor 1e-2) and elementwise (floor 1e-3) all within
+    ``tol``: the gates and the chain round once to fp16 or bf16 at the end
+    (measured elementwise at most 4.9e-4 for the gates, 3.8e-3 for the bf16
+    chain, 4.1e-2 fused-vs-composition outputs at floor 1e-3, which rounds
+    twice; that comparison is judged at floor 0.1)."""
+    floor = 0.1 if label.startswith("fused vs composition") else 1e-3
+    return parity.check(label, actual, expected, tol, row_tol=tol, elem_tol=tol,
+                        elem_floor=floor)
 
 
 # ------------------------------------------------------------- producer ---
