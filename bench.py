@@ -120,7 +120,8 @@ def _parse():
     p.add_argument("--warmup", type=int, default=50)
     p.add_argument("--workload", default="all",
                    choices=("all", "decode", "decode_fp16", "decode_fused", "prefill", "training",
-                            "recurrent_long", "copy", "matrix", "training_large"),
+                            "recurrent_long", "copy", "matrix", "training_large", "config0",
+                            "pretrain"),
                    help="all: decode headline line plus the prefill, training and "
                         "long-sequence legs; matrix: the reference operator benchmark's "
                         "case matrix with its correctness gate")
@@ -184,7 +185,7 @@ def cpu_baseline_decode(batch, heads, seconds):
 
 
 def cpu_baseline_torch(lengths, heads, seconds, *, seed=97, u_low=-5.0, heads_total=None,
-                       backward=False):
+                       backward=False, dtype=None):
     """The torch fp32 restatement of the naive recurrence (oracle.forward_torch)
     on the host CPU, timed once with every available core and once with
     torch.set_num_threads(1): 1 warm-up, then repeats until ``seconds`` pass
@@ -199,7 +200,8 @@ def cpu_baseline_torch(lengths, heads, seconds, *, seed=97, u_low=-5.0, heads_to
     cores = len(os.sched_getaffinity(0))
     heads_total = heads if heads_total is None else heads_total
     case = workloads.make_case(lengths=lengths, heads=heads, head_size=64,
-                               dtype=torch.bfloat16, seed=seed, state_std=0.1, u_low=u_low)
+                               dtype=dtype or torch.bfloat16, seed=seed, state_std=0.1,
+                               u_low=u_low)
     args = [case[n].float().requires_grad_(backward) for n in ("r", "w", "k", "v", "a", "b")]
     pool = case["state_pool"].float().requires_grad_(backward)
     cu, slots = case["cu_seqlens"].numpy(), case["state_indices"].numpy()
@@ -476,8 +478,10 @@ def chunk_flops(chunk: int = 64, d: int = 64) -> int:
     return 18 * chunk * chunk * d + 8 * chunk * d * d + chunk ** 3 // 3
 
 
-def cpu_baseline_prefill(t_len, heads_total, seconds):
-    """fp64 C oracle on a bounded sample: whole (sequence, head) recurrences."""
+def cpu_baseline_prefill(t_len, heads_total, seconds, *, lengths=None, u_low=-8.0, seed=98):
+    """fp64 C oracle on a bounded sample: whole (sequence, head) recurrences,
+    one sequence of ``t_len`` tokens, or the packed sequences ``lengths``
+    (the oracle loops over them one by one)."""
     import numpy as np
     import torch
 
@@ -486,10 +490,12 @@ def cpu_baseline_prefill(t_len, heads_total, seconds):
 
     cores = len(os.sched_getaffinity(0))
     sample_heads = max(1, cores)
-    case = workloads.make_case(lengths=[t_len], heads=sample_heads, head_size=64,
-                               dtype=torch.bfloat16, seed=98, state_std=0.0, u_low=-8.0)
+    lengths = [t_len] if lengths is None else list(lengths)
+    t_len = sum(lengths)
+    case = workloads.make_case(lengths=lengths, heads=sample_heads, head_size=64,
+                               dtype=torch.bfloat16, seed=seed, state_std=0.0, u_low=u_low)
     args = [case[n].double().numpy() for n in ("r", "w", "k", "v", "a", "b")]
-    pool = np.zeros((1, sample_heads, 64, 64))
+    pool = np.zeros((len(lengths), sample_heads, 64, 64))
     cu = case["cu_seqlens"].numpy()
     slots = case["state_indices"].numpy()
     reps = 0
@@ -506,9 +512,10 @@ def cpu_baseline_prefill(t_len, heads_total, seconds):
         "unit": "tokens/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"{reps} x (1 sequence x {sample_heads} heads x T={t_len}) through the fp64 "
-                  f"C oracle, OpenMP over heads, {elapsed:.1f} s; token-heads/s divided by "
-                  f"H={heads_total} (heads are independent)",
+        "sample": f"{reps} x ({len(lengths)} sequence(s) of {t_len} tokens in all x "
+                  f"{sample_heads} heads) through the fp64 C oracle, OpenMP over heads, "
+                  f"{elapsed:.1f} s; token-heads/s divided by H={heads_total} (heads are "
+                  f"independent)",
     }
 
 
@@ -781,7 +788,7 @@ def bench_prefill_varlen(args):
     nbytes = n_tok * heads * 7 * d * 2 + 2 * batch * heads * d * d * 4
     tflops = flops / (kernel_ms * 1e-3) / 1e12
     gbps = nbytes / (kernel_ms * 1e-3) / 1e9
-    return {
+    out = {
         "workload": f"wkv7_chunked_prefill_cfg3_varlen: {batch} sequences, lengths "
                     f"U[128,4096] (seeded; N={n_tok}), H=32, D=64, bf16 io, u~U(-8,0), "
                     "fp32 pool",
@@ -796,6 +803,15 @@ def bench_prefill_varlen(args):
         "algorithmic_flops": flops,
         "algorithmic_bytes": nbytes,
     }
+    if args.cpu_seconds > 0:
+        # The batch's first sequences, whole, as the oracle loops over them
+        # (the C oracle one by one; the torch restatement over the packed run).
+        sample = lengths[:4]
+        out["cpu_baseline"] = cpu_baseline_prefill(0, heads, args.cpu_seconds, lengths=sample,
+                                                   seed=20260810)
+        out["cpu_baseline"]["torch_fp32"] = cpu_baseline_torch(
+            sample, 8, args.cpu_seconds / 2, seed=20260810, u_low=-8.0, heads_total=heads)
+    return out
 
 
 def bench_training(args):
@@ -1002,6 +1018,179 @@ def bench_training_large(args):
     return out
 
 
+def bench_config0(args):
+    """benchmark config 0, the reference's CPU-runnable case: fp32 io, B=1,
+    T=64, H=32, D=64, S0 = 0, raw retention. fp32 tokens always run the
+    per-token fp32 kernel (four waves per (sequence, head), 32 units), so the
+    call is bound by its 64 dependent steps, not by bandwidth: the figures are
+    microseconds per call and tokens/s; the HBM line only states the rate the
+    call's 4.72 MB reach. kernel_us: 50 calls captured in one HIP graph and
+    replayed (no host launch cost); op_us: the public-op path per eager call
+    with a prepared ticket."""
+    import torch
+
+    import flashrwkv_amd
+    from flashrwkv_amd import capi, workloads
+    from flashrwkv_amd.tmix.wkv7 import DECAY_RAW_W, prepare_recurrent_metadata
+
+    if flashrwkv_amd._C is None:
+        raise SystemExit("flashrwkv_amd native library is not built")
+    ops = flashrwkv_amd._C.ops
+    dev = torch.device("cuda:0")
+    t_len, heads, d = 64, 32, 64
+    case = workloads.make_case(lengths=[t_len], heads=heads, head_size=d, dtype=torch.float32,
+                               seed=20260804, state_std=0.0)
+    tok = {n: case[n].to(dev) for n in ("r", "w", "k", "v", "a", "b")}
+    cu, slots = case["cu_seqlens"].to(dev), case["state_indices"].to(dev)
+    pool = torch.zeros((1, heads, d, d), device=dev)
+    out_t = torch.empty_like(tok["v"])
+    status, cu_snap, slot_snap = capi.metadata_validate(cu, slots, t_len, 1)
+    stream = torch.cuda.Stream(device=dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    per_graph, replays = 50, 20
+
+    def call():
+        capi.recurrent_forward(tok["r"], tok["w"], tok["k"], tok["v"], tok["a"], tok["b"],
+                               state_pool=pool, cu_seqlens=cu_snap, state_indices=slot_snap,
+                               metadata_status=status, output=out_t, max_seqlen=t_len)
+
+    with torch.cuda.stream(stream):
+        call()
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(per_graph):
+                call()
+        graph.replay()
+        stream.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(replays):
+            graph.replay()
+        e1.record(stream)
+        e1.synchronize()
+    kernel_ms = e0.elapsed_time(e1) / (per_graph * replays)
+    with torch.cuda.stream(stream):
+        ticket = prepare_recurrent_metadata(cu, slots, total_tokens=t_len, state_pool_size=1,
+                                            max_seqlen=t_len)
+        op_ms = _kernel_ms(lambda: ops.recurrent_fp32_forward_internal(
+            cu, slots, pool, tok["r"], tok["w"], tok["k"], tok["v"], tok["a"], tok["b"],
+            out_t, 1.0, DECAY_RAW_W, None, ticket, t_len), 200, stream)
+    nbytes = t_len * heads * 7 * d * 4 + 2 * heads * d * d * 4
+    flops = 9 * d * d * t_len * heads
+    gbps = nbytes / (kernel_ms * 1e-3) / 1e9
+    out = {
+        "workload": "wkv7_recurrent_cfg0: fp32 io, B=1, T=64, H=32, D=64, S0=0, raw retention "
+                    "(per-token fp32 kernel)",
+        "kernel_us": round(kernel_ms * 1e3, 2),
+        "op_us": round(op_ms * 1e3, 2),
+        "tokens_per_s": round(t_len / (kernel_ms * 1e-3), 1),
+        "bound": "latency (64 dependent steps per (sequence, head); 32 units)",
+        "hbm": {"achieved_GBps": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                "frac": round(gbps / HBM_PEAK_GBPS, 4), "algorithmic_bytes_per_call": nbytes},
+        "algorithmic_flops_per_call": flops,
+        "timing": "kernel_us: 50 calls in one HIP graph, replayed 20 times, HIP events on "
+                  "the launch stream; op_us: the internal op with a prepared ticket, eager",
+    }
+    if args.cpu_seconds > 0:
+        tb = cpu_baseline_torch([t_len], heads, args.cpu_seconds / 2, seed=20260804,
+                                heads_total=heads, dtype=torch.float32)
+        out["cpu_baseline"] = {
+            "value": tb["all_cores"]["value"], "unit": "tokens/s",
+            "cores": tb["all_cores"]["threads"], "kind": "port",
+            "sample": tb["sample"] + " (fp32 tokens), every core",
+            "one_thread": tb["one_thread"],
+            "fp64_c_oracle": cpu_baseline_prefill(t_len, heads, args.cpu_seconds / 2,
+                                                  u_low=-5.0, seed=20260804),
+        }
+    return out
+
+
+def bench_pretrain(args):
+    """clampw-v3 pretraining at the reference pretraining bench's shape
+    (benchmarks/tmix/wkv7/pretrain/bench.py:16-63): B=2, T=512, H=12, D=64,
+    dense bf16 [B,T,C] inputs N(0,1) * 0.05 (w as decay logits), dY ~ N(0,1);
+    one step = pretrain_recurrent_bf16 forward + torch.autograd.grad to all
+    six inputs, as that bench times it (5 warm-up steps). The shape has 192
+    chunk-heads for 256 CUs, so the step is bound by the chunk recurrence's
+    latency, not by bandwidth or the matrix cores."""
+    import torch
+
+    import flashrwkv_amd
+    from flashrwkv_amd import capi
+    from flashrwkv_amd.tmix.wkv7 import pretrain_recurrent_bf16
+
+    if flashrwkv_amd._C is None:
+        raise SystemExit("flashrwkv_amd native library is not built")
+    dev = torch.device("cuda:0")
+    batch, t_len, heads, d = 2, 512, 12, 64
+    shape = (batch, t_len, heads * d)
+    gen = torch.Generator(device=dev).manual_seed(20260806)
+    values = tuple((torch.randn(shape, generator=gen, device=dev) * 0.05).to(torch.bfloat16)
+                   .requires_grad_() for _ in range(6))
+    grad_output = torch.randn(shape, generator=gen, device=dev).to(torch.bfloat16)
+
+    def step():
+        y = pretrain_recurrent_bf16(*values)
+        torch.autograd.grad(y, values, grad_output)
+
+    for _ in range(5):
+        step()
+    torch.cuda.synchronize()
+    iters = max(10, 5 * args.training_steps)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        step()
+    e1.record()
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    # The two kernels alone through the C ABI.
+    stream = torch.cuda.Stream(device=dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    split = [v.detach().view(batch, t_len, heads, d) for v in values]
+    y_k = torch.empty_like(split[3])
+    bnd = torch.empty((batch, heads, t_len // 16, d, d), device=dev)
+    sda = torch.empty((batch, t_len, heads, d), device=dev, dtype=torch.float32)
+    grads = [torch.empty_like(t) for t in split]
+    dy = grad_output.view(batch, t_len, heads, d)
+    fwd_ms = _kernel_ms(lambda: capi.pretrain_forward(*split, output=y_k, boundary=bnd,
+                                                      state_dot_a=sda), iters, stream)
+    bwd_ms = _kernel_ms(lambda: capi.pretrain_backward(*split, grad_output=dy, boundary=bnd,
+                                                       grads=grads), iters, stream)
+    chunk_heads = batch * heads * (t_len // 64)
+    flops = 3 * chunk_heads * chunk_flops()
+    tflops = flops / ((fwd_ms + bwd_ms) * 1e-3) / 1e12
+    out = {
+        "workload": "clampw-v3 pretraining, reference bench shape: B=2, T=512, H=12, D=64, "
+                    "bf16, decay logits, S0=0",
+        "ms_per_step": round(ms, 4),
+        "train_tokens_per_s": round(batch * t_len / (ms * 1e-3), 1),
+        "kernel_ms": {"forward": round(fwd_ms, 4), "backward": round(bwd_ms, 4)},
+        "achieved_TFLOPs": round(tflops, 3),
+        "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 5),
+        "algorithmic_flops_per_step": flops,
+        "bound": "latency (192 chunk-heads, 8 chunks each, on 256 CUs)",
+        "timing": "ms_per_step: autograd forward + torch.autograd.grad, as the reference "
+                  "bench; kernel_ms: the two kernels alone through the C ABI",
+        "iterations": iters,
+    }
+    if args.cpu_seconds > 0:
+        tb = cpu_baseline_torch([t_len] * batch, heads, args.cpu_seconds / 2, seed=20260806,
+                                heads_total=heads, backward=True)
+        out["cpu_baseline"] = {
+            "value": tb["all_cores"]["value"], "unit": "train tokens/s",
+            "cores": tb["all_cores"]["threads"], "kind": "port",
+            "sample": tb["sample"] + ", every core (RWKV-7 input distributions and raw "
+                      "retention: the same arithmetic as the logits form)",
+            "one_thread": tb["one_thread"],
+            "fp64_c_oracle": cpu_baseline_training(t_len, heads, args.cpu_seconds / 2),
+        }
+    return out
+
+
 def bench_copy(args):
     """A plain device copy of known size: the calibration run for the
     FETCH_SIZE / WRITE_SIZE counters (bytes per dispatch vs counter KiB)."""
@@ -1079,13 +1268,19 @@ def bench_recurrent_long(args):
         "mfma_busy_pct": pmc_mfma_busy(kernel),
         "kernel": kernel, "algorithmic_bytes_per_launch": nbytes,
     }
-    return {
+    out = {
         "workload": "wkv7_recurrent_long_cfg2: B=8, T=4096, H=32, D=64, bf16 io, fp32 state",
         "recurrent_op": op,
         "per_token_kernel": leg(token_ms, "recurrent_fp32_kernel"),
         "bf16_chunk_op": leg(chunk_ms, "chunk_fwd_kernel, bf16 products"),
         "algorithmic_bytes": nbytes,
     }
+    if args.cpu_seconds > 0:
+        out["cpu_baseline"] = cpu_baseline_prefill(t_len, heads, args.cpu_seconds, u_low=-5.0,
+                                                   seed=20260806)
+        out["cpu_baseline"]["torch_fp32"] = cpu_baseline_torch(
+            [t_len], 8, args.cpu_seconds / 2, seed=20260806, heads_total=heads)
+    return out
 
 
 # The reference operator benchmark's case matrix (benchmarks/tmix/wkv7/bench.py:132-172):
@@ -1294,6 +1489,11 @@ def bench_matrix(args):
             "rows": rows}
 
 
+def _progress(leg: str) -> None:
+    """One line per finished leg on stderr (stdout carries only the JSON line)."""
+    print(f"[bench] {leg} done", file=sys.stderr, flush=True)
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -1330,15 +1530,28 @@ def main():
         line = {"metric": METRIC, "matrix": bench_matrix(args)}
     elif args.workload == "training_large":
         line = {"metric": METRIC, "training_large_heads": bench_training_large(args)}
+    elif args.workload == "config0":
+        line = {"metric": METRIC, "recurrent_cfg0": bench_config0(args)}
+    elif args.workload == "pretrain":
+        line = {"metric": METRIC, "pretrain_clampw": bench_pretrain(args)}
     else:
         line = bench_decode(args)
+        _progress("decode")
         if args.workload == "all":
-            line["decode_fp16_state"] = bench_decode(args, fp16_state=True)
-            line["decode_tmix_fused"] = bench_decode_fused(args)
-            line["chunked_prefill"] = bench_prefill(args)
-            line["chunked_prefill"]["varlen"] = bench_prefill_varlen(args)
-            line["training"] = bench_training(args)
-            line["recurrent_long"] = bench_recurrent_long(args)
+            legs = (("decode_fp16_state", lambda: bench_decode(args, fp16_state=True)),
+                    ("decode_tmix_fused", lambda: bench_decode_fused(args)),
+                    ("chunked_prefill", lambda: bench_prefill(args)),
+                    ("varlen", lambda: bench_prefill_varlen(args)),
+                    ("training", lambda: bench_training(args)),
+                    ("recurrent_long", lambda: bench_recurrent_long(args)),
+                    ("recurrent_cfg0", lambda: bench_config0(args)),
+                    ("pretrain_clampw", lambda: bench_pretrain(args)))
+            for name, leg in legs:
+                if name == "varlen":
+                    line["chunked_prefill"]["varlen"] = leg()
+                else:
+                    line[name] = leg()
+                _progress(name)
     print(json.dumps(line), flush=True)
 
 

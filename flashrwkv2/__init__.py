@@ -26,6 +26,7 @@ _MODULES = {
     "tmix.wkv7.pretrain": "flashrwkv_amd.tmix.wkv7.pretrain",
     "tmix.kk_a_gate": "flashrwkv_amd.tmix.kk_a_gate",
     "tmix.lnx_rkvres_xg": "flashrwkv_amd.tmix.lnx_rkvres_xg",
+    "tmix.lnx_rkvres_xg.pretrain": "flashrwkv_amd.tmix.lnx_rkvres_xg.pretrain",
     "rl_infctx": "flashrwkv_amd.rl_infctx",
     "rl_infctx.wkv7": "flashrwkv_amd.rl_infctx.wkv7",
 }
@@ -58,6 +59,9 @@ from flashrwkv_amd.tmix.gates import (  # noqa: E402
     infer_tmix_kk_a_gate_forward_varlen,
     infer_tmix_lnx_rkvres_xg_forward_varlen,
 )
+from flashrwkv_amd.tmix.lnx_rkvres_xg.pretrain import (  # noqa: E402
+    pretrain_tmix_lnx_rkvres_xg_bf16,
+)
 
 __all__ = [
     "infer_chunk_bf16_forward_varlen",
@@ -70,6 +74,7 @@ __all__ = [
     "infer_tmix_lnx_rkvres_xg_forward_varlen",
     "prepare_recurrent_metadata",
     "pretrain_recurrent_bf16",
+    "pretrain_tmix_lnx_rkvres_xg_bf16",
     "rl_infctx_chunk_fp32io16",
     "rl_infctx_chunk_fp32io16_factor_recompute",
     "statetune_recurrent_fp32io16",

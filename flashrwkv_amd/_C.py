@@ -187,3 +187,19 @@ def tmix_lnx_rkvres_xg_forward_varlen(x, r, k, v, r_k, weight, bias, g, head_siz
     return direct.tmix_lnx_rkvres_xg_forward_varlen(x, r, k, v, r_k, weight, bias, g,
                                                     int(head_size), int(batch_size),
                                                     int(max_seqlen))
+
+
+def pretrain_tmix_lnx_rkvres_xg_forward(x, r, k, v, residual_scale, weight, bias, g,
+                                        head_size=64):
+    """Reference lnx_rkvres_xg/pretrain_bf16_forward.cpp:75-98: returns (output, mean, rstd)."""
+    return ops.pretrain_tmix_lnx_rkvres_xg_forward(x, r, k, v, residual_scale, weight, bias, g,
+                                                   int(head_size))
+
+
+def pretrain_tmix_lnx_rkvres_xg_backward(grad_output, x, r, k, v, residual_scale, weight, bias,
+                                         g, mean, rstd, head_size=64):
+    """Reference lnx_rkvres_xg/pretrain_bf16_backward.cpp:83-110: returns (grad_x, grad_r,
+    grad_k, grad_v, grad_residual_scale, grad_weight, grad_bias, grad_g)."""
+    return ops.pretrain_tmix_lnx_rkvres_xg_backward(grad_output, x, r, k, v, residual_scale,
+                                                    weight, bias, g, mean, rstd,
+                                                    int(head_size))

@@ -46,6 +46,9 @@ SIGNATURES = {
     "frwkv_add_vec": [_I64, _I32] + [_VP] * 4,
     "frwkv_kk_a_gate": [_INT, _I64, _I32, _I32] + [_VP] * 9,
     "frwkv_lnx_rkvres_xg": [_INT, _I64, _I32, _I32] + [_VP] * 10,
+    "frwkv_lnx_pretrain_forward": [_INT, _I64, _I32, _I32] + [_VP] * 12,
+    "frwkv_lnx_pretrain_backward_workspace_bytes": [_I64, _I32, _I32],
+    "frwkv_lnx_pretrain_backward": [_INT, _I64, _I32, _I32] + [_VP] * 20 + [_SZ, _VP],
     "frwkv_recurrent_tmix_fused_forward": [_INT] * 2 + [_I32] * 5 + [_VP] * 18 + [_F32, _VP],
 }
 
@@ -268,3 +271,31 @@ def recurrent_tmix_fused_forward(r, decay, k, v, a12, g, k_k, a0, k_a, r_k, ln_w
         _p(cu_seqlens), _p(state_indices), _p(metadata_status), _p(state_pool), _p(r),
         _p(decay), _p(decay_bias), _p(k), _p(v), _p(a12), _p(g), _p(k_k), _p(a0), _p(k_a),
         _p(r_k), _p(ln_weight), _p(ln_bias), _p(output), float(scale), _stream()))
+
+
+def lnx_pretrain_forward(x, r, k, v, residual_scale, weight, bias, g, *, output, mean, rstd,
+                         head_size=64):
+    """Training consumer forward over ``[N, C]`` (or ``[B, T, C]``) tokens;
+    ``mean`` / ``rstd`` fp32 with N * C / head_size elements."""
+    c = x.shape[-1]
+    n = x.numel() // c
+    _check(library().frwkv_lnx_pretrain_forward(
+        DTYPE[x.dtype], n, c // head_size, head_size, _p(x), _p(r), _p(k), _p(v),
+        _p(residual_scale), _p(weight), _p(bias), _p(g), _p(output), _p(mean), _p(rstd),
+        _stream()))
+
+
+def lnx_pretrain_backward(grad_output, x, r, k, v, residual_scale, weight, bias, g, mean,
+                          rstd, *, grads, head_size=64, work=None):
+    """``grads`` = (grad_x, grad_r, grad_k, grad_v, grad_residual_scale,
+    grad_weight, grad_bias, grad_g)."""
+    c = x.shape[-1]
+    n = x.numel() // c
+    need = int(library().frwkv_lnx_pretrain_backward_workspace_bytes(n, c // head_size,
+                                                                      head_size))
+    if work is None:
+        work = workspace(need, x.device)
+    _check(library().frwkv_lnx_pretrain_backward(
+        DTYPE[x.dtype], n, c // head_size, head_size, _p(grad_output), _p(x), _p(r), _p(k),
+        _p(v), _p(residual_scale), _p(weight), _p(bias), _p(g), _p(mean), _p(rstd),
+        *(_p(t) for t in grads), _p(work), 0 if work is None else work.numel(), _stream()))

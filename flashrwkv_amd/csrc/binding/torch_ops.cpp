@@ -1164,6 +1164,112 @@ void check_gate_common(const Tensor& x, const char* name, int64_t head_size,
   TORCH_CHECK(max_seqlen > 0, "max_seqlen must be positive");
 }
 
+// ------------------------------------------- lnx_rkvres_xg (training) ---
+// Reference pretrain_tmix_lnx_rkvres_xg_forward / _backward
+// (csrc/sm90/tmix/lnx_rkvres_xg/pretrain_bf16_forward.cpp:24-88,
+// pretrain_bf16_backward.cpp:24-99): the same checks, in the same order, with
+// the same messages.
+
+void check_lnx_bf16(const Tensor& t, const char* name) {
+  TORCH_CHECK(t.is_cuda() && t.is_contiguous() && t.scalar_type() == at::kBFloat16, name,
+              " must be contiguous CUDA bfloat16");
+}
+
+void check_lnx_train_inputs(const Tensor& x, const Tensor& r, const Tensor& k,
+                            const Tensor& v, const Tensor& residual_scale,
+                            const Tensor& weight, const Tensor& bias, const Tensor& g,
+                            int64_t head_size) {
+  TORCH_CHECK(head_size == 64 || head_size == 128 || head_size == 256,
+              "head_size must be one of 64, 128, or 256");
+  const std::pair<const Tensor*, const char*> all[] = {
+      {&x, "x"}, {&r, "r"}, {&k, "k"}, {&v, "v"}, {&residual_scale, "residual_scale"},
+      {&weight, "weight"}, {&bias, "bias"}, {&g, "g"}};
+  for (const auto& item : all) check_lnx_bf16(*item.first, item.second);
+  TORCH_CHECK(x.dim() == 3 && x.size(0) > 0 && x.size(1) > 0 && x.size(2) > 0 &&
+                  x.size(2) % head_size == 0,
+              "x must have shape [B,T,C] with C divisible by head_size");
+  for (const auto* t : {&r, &k, &v, &g}) {
+    TORCH_CHECK(t->sizes() == x.sizes(), "token tensors must match x");
+  }
+  const int64_t heads = x.size(2) / head_size;
+  TORCH_CHECK(residual_scale.dim() == 2 && residual_scale.size(0) == heads &&
+                  residual_scale.size(1) == head_size,
+              "residual_scale must have shape [C/head_size,head_size]");
+  TORCH_CHECK(weight.dim() == 1 && bias.dim() == 1 && weight.size(0) == x.size(2) &&
+                  bias.size(0) == x.size(2),
+              "weight and bias must have shape [C]");
+  for (const auto* t : {&r, &k, &v, &residual_scale, &weight, &bias, &g}) {
+    TORCH_CHECK(t->device() == x.device(), "lnx tensors must share a device");
+  }
+}
+
+std::tuple<Tensor, Tensor, Tensor> pretrain_tmix_lnx_rkvres_xg_forward(
+    Tensor x, Tensor r, Tensor k, Tensor v, Tensor residual_scale, Tensor weight, Tensor bias,
+    Tensor g, int64_t head_size) {
+  check_lnx_train_inputs(x, r, k, v, residual_scale, weight, bias, g, head_size);
+  c10::DeviceGuard guard(x.device());
+  const int64_t heads = x.size(2) / head_size;
+  Tensor out = at::empty_like(x);
+  Tensor mean = at::empty({x.size(0), x.size(1), heads}, x.options().dtype(at::kFloat));
+  Tensor rstd = at::empty_like(mean);
+  check_rc(frwkv_lnx_pretrain_forward(
+      FRWKV_DTYPE_BF16, x.size(0) * x.size(1), static_cast<int32_t>(heads),
+      static_cast<int32_t>(head_size), x.data_ptr(), r.data_ptr(), k.data_ptr(), v.data_ptr(),
+      residual_scale.data_ptr(), weight.data_ptr(), bias.data_ptr(), g.data_ptr(),
+      out.data_ptr(), mean.data_ptr<float>(), rstd.data_ptr<float>(), current_stream(x)));
+  return {out, mean, rstd};
+}
+
+std::vector<Tensor> pretrain_tmix_lnx_rkvres_xg_backward(
+    Tensor grad_output, Tensor x, Tensor r, Tensor k, Tensor v, Tensor residual_scale,
+    Tensor weight, Tensor bias, Tensor g, Tensor mean, Tensor rstd, int64_t head_size) {
+  TORCH_CHECK(head_size == 64 || head_size == 128 || head_size == 256,
+              "head_size must be one of 64, 128, or 256");
+  const std::pair<const Tensor*, const char*> all[] = {
+      {&grad_output, "grad_output"}, {&x, "x"}, {&r, "r"}, {&k, "k"}, {&v, "v"},
+      {&residual_scale, "residual_scale"}, {&weight, "weight"}, {&bias, "bias"}, {&g, "g"}};
+  for (const auto& item : all) check_lnx_bf16(*item.first, item.second);
+  TORCH_CHECK(x.dim() == 3 && x.size(2) > 0 && x.size(2) % head_size == 0,
+              "x must have shape [B,T,C] with C divisible by head_size");
+  for (const auto* t : {&grad_output, &r, &k, &v, &g}) {
+    TORCH_CHECK(t->sizes() == x.sizes(), "lnx token tensors must match x");
+  }
+  const int64_t heads = x.size(2) / head_size;
+  TORCH_CHECK(residual_scale.dim() == 2 && residual_scale.size(0) == heads &&
+                  residual_scale.size(1) == head_size,
+              "residual_scale must have shape [C/head_size,head_size]");
+  TORCH_CHECK(weight.dim() == 1 && weight.size(0) == x.size(2) && bias.sizes() == weight.sizes(),
+              "weight and bias must have shape [C]");
+  TORCH_CHECK(mean.dim() == 3 && mean.size(0) == x.size(0) && mean.size(1) == x.size(1) &&
+                  mean.size(2) == heads && rstd.sizes() == mean.sizes() &&
+                  mean.scalar_type() == at::kFloat && rstd.scalar_type() == at::kFloat,
+              "mean and rstd must be float32 [B,T,C/head_size]");
+  TORCH_CHECK(x.device() == mean.device() && x.device() == rstd.device(),
+              "lnx tensors must share a device");
+  for (const auto* t : {&grad_output, &r, &k, &v, &residual_scale, &weight, &bias, &g}) {
+    TORCH_CHECK(t->device() == x.device(), "lnx tensors must share a device");
+  }
+  check_device_contiguous(mean, "mean");
+  check_device_contiguous(rstd, "rstd");
+  c10::DeviceGuard guard(x.device());
+  Tensor gx = at::empty_like(x), gr = at::empty_like(x), gk = at::empty_like(x),
+         gv = at::empty_like(x), gg = at::empty_like(x);
+  Tensor g_rk = at::empty_like(residual_scale), g_w = at::empty_like(weight),
+         g_b = at::empty_like(weight);
+  const int64_t tokens = x.size(0) * x.size(1);
+  const size_t ws_bytes = frwkv_lnx_pretrain_backward_workspace_bytes(
+      tokens, static_cast<int32_t>(heads), static_cast<int32_t>(head_size));
+  Tensor ws = workspace_like(x, ws_bytes);
+  check_rc(frwkv_lnx_pretrain_backward(
+      FRWKV_DTYPE_BF16, tokens, static_cast<int32_t>(heads), static_cast<int32_t>(head_size),
+      grad_output.data_ptr(), x.data_ptr(), r.data_ptr(), k.data_ptr(), v.data_ptr(),
+      residual_scale.data_ptr(), weight.data_ptr(), bias.data_ptr(), g.data_ptr(),
+      mean.data_ptr<float>(), rstd.data_ptr<float>(), gx.data_ptr(), gr.data_ptr(),
+      gk.data_ptr(), gv.data_ptr(), g_rk.data_ptr(), g_w.data_ptr(), g_b.data_ptr(),
+      gg.data_ptr(), ws.defined() ? ws.data_ptr() : nullptr, ws_bytes, current_stream(x)));
+  return {gx, gr, gk, gv, g_rk, g_w, g_b, gg};
+}
+
 // Reference tmix_kk_a_gate_forward_varlen (kk_a_gate/infer_fp16_forward_varlen.cpp:41-75).
 std::tuple<Tensor, Tensor, Tensor> tmix_kk_a_gate_forward_varlen(
     Tensor k, Tensor k_k, Tensor a0, Tensor a12, Tensor k_a, int64_t head_size,
@@ -1324,6 +1430,16 @@ TORCH_LIBRARY(flashrwkv2, m) {
       "__torch__.torch.classes.flashrwkv2.MetadataTicket? "
       "validated_metadata=None, int max_seqlen=-1) -> ()",
       &recurrent_fp32_forward_internal);
+  m.def(
+      "pretrain_tmix_lnx_rkvres_xg_forward(Tensor x, Tensor r, Tensor k, Tensor v, "
+      "Tensor residual_scale, Tensor weight, Tensor bias, Tensor g, int head_size=64) -> "
+      "(Tensor, Tensor, Tensor)",
+      &pretrain_tmix_lnx_rkvres_xg_forward);
+  m.def(
+      "pretrain_tmix_lnx_rkvres_xg_backward(Tensor grad_output, Tensor x, Tensor r, Tensor k, "
+      "Tensor v, Tensor residual_scale, Tensor weight, Tensor bias, Tensor g, Tensor mean, "
+      "Tensor rstd, int head_size=64) -> Tensor[]",
+      &pretrain_tmix_lnx_rkvres_xg_backward);
   m.def("set_recurrent_long_route(int route) -> int", &set_recurrent_long_route);
   m.def("recurrent_long_route() -> int", &recurrent_long_route);
   m.def(

@@ -423,6 +423,51 @@ int frwkv_lnx_rkvres_xg(int io_dtype, int64_t total_tokens, int32_t num_heads,
                         const void* g, void* output, void* stream);
 
 /*
+ * Training form of the consumer (the reference's clampw-v3 pretraining
+ * pipeline), forward: out as frwkv_lnx_rkvres_xg over tokens [total_tokens,
+ * H*head_size] (dense [B,T,C] is total_tokens = B*T) with residual_scale =
+ * r_k [H,head_size], and the row statistics mean[total_tokens*H] and
+ * rstd[total_tokens*H] (fp32, row = token*H + head, i.e. the reference's
+ * [B,T,H]) that the backward reads. io_dtype F16 or BF16 (the reference op is
+ * bfloat16 only); token and parameter buffers 16-byte aligned.
+ * Replaces pretrain_tmix_lnx_rkvres_xg_cuda
+ * (csrc/sm90/tmix/lnx_rkvres_xg/pretrain_bf16_forward.cu:63-126, 318-362;
+ * binding pretrain_bf16_forward.cpp:75-98).
+ */
+int frwkv_lnx_pretrain_forward(int io_dtype, int64_t total_tokens, int32_t num_heads,
+                               int32_t head_size, const void* x, const void* r,
+                               const void* k, const void* v, const void* residual_scale,
+                               const void* weight, const void* bias, const void* g,
+                               void* output, float* mean, float* rstd, void* stream);
+
+/* Workspace bytes of frwkv_lnx_pretrain_backward: 3 x H*head_size fp32 per
+ * block of 64 tokens. */
+size_t frwkv_lnx_pretrain_backward_workspace_bytes(int64_t total_tokens, int32_t num_heads,
+                                                   int32_t head_size);
+
+/*
+ * Training backward of the consumer: from grad_output and the forward's
+ * inputs and row statistics, writes grad_x, grad_r, grad_k, grad_v, grad_g
+ * (shaped like x) and grad_residual_scale [H,head_size], grad_weight,
+ * grad_bias [H*head_size] (io dtype). The three parameter gradients are sums
+ * over all rows, formed per 64-token block in the workspace
+ * (frwkv_lnx_pretrain_backward_workspace_bytes, 16-byte aligned) and then
+ * added over the blocks in a fixed order, so results are bitwise
+ * deterministic. Replaces pretrain_tmix_lnx_rkvres_xg_backward_cuda
+ * (csrc/sm90/tmix/lnx_rkvres_xg/pretrain_bf16_backward.cu:125-275, 330-414;
+ * binding pretrain_bf16_backward.cpp:83-110).
+ */
+int frwkv_lnx_pretrain_backward(int io_dtype, int64_t total_tokens, int32_t num_heads,
+                                int32_t head_size, const void* grad_output, const void* x,
+                                const void* r, const void* k, const void* v,
+                                const void* residual_scale, const void* weight,
+                                const void* bias, const void* g, const float* mean,
+                                const float* rstd, void* grad_x, void* grad_r, void* grad_k,
+                                void* grad_v, void* grad_residual_scale, void* grad_weight,
+                                void* grad_bias, void* grad_g, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
+/*
  * The TMix chain kk_a_gate -> WKV7 recurrent step -> lnx_rkvres_xg in one
  * kernel, for decode and short sequences (fp32 state pool, head_size 64),
  * with no intermediate written to memory and none rounded to 16 bits:

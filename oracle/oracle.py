@@ -446,6 +446,63 @@ def lnx_rkvres_xg(x, r, k, v, r_k, weight, bias, g, head_size=64, eps=64.0e-5):
     return out.reshape(n, c)
 
 
+def lnx_pretrain_forward(x, r, k, v, residual_scale, weight, bias, g, head_size=64,
+                         eps=64.0e-5):
+    """The consumer's training forward (reference
+    csrc/sm90/tmix/lnx_rkvres_xg/pretrain_bf16_forward.cu:63-126), fp64 on
+    ``[N, C]`` rows (a dense ``[B, T, C]`` is N = B T): the output of
+    :func:`lnx_rkvres_xg` with ``r_k = residual_scale``, and the per-(row,
+    head) ``mean`` and ``rstd = 1 / sqrt(var + eps)`` as ``[N, H]``."""
+    x = _f64(x)
+    n, c = x.shape
+    h = c // head_size
+    xr = x.reshape(n, h, head_size)
+    mean = xr.mean(-1)
+    var = ((xr - mean[..., None]) ** 2).mean(-1)
+    out = lnx_rkvres_xg(x, r, k, v, _f64(residual_scale).reshape(-1), weight, bias, g,
+                        head_size=head_size, eps=eps)
+    return out, mean, 1.0 / np.sqrt(var + eps)
+
+
+def lnx_pretrain_backward(dout, x, r, k, v, residual_scale, weight, bias, g,
+                          head_size=64, eps=64.0e-5):
+    """Gradients of :func:`lnx_pretrain_forward`'s output (reference
+    csrc/sm90/tmix/lnx_rkvres_xg/pretrain_bf16_backward.cu:125-275), fp64, in
+    closed form per (row, head) with gy = dout g, xhat = (x - mean) rstd,
+    q = sum_d gy v, rkv = sum_d r k r_k:
+    dx = rstd (gy w - mean_d(gy w) - xhat mean_d(gy w xhat)), dv = gy rkv,
+    dr = q k r_k, dk = q r r_k, dg = dout (xhat w + b + rkv v), and the
+    parameter gradients summed over rows: dw = sum gy xhat, db = sum gy,
+    dr_k = sum q r k. Returns a dict keyed dx, dr, dk, dv, dresidual_scale
+    ([H, D]), dweight, dbias ([C]), dg."""
+    dout, x, r, k, v, g = (_f64(t) for t in (dout, x, r, k, v, g))
+    n, c = x.shape
+    h = c // head_size
+    shp = (n, h, head_size)
+    rk = _f64(residual_scale).reshape(1, h, head_size)
+    w = _f64(weight).reshape(1, h, head_size)
+    b = _f64(bias).reshape(1, h, head_size)
+    xr, rr, kr, vr, gr, do = (t.reshape(shp) for t in (x, r, k, v, g, dout))
+    mean = xr.mean(-1, keepdims=True)
+    rstd = 1.0 / np.sqrt(((xr - mean) ** 2).mean(-1, keepdims=True) + eps)
+    xhat = (xr - mean) * rstd
+    gy = do * gr
+    dxhat = gy * w
+    dx = rstd * (dxhat - dxhat.mean(-1, keepdims=True)
+                 - xhat * (dxhat * xhat).mean(-1, keepdims=True))
+    rkv = np.sum(rr * kr * rk, axis=-1, keepdims=True)
+    q = np.sum(gy * vr, axis=-1, keepdims=True)
+    out = {
+        "dx": dx, "dv": gy * rkv, "dr": q * kr * rk, "dk": q * rr * rk,
+        "dg": do * (xhat * w + b + rkv * vr),
+    }
+    out = {key: val.reshape(n, c) for key, val in out.items()}
+    out["dweight"] = np.sum(gy * xhat, axis=0).reshape(c)
+    out["dbias"] = np.sum(gy, axis=0).reshape(c)
+    out["dresidual_scale"] = np.sum(q * rr * kr, axis=0)
+    return out
+
+
 def tmix_fused(r, w, k, v, a12, g, k_k, a0, k_a, r_k, ln_weight, ln_bias, state_pool,
                cu_seqlens, state_indices, scale=1.0):
     """The fused chain, with no rounding between its stages: the producer

@@ -59,6 +59,12 @@ REFERENCE_SIGNATURES = {
     "flashrwkv2.tmix.lnx_rkvres_xg.infer_tmix_lnx_rkvres_xg_forward_varlen": (
         ["x", "r", "k", "v", "r_k", "weight", "bias", "g"],
         [("head_size", 64), ("batch_size", 1), ("max_seqlen", None)]),
+    "flashrwkv2.tmix.lnx_rkvres_xg.pretrain_tmix_lnx_rkvres_xg_bf16": (
+        ["x", "r", "k", "v", "residual_scale", "weight", "bias", "g"], [("head_size", 64)]),
+    "flashrwkv2.tmix.lnx_rkvres_xg.pretrain.pretrain_tmix_lnx_rkvres_xg_bf16": (
+        ["x", "r", "k", "v", "residual_scale", "weight", "bias", "g"], [("head_size", 64)]),
+    "flashrwkv2.pretrain_tmix_lnx_rkvres_xg_bf16": (
+        ["x", "r", "k", "v", "residual_scale", "weight", "bias", "g"], [("head_size", 64)]),
 }
 
 
@@ -297,3 +303,26 @@ def test_rl_chunk_lists_match_a_token_walk(chunk_size):
     want = _chunk_lists_loop(offsets.tolist(), chunk_size)
     for g, w in zip(got, want):
         assert g.tolist() == w
+
+
+def test_lnx_pretrain_contract_rejects_before_launch():
+    """Reference ``tmix/lnx_rkvres_xg/pretrain.py:9-30``: head size, then per
+    tensor its type and dtype/device/contiguity, then token shapes,
+    residual_scale and weight/bias shapes, all before any launch (CPU tensors
+    fail at the dtype/device check)."""
+    from flashrwkv2.tmix.lnx_rkvres_xg import pretrain_tmix_lnx_rkvres_xg_bf16 as fn
+
+    x = torch.zeros((1, 2, 64), dtype=torch.bfloat16)
+    args = [x] * 4 + [torch.zeros((1, 64), dtype=torch.bfloat16),
+                      torch.zeros(64, dtype=torch.bfloat16), torch.zeros(64, dtype=torch.bfloat16),
+                      x]
+    with pytest.raises(ValueError, match="head_size must be one of 64, 128, or 256"):
+        fn(*args, head_size=32)
+    with pytest.raises(TypeError, match="x must be a torch.Tensor"):
+        fn(None, *args[1:])
+    # Each tensor is type-checked and then dtype/device-checked before the
+    # next one, so a CPU x fails before a non-tensor r is looked at.
+    with pytest.raises(ValueError, match="x must be contiguous CUDA bfloat16"):
+        fn(x, [1], *args[2:])
+    with pytest.raises(ValueError, match="x must be contiguous CUDA bfloat16"):
+        fn(*args)

@@ -490,6 +490,80 @@ def test_lnx_rkvres_xg_constant_rows_hand_worked_row_and_heads():
     np.testing.assert_array_equal(o_a[:, :d], o_b[:, :d])
 
 
+def _lnx_case(rng, n, h, d):
+    c = h * d
+    x, r, k, v, g = (rng.standard_normal((n, c)) for _ in range(5))
+    rs = rng.standard_normal((h, d))
+    weight, bias = rng.standard_normal(c), rng.standard_normal(c)
+    return [x, r, k, v, rs, weight, bias, g]
+
+
+def test_lnx_pretrain_forward_statistics_and_output():
+    """The training forward's output is the pinned inference consumer with
+    r_k = residual_scale; mean and rstd are the row mean and
+    1 / sqrt(biased var + 64e-5), checked by explicit loops."""
+    rng = np.random.default_rng(11)
+    n, h, d = 3, 2, 8
+    args = _lnx_case(rng, n, h, d)
+    out, mean, rstd = oracle.lnx_pretrain_forward(*args, head_size=d)
+    x = args[0]
+    for t in range(n):
+        for hh in range(h):
+            row = x[t, hh * d:(hh + 1) * d]
+            m = sum(row) / d
+            var = sum((e - m) ** 2 for e in row) / d
+            assert mean[t, hh] == pytest.approx(m, rel=1e-13)
+            assert rstd[t, hh] == pytest.approx(1.0 / math.sqrt(var + 64.0e-5), rel=1e-13)
+    want = oracle.lnx_rkvres_xg(*args[:4], args[4].reshape(-1), *args[5:], head_size=d)
+    np.testing.assert_array_equal(out, want)
+
+
+def test_lnx_pretrain_backward_matches_central_differences():
+    """Every gradient of the closed-form adjoint against central finite
+    differences of L = sum(dout * out) through the fp64 forward (H=2, D=4)."""
+    rng = np.random.default_rng(12)
+    n, h, d = 3, 2, 4
+    args = _lnx_case(rng, n, h, d)
+    dout = rng.standard_normal((n, h * d))
+    grads = oracle.lnx_pretrain_backward(dout, *args, head_size=d)
+    names = ("dx", "dr", "dk", "dv", "dresidual_scale", "dweight", "dbias", "dg")
+
+    def loss(a):
+        return float(np.sum(dout * oracle.lnx_pretrain_forward(*a, head_size=d)[0]))
+
+    eps = 1e-6
+    for i, name in enumerate(names):
+        base = args[i]
+        fd = np.zeros_like(base)
+        for idx in np.ndindex(base.shape):
+            plus = [a.copy() for a in args]
+            minus = [a.copy() for a in args]
+            plus[i][idx] += eps
+            minus[i][idx] -= eps
+            fd[idx] = (loss(plus) - loss(minus)) / (2 * eps)
+        np.testing.assert_allclose(grads[name], fd, rtol=1e-6, atol=1e-7, err_msg=name)
+
+
+def test_lnx_pretrain_backward_matches_torch_autograd():
+    """The same gradients from torch fp64 autograd through a restatement
+    written with torch's own layer norm (biased var, eps 64e-5): an
+    independent route to the adjoint at D = 64."""
+    rng = np.random.default_rng(13)
+    n, h, d = 5, 3, 64
+    args = _lnx_case(rng, n, h, d)
+    dout = rng.standard_normal((n, h * d))
+    ts = [torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in args]
+    x, r, k, v, rs, w, b, g = ts
+    xn = torch.nn.functional.layer_norm(x.view(n, h, d), (d,), eps=64.0e-5)
+    rkv = (r.view(n, h, d) * k.view(n, h, d) * rs.view(1, h, d)).sum(-1, keepdim=True)
+    y = (xn * w.view(1, h, d) + b.view(1, h, d) + rkv * v.view(n, h, d)) * g.view(n, h, d)
+    y.reshape(n, h * d).backward(torch.tensor(dout))
+    grads = oracle.lnx_pretrain_backward(dout, *args, head_size=d)
+    for t, name in zip(ts, ("dx", "dr", "dk", "dv", "dresidual_scale", "dweight", "dbias", "dg")):
+        np.testing.assert_allclose(grads[name], t.grad.numpy(), rtol=1e-10, atol=1e-10,
+                                   err_msg=name)
+
+
 def test_tmix_fused_is_the_rwkv7_update_with_a_minus_kk_and_b_kk_gate():
     rng = np.random.default_rng(7)
     h, d = 2, 8
