@@ -747,7 +747,13 @@ __device__ __forceinline__ int sequence_by_length_rank(const ChunkFwdParams& p, 
   return hit != 0 ? static_cast<int>(__builtin_ctzll(hit)) : rank;
 }
 
-template <typename T, DecayMode M, typename PoolT, bool kPrecise>
+// kLean: the instantiation for calls with none of the optional layouts --
+// no segment lists, boundary or interior states, every-16-token checkpoints,
+// state_dot_a, read-only or absent state (the prefill op and the recurrent
+// operator's chunk route). Those paths then compile away, and with them the
+// scalar registers their descriptors and offsets would hold across the chunk
+// loop (spilled to VGPR lanes and reloaded every chunk otherwise).
+template <typename T, DecayMode M, typename PoolT, bool kPrecise, bool kLean>
 __global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_kernel(
     ChunkFwdParams p) {
   __shared__ ChunkSmem sm;
@@ -776,9 +782,15 @@ __global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_ker
 
   // Segments: the lists of seg_offsets, or (seg_offsets null, seg_starts
   // given) exactly one segment per sequence, segment s for sequence s.
-  const bool segmented = p.seg_starts != nullptr;
+  const bool segmented = !kLean && p.seg_starts != nullptr;
+  const bool fill_only = !kLean && p.fill_only;
+  const bool boundary16 = !kLean && p.boundary16;
+  float* const boundary = kLean ? nullptr : p.boundary;
+  float* const interior = kLean ? nullptr : p.interior;
+  float* const state_dot_a = kLean ? nullptr : p.state_dot_a;
+  const bool has_state = kLean || p.state != nullptr;
   int seg_lo = 0, seg_hi = 1;
-  if (p.seg_offsets != nullptr) {
+  if (!kLean && p.seg_offsets != nullptr) {
     seg_lo = uniform(max(p.seg_offsets[seq], 0));
     seg_hi = uniform(min(p.seg_offsets[seq + 1], p.num_segments));
   } else if (segmented) {
@@ -789,7 +801,7 @@ __global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_ker
   // Interior-state fill (replay layout, one segment per unit): a segment of
   // at most one chunk has no interior state, so its unit ends before it
   // loads the start state or any token row.
-  if (p.fill_only) {
+  if (fill_only) {
     if (seg_lo >= seg_hi) return;
     const int tb = uniform(max(p.seg_starts[seg_lo], 0));
     const int te = uniform(min(p.seg_ends[seg_lo], p.total_tokens));
@@ -811,7 +823,7 @@ __global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_ker
   constexpr int kPoolBytes = static_cast<int>(sizeof(PS));
   const int64_t sbase = (static_cast<int64_t>(slot) * heads + head) * kHead * kHead;
   const auto state_rs =
-      p.state != nullptr
+      has_state
           ? buffer_rsrc(static_cast<PS*>(p.state) + sbase, kHead * kHead * kPoolBytes)
           : buffer_rsrc(static_cast<PS*>(nullptr), 0u);
   const uint32_t s_off = static_cast<uint32_t>((4 * g) * kHead + 16 * wave + n) * kPoolBytes;
@@ -822,7 +834,7 @@ __global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_ker
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int so = (16 * kb + j) * kHead * kPoolBytes;
-      if (p.state == nullptr) {
+      if (!has_state) {
         S[kb][j] = 0.0f;
       } else if constexpr (kPoolBytes == 4) {
         S[kb][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(state_rs, s_off, so, 0));
@@ -935,7 +947,7 @@ __global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_ker
     // reach no prepare (empty, or skipped by fill_only) store it here.
     auto store_boundary = [&]() {
       const auto brs = buffer_rsrc(
-          p.boundary + (static_cast<int64_t>(seg) * heads + head) * kHead * kHead,
+          boundary + (static_cast<int64_t>(seg) * heads + head) * kHead * kHead,
           kHead * kHead * 4);
       const uint32_t b_off = static_cast<uint32_t>((4 * g) * kHead + 16 * wave + n) * 4;
 #pragma unroll
@@ -947,15 +959,15 @@ __global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_ker
         }
       }
     };
-    const bool want_boundary = p.boundary != nullptr && !p.boundary16;
-    const bool defer_boundary = t_end > t_begin && !p.fill_only;
+    const bool want_boundary = boundary != nullptr && !boundary16;
+    const bool defer_boundary = t_end > t_begin && !fill_only;
     if (want_boundary && !defer_boundary) store_boundary();
-    if (p.fill_only && t_end - t_begin <= kChunk) continue;
+    if (fill_only && t_end - t_begin <= kChunk) continue;
     for (int c0 = t_begin; c0 < t_end; c0 += kChunk) {
       const int ntok = min(kChunk, t_end - c0);
-      if (p.interior != nullptr && c0 > t_begin) {
+      if (interior != nullptr && c0 > t_begin) {
         const auto irs = buffer_rsrc(
-            p.interior + (static_cast<int64_t>(c0 / kChunk) * heads + head) * kHead * kHead,
+            interior + (static_cast<int64_t>(c0 / kChunk) * heads + head) * kHead * kHead,
             kHead * kHead * 4);
         const uint32_t i_off = static_cast<uint32_t>((4 * g) * kHead + 16 * wave + n) * 4;
 #pragma unroll
@@ -967,7 +979,7 @@ __global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_ker
           }
         }
       }
-      if (p.fill_only && c0 + kChunk >= t_end) break;
+      if (fill_only && c0 + kChunk >= t_end) break;
       int nseg = seg, nc0 = c0, nend = t_end;
       const bool has_next = next_chunk(nseg, nc0, nend);
       // Every-16-tokens boundary layout [B, H, dense_t / 16, D, D]: the state
@@ -975,8 +987,8 @@ __global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_ker
       const int64_t b16_base = (static_cast<int64_t>(seq) * heads + head) * (p.dense_t / 16) +
                                (c0 - t_begin) / 16;
       auto b16_rs = [&](int i, int count) {
-        if (!p.boundary16 || count <= 0) return buffer_rsrc(static_cast<float*>(nullptr), 0u);
-        return buffer_rsrc(p.boundary + (b16_base + i / 16) * kHead * kHead,
+        if (!boundary16 || count <= 0) return buffer_rsrc(static_cast<float*>(nullptr), 0u);
+        return buffer_rsrc(boundary + (b16_base + i / 16) * kHead * kHead,
                            static_cast<uint32_t>(count) * kHead * kHead * 4);
       };
       auto store_b16 = [&](int i) {
@@ -991,7 +1003,7 @@ __global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_ker
           }
         }
       };
-      if (p.boundary16) store_b16(0);
+      if (boundary16) store_b16(0);
       // One pass over [lo, hi) per iteration. The first pass prepares the
       // whole chunk; if its decay span is above the limit (strong decay), the
       // chunk is redone as 16-token sub-chunks, or 4-token ones where a
@@ -1033,15 +1045,14 @@ __global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_ker
               p.out != nullptr ? static_cast<S16c*>(p.out) + base : nullptr,
               p.out != nullptr ? static_cast<uint32_t>(ntok) * row_bytes : 0u);
           const auto sda_rs = buffer_rsrc(
-              p.state_dot_a != nullptr ? p.state_dot_a + base : nullptr,
-              p.state_dot_a != nullptr ? 2u * static_cast<uint32_t>(ntok) * row_bytes : 0u);
-          const int nsub = (p.boundary16 && whole) ? (ntok - 1) / 16 : 0;
-          state_pass<T, kPrecise>(sm, ext, S, sm.vt, out_rs, sda_rs,
-                                  p.state_dot_a != nullptr, row_bytes, p.scale, lo, hi,
-                                  b16_rs(16, nsub), nsub);
+              state_dot_a != nullptr ? state_dot_a + base : nullptr,
+              state_dot_a != nullptr ? 2u * static_cast<uint32_t>(ntok) * row_bytes : 0u);
+          const int nsub = (boundary16 && whole) ? (ntok - 1) / 16 : 0;
+          state_pass<T, kPrecise>(sm, ext, S, sm.vt, out_rs, sda_rs, state_dot_a != nullptr,
+                                  row_bytes, p.scale, lo, hi, b16_rs(16, nsub), nsub);
         }
         if (whole) break;
-        if (p.boundary16 && hi % 16 == 0 && hi < ntok) store_b16(hi);
+        if (boundary16 && hi % 16 == 0 && hi < ntok) store_b16(hi);
         lo = hi;
         if (lo >= ntok) break;
         const int q = lo >> 4;
@@ -1054,7 +1065,7 @@ __global__ __launch_bounds__(kChunkThreads, kPrecise ? 1 : 2) void chunk_fwd_ker
     }
   }
 
-  if (p.state == nullptr || p.read_only_state) return;
+  if (!has_state || (!kLean && p.read_only_state)) return;
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
@@ -1075,8 +1086,17 @@ int launch_chunk(const ChunkFwdParams& p, int units, hipStream_t stream) {
     return set_error(FRWKV_ERR_UNSUPPORTED, "chunked kernels take at most %d heads, got %d",
                      kMaxChunkHeads, p.num_heads);
   }
-  hipLaunchKernelGGL((chunk_fwd_kernel<T, M, PoolT, kPrecise>), dim3(units),
-                     dim3(kChunkThreads), 0, stream, p);
+  const bool lean = p.seg_starts == nullptr && p.seg_offsets == nullptr &&
+                    p.boundary == nullptr && p.state_dot_a == nullptr &&
+                    p.interior == nullptr && !p.fill_only && !p.boundary16 &&
+                    !p.read_only_state && p.state != nullptr;
+  if (lean) {
+    hipLaunchKernelGGL((chunk_fwd_kernel<T, M, PoolT, kPrecise, true>), dim3(units),
+                       dim3(kChunkThreads), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((chunk_fwd_kernel<T, M, PoolT, kPrecise, false>), dim3(units),
+                       dim3(kChunkThreads), 0, stream, p);
+  }
   return check_launch("chunk_fwd_kernel");
 }
 
