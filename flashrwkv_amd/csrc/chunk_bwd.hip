@@ -63,7 +63,6 @@
 // from the state recomputed by forward steps over sub-pieces 0 .. r-1 from the
 // piece start, so the backward stays exact for any decay (at a cost quadratic
 // in the number of sub-pieces, which only such pieces pay).
-#include <mutex>
 
 #include "capi_internal.h"
 #include "chunk_common.h"
@@ -1497,83 +1496,6 @@ extern "C" int frwkv_statetune_backward(
   p.scale = scale;
   return dispatch_bwd(p, io_dtype, decay_mode, num_sequences * num_heads,
                       static_cast<hipStream_t>(stream));
-}
-
-// ------------------------------------------------- allocation-free variant ---
-//
-// frwkv_statetune_backward_noalloc runs frwkv_statetune_backward with its
-// workspace in the file-scope device array `scratch` instead of a caller
-// buffer. Each device holds its own copy of the array (FRWKV_NOALLOC_SCRATCH_BYTES)
-// from the library's first use on it until the process ends. In host code the
-// name `scratch` only stands for the symbol: its device address, per device,
-// comes from hipGetSymbolAddress on the variant's first call with that device
-// current, and only that address is handed to kernels.
-
-static __device__ __align__(256) unsigned char scratch[FRWKV_NOALLOC_SCRATCH_BYTES];
-
-namespace {
-
-constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mutex;
-void* g_scratch_address[kMaxDevices] = {};
-
-// Device address of this device's `scratch` (looked up once per device).
-int scratch_address(void** out) {
-  using namespace frwkv;
-  int device = -1;
-  hipError_t err = hipGetDevice(&device);
-  if (err != hipSuccess || device < 0 || device >= kMaxDevices) {
-    return set_error(FRWKV_ERR_HIP, "frwkv_statetune_backward_noalloc: no usable device (%s)",
-                     hipGetErrorString(err));
-  }
-  std::lock_guard<std::mutex> lock(g_scratch_mutex);
-  if (g_scratch_address[device] == nullptr) {
-    void* address = nullptr;
-    err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
-    if (err != hipSuccess || address == nullptr) {
-      return set_error(FRWKV_ERR_HIP,
-                       "frwkv_statetune_backward_noalloc: scratch address on device %d: %s",
-                       device, hipGetErrorString(err));
-    }
-    g_scratch_address[device] = address;
-  }
-  *out = g_scratch_address[device];
-  return FRWKV_OK;
-}
-
-}  // namespace
-
-extern "C" int frwkv_statetune_backward_noalloc(
-    int io_dtype, int decay_mode, int32_t num_sequences, int32_t num_heads, int32_t head_size,
-    int32_t total_tokens, int32_t num_chunks, const int32_t* sequence_chunk_offsets,
-    const int32_t* chunk_token_starts, const int32_t* chunk_token_ends, const float* boundary,
-    const float* interior, const void* r, const void* decay, const void* decay_bias,
-    const void* k, const void* v, const void* a, const void* b, const void* grad_output,
-    const float* grad_final_state, void* grad_r, void* grad_decay, void* grad_k, void* grad_v,
-    void* grad_a, void* grad_b, float* grad_initial_state, float scale, void* stream) {
-  using namespace frwkv;
-  const size_t need = frwkv_statetune_backward_workspace_bytes(head_size, num_heads,
-                                                               total_tokens, interior != nullptr);
-  if (need > FRWKV_NOALLOC_SCRATCH_BYTES) {
-    return set_error(FRWKV_ERR_INVALID_ARGUMENT,
-                     "frwkv_statetune_backward_noalloc: needs %zu bytes of scratch, the "
-                     "static buffer holds %zu (pass the forward's interior states, or fewer "
-                     "tokens or heads per call)",
-                     need, static_cast<size_t>(FRWKV_NOALLOC_SCRATCH_BYTES));
-  }
-  void* work = nullptr;
-  size_t work_bytes = 0;
-  if (need > 0) {
-    const int rc = scratch_address(&work);
-    if (rc != FRWKV_OK) return rc;
-    work_bytes = FRWKV_NOALLOC_SCRATCH_BYTES;
-  }
-  return frwkv_statetune_backward(io_dtype, decay_mode, num_sequences, num_heads, head_size,
-                                  total_tokens, num_chunks, sequence_chunk_offsets,
-                                  chunk_token_starts, chunk_token_ends, boundary, interior, r,
-                                  decay, decay_bias, k, v, a, b, grad_output, grad_final_state,
-                                  grad_r, grad_decay, grad_k, grad_v, grad_a, grad_b,
-                                  grad_initial_state, work, work_bytes, scale, stream);
 }
 
 extern "C" size_t frwkv_pretrain_backward_workspace_bytes(int32_t batch, int32_t tokens,

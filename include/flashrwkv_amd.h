@@ -302,8 +302,9 @@ size_t frwkv_statetune_backward_workspace_bytes(int32_t head_size, int32_t num_h
  * frwkv_statetune_backward without the workspace argument: the workspace
  * (frwkv_statetune_backward_workspace_bytes(head_size, H, total_tokens,
  * interior != NULL) bytes) lives in a static device array of
- * FRWKV_NOALLOC_SCRATCH_BYTES (64 MiB) that each device holds from the
- * library's first use on it until the process ends; larger needs are
+ * FRWKV_NOALLOC_SCRATCH_BYTES (64 MiB), in a code object of its own that a
+ * device loads at this entry's first call on it and holds until the process
+ * ends (a process that never calls it holds none of it); larger needs are
  * rejected with FRWKV_ERR_INVALID_ARGUMENT before anything runs. The call
  * allocates and frees nothing. Every call on one device shares that device's
  * array: calls that overlap on one device (other streams, other threads)

@@ -11,6 +11,10 @@ are recomputed into it), and head size 256 (fp32 gradient slices).
 
 from __future__ import annotations
 
+import os
+import subprocess
+import sys
+
 import numpy as np
 import pytest
 import torch
@@ -21,6 +25,7 @@ from oracle import oracle
 pytestmark = pytest.mark.gpu
 
 DEV = torch.device("cuda")
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 NAMES = ("r", "w", "k", "v", "a", "b")
 
 
@@ -102,3 +107,38 @@ def test_noalloc_backward_rejects_oversized_workspace_before_launch():
             interior=torch.zeros((n_tok // 16, heads, d, d), device=DEV))
     torch.cuda.synchronize()
     assert all(bool((g == 7.0).all()) for g in grads) and bool((ds0 == 7.0).all())
+
+
+_RESIDENCY_CHILD = """
+import sys
+import torch
+sys.path.insert(0, {repo!r})
+from flashrwkv_amd import capi
+from tests.test_zz_no_alloc import _backward, _case
+toks, meta, boundary, dy, ds = _case((300, 90), 160, 2, 64, seed=700)
+for _ in range(2):
+    _backward(capi.statetune_backward, toks, meta, boundary, dy, ds)
+torch.cuda.synchronize()
+free_before = torch.cuda.mem_get_info()[0]
+_backward(capi.statetune_backward_noalloc, toks, meta, boundary, dy, ds)
+torch.cuda.synchronize()
+free_after = torch.cuda.mem_get_info()[0]
+print("scratch-residency", free_before - free_after, flush=True)
+"""
+
+
+def test_scratch_becomes_resident_at_the_first_noalloc_call():
+    """The static scratch sits in a code object of its own, which HIP loads on
+    a device at the first use of one of its symbols: a process that runs the
+    library's other kernels holds none of it, and the first call of the
+    allocation-free entry makes it resident. Checked in a fresh process (the
+    array of this one may be loaded already) from the device's free memory."""
+    print("child process: workspace backward twice, then the noalloc entry", flush=True)
+    proc = subprocess.run([sys.executable, "-c", _RESIDENCY_CHILD.format(repo=REPO)],
+                          cwd=REPO, capture_output=True, text=True, timeout=300)
+    assert proc.returncode == 0, proc.stdout[-2000:] + proc.stderr[-2000:]
+    line = [x for x in proc.stdout.splitlines() if x.startswith("scratch-residency")][-1]
+    grown = int(line.split()[1])
+    print(f"device memory taken by the first noalloc call: {grown} bytes", flush=True)
+    assert grown >= capi.NOALLOC_SCRATCH_BYTES
+    assert grown < capi.NOALLOC_SCRATCH_BYTES + (64 << 20)
