@@ -106,6 +106,43 @@ def build_binding() -> Path:
     return OPS
 
 
+# Host-side AddressSanitizer build of the library, for the CPU tests of the C
+# ABI's host code (argument checks, workspace sizing, error reporting). The
+# sanitizer flags reach the host compilation only (each behind -Xarch_host);
+# the device code is built as usual (at -O1: it is never launched from this
+# build, which runs where there is no GPU). Loaded by a process that preloads
+# the matching runtime (asan_runtime()).
+ASAN_DIR = OBJ_DIR / "asan"
+ASAN_LIB = ASAN_DIR / "libflashrwkv_amd_asan.so"
+ASAN_HOST_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer",
+                   "-Xarch_host", "-g"]
+
+
+def asan_runtime() -> Path | None:
+    """The clang AddressSanitizer runtime that ASAN_LIB links against."""
+    found = sorted(Path("/opt/rocm/lib/llvm/lib/clang").glob(
+        "*/lib/linux/libclang_rt.asan-x86_64.so"))
+    return found[-1] if found else None
+
+
+def _compile_hip_asan(src: Path) -> Path:
+    obj = ASAN_DIR / (src.stem + ".o")
+    flags = [f for f in HIP_FLAGS if f != "-O3"]
+    _run([HIPCC, *flags, "-O1", *ASAN_HOST_FLAGS, "-c", str(src), "-o", str(obj)])
+    return obj
+
+
+def build_sanitized_library() -> Path:
+    ASAN_DIR.mkdir(parents=True, exist_ok=True)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(HIP_SOURCES))) as pool:
+        objs = list(pool.map(_compile_hip_asan, HIP_SOURCES))
+    tmp = ASAN_LIB.with_suffix(".so.tmp")
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Xarch_host", "-fsanitize=address",
+          "-shared-libasan", *map(str, objs), "-o", str(tmp)])
+    os.replace(tmp, ASAN_LIB)
+    return ASAN_LIB
+
+
 def build() -> tuple[Path, Path]:
     """Compile every native artefact (always rebuilds)."""
     return build_library(), build_binding()
@@ -114,3 +151,5 @@ def build() -> tuple[Path, Path]:
 if __name__ == "__main__":
     for path in build():
         print(path)
+    if "--asan" in sys.argv[1:]:
+        print(build_sanitized_library())

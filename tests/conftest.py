@@ -2,6 +2,7 @@
 
 from __future__ import annotations
 
+import os
 import sys
 from pathlib import Path
 
@@ -13,3 +14,10 @@ if str(ROOT) not in sys.path:
 def pytest_configure(config):
     config.addinivalue_line(
         "markers", "gpu: needs an MI355X (gfx950) GPU and the built native library")
+    # FRWKV_TEST_LIBRARY: run the C-ABI tests against another build of the
+    # library (the host-sanitized one, tests/test_capi_asan.py).
+    other = os.environ.get("FRWKV_TEST_LIBRARY")
+    if other:
+        from flashrwkv_amd import capi
+
+        capi.LIBRARY = Path(other)

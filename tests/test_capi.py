@@ -4,6 +4,7 @@ point, and argument errors are reported without touching a GPU."""
 from __future__ import annotations
 
 import ctypes
+import os
 import re
 from pathlib import Path
 
@@ -12,7 +13,8 @@ import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADERS = sorted((ROOT / "include").glob("*.h"))
-LIB_PATH = ROOT / "flashrwkv_amd" / "libflashrwkv_amd.so"
+LIB_PATH = Path(os.environ.get("FRWKV_TEST_LIBRARY")
+                or ROOT / "flashrwkv_amd" / "libflashrwkv_amd.so")
 
 DECL = re.compile(r"^[A-Za-z_][\w\s\*]*?\b(frwkv_\w+)\s*\(", re.MULTILINE)
 
