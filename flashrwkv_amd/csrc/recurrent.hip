@@ -17,9 +17,11 @@
 // MI355X design. The value columns of a state are independent given the token
 // vectors (sa[v], y[v] and S[:,v] only touch column v), so the work unit is a
 // wave owning a slab of CW columns of one (sequence, head) state:
-//   * lane l holds a 4-column group cg for RPL consecutive key rows of row
-//     group rg (NG = 64/(CW/4) row groups), i.e. RPL float4 registers; the
-//     wave's loads and stores of a state slab are 16-byte per lane;
+//   * lane l holds a group cg of NC = 4 columns (NC = 2 in the 8-column
+//     slabs that launches over few states use) for RPL consecutive key rows
+//     of row group rg (NG = 64/(CW/NC) row groups), i.e. RPL float4 (float2)
+//     registers; the wave's loads and stores of a state slab are 16-byte
+//     (8-byte) per lane;
 //   * token vectors of the lane's RPL rows are contiguous and read directly
 //     from global memory (lanes sharing rows share the cache line);
 //   * S^T a and S^T r reduce first in-lane over RPL rows, then across the
@@ -67,6 +69,69 @@ __device__ __forceinline__ float4 load_state4(const typename StateTraits<SK>::st
                        f16_to_f32(static_cast<uint16_t>(q.x >> 16)),
                        f16_to_f32(static_cast<uint16_t>(q.y & 0xffffu)),
                        f16_to_f32(static_cast<uint16_t>(q.y >> 16)));
+  }
+}
+
+// NC consecutive state columns (NC = 4 or 2) of a lane: float4 or float2.
+// The kernel names the components (x, y[, z, w]) rather than indexing a
+// vector: indexed forms changed the schedule of the four-column kernels
+// (decode included) for no gain.
+template <int NC>
+struct ColVec {
+  using type = float4;
+};
+template <>
+struct ColVec<2> {
+  using type = float2;
+};
+
+template <typename V>
+__device__ __forceinline__ V zero_cols() {
+  if constexpr (sizeof(V) == 16) return make_float4(0.f, 0.f, 0.f, 0.f);
+  else return make_float2(0.f, 0.f);
+}
+
+template <StateKind SK>
+__device__ __forceinline__ float2 load_state2(const typename StateTraits<SK>::storage* p) {
+  if constexpr (SK == StateKind::kFp32) {
+    const u32x2_t q = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+    return make_float2(__uint_as_float(q.x), __uint_as_float(q.y));
+  } else {
+    const uint32_t q = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+    return make_float2(f16_to_f32(static_cast<uint16_t>(q & 0xffffu)),
+                       f16_to_f32(static_cast<uint16_t>(q >> 16)));
+  }
+}
+
+template <StateKind SK>
+__device__ __forceinline__ void store_state2(typename StateTraits<SK>::storage* p, float2 v) {
+  if constexpr (SK == StateKind::kFp32) {
+    const u32x2_t q = {__float_as_uint(v.x), __float_as_uint(v.y)};
+    __builtin_nontemporal_store(q, reinterpret_cast<u32x2_t*>(p));
+  } else {
+    // v holds fp16 values already; the conversion is exact.
+    __builtin_nontemporal_store(pack2<F16>(v.x, v.y), reinterpret_cast<uint32_t*>(p));
+  }
+}
+
+// Two consecutive output values (16-bit io: 4 bytes; fp32: 8 bytes).
+template <typename T>
+__device__ __forceinline__ void store2(typename IoTraits<T>::storage* p, float x0, float x1) {
+  if constexpr (__is_same(T, float)) {
+    *reinterpret_cast<float2*>(p) = make_float2(x0, x1);
+  } else {
+    *reinterpret_cast<uint32_t*>(p) = pack2<T>(x0, x1);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store2_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voffset,
+                                           int soffset, float x0, float x1) {
+  if constexpr (__is_same(T, float)) {
+    const u32x2_t q = {__float_as_uint(x0), __float_as_uint(x1)};
+    __builtin_amdgcn_raw_buffer_store_b64(q, rs, voffset, soffset, 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b32(pack2<T>(x0, x1), rs, voffset, soffset, 0);
   }
 }
 
@@ -181,10 +246,12 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
   const int32_t total_tokens = p.total_tokens;
   const float scale = p.scale;
   constexpr int kWavesPerUnit = D / CW;
-  constexpr int kCg = CW / 4;       // lanes per row group (float4 columns)
-  constexpr int kNg = 64 / kCg;     // row groups per wave
-  constexpr int kRpl = D / kNg;     // key rows per lane
+  constexpr int kNc = CW == 8 ? 2 : 4;  // state columns per lane (one vector)
+  constexpr int kCg = CW / kNc;       // lanes per row group
+  constexpr int kNg = 64 / kCg;       // row groups per wave
+  constexpr int kRpl = D / kNg;       // key rows per lane
   static_assert(kRpl % 4 == 0, "lane rows load in 4-element pieces");
+  using VC = typename ColVec<kNc>::type;
 
   if (p.status != nullptr && p.status[0] != 0) {
     fill_nan<T>(out_ptr, p.output_elements);
@@ -201,7 +268,7 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
   const int rg = kLowRows ? lane % kNg : lane / kCg;
   const int cg = kLowRows ? lane / kNg : lane % kCg;
   const int row0 = rg * kRpl;
-  const int col = slab * CW + 4 * cg;
+  const int col = slab * CW + kNc * cg;
 
   // One wave handles one sequence, so its bounds and slot are wave-uniform;
   // readfirstlane makes the token loop's branches scalar.
@@ -219,10 +286,14 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
   using SS = typename StateTraits<SK>::storage;
   SS* sbase = static_cast<SS*>(p.state) +
               ((static_cast<int64_t>(slot) * num_heads + head) * D) * D;
-  float4 s[kRpl];
+  VC s[kRpl];
 #pragma unroll
   for (int j = 0; j < kRpl; ++j) {
-    s[j] = load_state4<SK>(sbase + static_cast<int64_t>(row0 + j) * D + col);
+    if constexpr (kNc == 4) {
+      s[j] = load_state4<SK>(sbase + static_cast<int64_t>(row0 + j) * D + col);
+    } else {
+      s[j] = load_state2<SK>(sbase + static_cast<int64_t>(row0 + j) * D + col);
+    }
   }
   // fp16 state: phase of key row0 at the first token.
   uint32_t phase0 = 0;
@@ -248,7 +319,7 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
   // so its register count must stay low.
   struct TokenRows {
     RawRow<T, kRpl> a, w, b, k, r;
-    RawRow<T, 4> v;
+    RawRow<T, kNc> v;
   };
   // kBuf (prefetching shapes, tensors under 2 GiB): buffer loads whose
   // per-lane offset is fixed and whose token offset is one scalar, so a
@@ -279,7 +350,7 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
       load_raw_buf<T, kRpl>(rs_b, vo_rows, so, dst.b);
       load_raw_buf<T, kRpl>(rs_k, vo_rows, so, dst.k);
       load_raw_buf<T, kRpl>(rs_r, vo_rows, so, dst.r);
-      load_raw_buf<T, 4>(rs_v, vo_cols, so, dst.v);
+      load_raw_buf<T, kNc>(rs_v, vo_cols, so, dst.v);
     } else {
       const int64_t base = (static_cast<int64_t>(t) * num_heads + head) * D;
       load_raw<T, kRpl>(a_ptr + base + row0, dst.a);
@@ -287,11 +358,11 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
       load_raw<T, kRpl>(b_ptr + base + row0, dst.b);
       load_raw<T, kRpl>(k_ptr + base + row0, dst.k);
       load_raw<T, kRpl>(r_ptr + base + row0, dst.r);
-      load_raw<T, 4>(v_ptr + base + col, dst.v);
+      load_raw<T, kNc>(v_ptr + base + col, dst.v);
     }
   };
   // About 96 registers of ring; the one-wave decode shape loads in place.
-  constexpr int kTokenWords = 5 * RawRow<T, kRpl>::kWords + RawRow<T, 4>::kWords;
+  constexpr int kTokenWords = 5 * RawRow<T, kRpl>::kWords + RawRow<T, kNc>::kWords;
   constexpr int kRing = 96 / kTokenWords < 1 ? 1 : (96 / kTokenWords > 8 ? 8 : 96 / kTokenWords);
   constexpr int kPrefetch = (CW == 64) ? 1 : kRing;
   TokenRows ring[kPrefetch];
@@ -308,37 +379,41 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
       const int32_t t = t0 + jp;
       if (t >= t_end) break;
       if constexpr (kPrefetch == 1) load_token(ring[0], t);
-      float rr[kRpl], ww[kRpl], kk[kRpl], aa[kRpl], bb[kRpl], vv[4];
+      float rr[kRpl], ww[kRpl], kk[kRpl], aa[kRpl], bb[kRpl], vv[kNc];
       decode_raw<T, kRpl>(ring[jp].a, aa);
       decode_raw<T, kRpl>(ring[jp].w, ww);
       decode_raw<T, kRpl>(ring[jp].b, bb);
       decode_raw<T, kRpl>(ring[jp].k, kk);
       decode_raw<T, kRpl>(ring[jp].r, rr);
-      decode_raw<T, 4>(ring[jp].v, vv);
+      decode_raw<T, kNc>(ring[jp].v, vv);
       if constexpr (kPrefetch > 1) {
         // Unconditional (the last token again past the end): a skipped load
         // would make the ring registers a join of two paths, copied per token.
         load_token(ring[jp], min(t + kPrefetch, t_end - 1));
       }
 
-      float4 sa = make_float4(0.f, 0.f, 0.f, 0.f);
+      VC sa = zero_cols<VC>();
 #pragma unroll
       for (int j = 0; j < kRpl; ++j) {
         sa.x = fmaf(aa[j], s[j].x, sa.x);
         sa.y = fmaf(aa[j], s[j].y, sa.y);
-        sa.z = fmaf(aa[j], s[j].z, sa.z);
-        sa.w = fmaf(aa[j], s[j].w, sa.w);
+        if constexpr (kNc == 4) {
+          sa.z = fmaf(aa[j], s[j].z, sa.z);
+          sa.w = fmaf(aa[j], s[j].w, sa.w);
+        }
       }
       sa.x = sum_row_groups<kNg, kLowRows>(sa.x);
       sa.y = sum_row_groups<kNg, kLowRows>(sa.y);
-      sa.z = sum_row_groups<kNg, kLowRows>(sa.z);
-      sa.w = sum_row_groups<kNg, kLowRows>(sa.w);
+      if constexpr (kNc == 4) {
+        sa.z = sum_row_groups<kNg, kLowRows>(sa.z);
+        sa.w = sum_row_groups<kNg, kLowRows>(sa.w);
+      }
       if (p.state_dot_a != nullptr && rg == 0) {
-        *reinterpret_cast<float4*>(
+        *reinterpret_cast<VC*>(
             p.state_dot_a + (static_cast<int64_t>(t) * num_heads + head) * D + col) = sa;
       }
 
-      float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+      VC y = zero_cols<VC>();
 #pragma unroll
       for (int j = 0; j < kRpl; ++j) {
         // (The raw-retention prefetch path skips the zero bias; the decode
@@ -349,33 +424,52 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
         if constexpr (SK == StateKind::kFp32) {
           s[j].x = fmaf(w, s[j].x, fmaf(bb[j], sa.x, kk[j] * vv[0]));
           s[j].y = fmaf(w, s[j].y, fmaf(bb[j], sa.y, kk[j] * vv[1]));
-          s[j].z = fmaf(w, s[j].z, fmaf(bb[j], sa.z, kk[j] * vv[2]));
-          s[j].w = fmaf(w, s[j].w, fmaf(bb[j], sa.w, kk[j] * vv[3]));
+          if constexpr (kNc == 4) {
+            s[j].z = fmaf(w, s[j].z, fmaf(bb[j], sa.z, kk[j] * vv[2]));
+            s[j].w = fmaf(w, s[j].w, fmaf(bb[j], sa.w, kk[j] * vv[3]));
+          }
         } else {
           const uint32_t phase = phase0 + static_cast<uint32_t>(j + t);
           const float delta = round_f16(w - 1.0f + phase_dither(phase));
           s[j].x = round_f16(fmaf(kk[j], vv[0], fmaf(bb[j], sa.x, fmaf(s[j].x, delta, s[j].x))));
           s[j].y = round_f16(fmaf(kk[j], vv[1], fmaf(bb[j], sa.y, fmaf(s[j].y, delta, s[j].y))));
-          s[j].z = round_f16(fmaf(kk[j], vv[2], fmaf(bb[j], sa.z, fmaf(s[j].z, delta, s[j].z))));
-          s[j].w = round_f16(fmaf(kk[j], vv[3], fmaf(bb[j], sa.w, fmaf(s[j].w, delta, s[j].w))));
+          if constexpr (kNc == 4) {
+            s[j].z =
+                round_f16(fmaf(kk[j], vv[2], fmaf(bb[j], sa.z, fmaf(s[j].z, delta, s[j].z))));
+            s[j].w =
+                round_f16(fmaf(kk[j], vv[3], fmaf(bb[j], sa.w, fmaf(s[j].w, delta, s[j].w))));
+          }
         }
         y.x = fmaf(rr[j], s[j].x, y.x);
         y.y = fmaf(rr[j], s[j].y, y.y);
-        y.z = fmaf(rr[j], s[j].z, y.z);
-        y.w = fmaf(rr[j], s[j].w, y.w);
+        if constexpr (kNc == 4) {
+          y.z = fmaf(rr[j], s[j].z, y.z);
+          y.w = fmaf(rr[j], s[j].w, y.w);
+        }
       }
       y.x = sum_row_groups<kNg, kLowRows>(y.x);
       y.y = sum_row_groups<kNg, kLowRows>(y.y);
-      y.z = sum_row_groups<kNg, kLowRows>(y.z);
-      y.w = sum_row_groups<kNg, kLowRows>(y.w);
+      if constexpr (kNc == 4) {
+        y.z = sum_row_groups<kNg, kLowRows>(y.z);
+        y.w = sum_row_groups<kNg, kLowRows>(y.w);
+      }
       if (rg == 0) {
         if constexpr (kBuf) {
-          store4_buf<T>(rs_out, vo_cols, static_cast<int>(static_cast<uint32_t>(t) * token_bytes),
-                        scale * y.x, scale * y.y, scale * y.z, scale * y.w);
+          const int so = static_cast<int>(static_cast<uint32_t>(t) * token_bytes);
+          if constexpr (kNc == 4) {
+            store4_buf<T>(rs_out, vo_cols, so, scale * y.x, scale * y.y, scale * y.z,
+                          scale * y.w);
+          } else {
+            store2_buf<T>(rs_out, vo_cols, so, scale * y.x, scale * y.y);
+          }
         } else {
           const int64_t base = (static_cast<int64_t>(t) * num_heads + head) * D;
-          store4<T>(out_ptr + base + col, scale * y.x, scale * y.y, scale * y.z,
-                    scale * y.w);
+          if constexpr (kNc == 4) {
+            store4<T>(out_ptr + base + col, scale * y.x, scale * y.y, scale * y.z,
+                      scale * y.w);
+          } else {
+            store2<T>(out_ptr + base + col, scale * y.x, scale * y.y);
+          }
         }
       }
     }
@@ -384,7 +478,11 @@ __global__ __launch_bounds__(WG) void recurrent_fp32_kernel(
   if (p.read_only_state) return;
 #pragma unroll
   for (int j = 0; j < kRpl; ++j) {
-    store_state4<SK>(sbase + static_cast<int64_t>(row0 + j) * D + col, s[j]);
+    if constexpr (kNc == 4) {
+      store_state4<SK>(sbase + static_cast<int64_t>(row0 + j) * D + col, s[j]);
+    } else {
+      store_state2<SK>(sbase + static_cast<int64_t>(row0 + j) * D + col, s[j]);
+    }
   }
 }
 
@@ -623,6 +721,9 @@ int launch_fp16_decode(const RecurrentArgs& p) {
   return check_launch("recurrent_fp16_decode_kernel");
 }
 
+// SIMDs of an MI355X (256 CUs x 4), the gfx950 part this library is built for.
+constexpr int64_t kSimdCount = 1024;
+
 // Smallest max_seqlen that the recurrent operator routes to the chunk kernel.
 constexpr int32_t kChunkedMinSeqlen = 64;
 
@@ -642,6 +743,15 @@ int dispatch_head_size(const RecurrentArgs& p) {
       if (p.max_seqlen > 0 && p.max_seqlen <= 2) {
         if constexpr (SK == StateKind::kFp16) return launch_fp16_decode(p);
         return launch_recurrent<64, 64, 64, T, M, SK>(p);
+      }
+      // Few states: 8-column slabs (8 waves per state), so that the launch
+      // fills more SIMDs and each wave's token step is half as long. Beyond
+      // one wave per SIMD the 16-column slabs' fewer redundant decay and
+      // token-row evaluations win (same-box, B x H = 32 .. 128: 23-24%
+      // faster; 256: 2.5% slower).
+      if (static_cast<int64_t>(p.num_sequences) * p.num_heads * 8 <= kSimdCount) {
+        if (buffer_addressable<64, T>(p)) return launch_recurrent<64, 8, 256, T, M, SK, true>(p);
+        return launch_recurrent<64, 8, 256, T, M, SK>(p);
       }
       if (buffer_addressable<64, T>(p)) return launch_recurrent<64, 16, 256, T, M, SK, true>(p);
       return launch_recurrent<64, 16, 256, T, M, SK>(p);

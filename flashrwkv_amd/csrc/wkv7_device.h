@@ -162,13 +162,13 @@ __device__ __forceinline__ void load_vec(const typename IoTraits<T>::storage* p,
   }
 }
 
-// Raw (undecoded) storage of N contiguous elements, loaded with 8- or
-// 16-byte vector loads. Decoding is split from loading so that a kernel can
-// issue the loads of later tokens long before it decodes them.
+// Raw (undecoded) storage of N contiguous elements, loaded with 16-, 8- or
+// (two 16-bit elements) 4-byte loads. Decoding is split from loading so that
+// a kernel can issue the loads of later tokens long before it decodes them.
 template <typename T, int N>
 struct RawRow {
   static constexpr int kWords = N * IoTraits<T>::kBytes / 4;
-  static_assert(kWords % 2 == 0, "rows load in 8-byte pieces");
+  static_assert(kWords % 2 == 0 || kWords == 1, "rows load in 4-, 8- or 16-byte pieces");
   uint32_t w[kWords];
 };
 
@@ -176,7 +176,9 @@ template <typename T, int N>
 __device__ __forceinline__ void load_raw(const typename IoTraits<T>::storage* p,
                                          RawRow<T, N>& out) {
   constexpr int kWords = RawRow<T, N>::kWords;
-  if constexpr (kWords % 4 == 0) {
+  if constexpr (kWords == 1) {
+    out.w[0] = *reinterpret_cast<const uint32_t*>(p);
+  } else if constexpr (kWords % 4 == 0) {
 #pragma unroll
     for (int i = 0; i < kWords / 4; ++i) {
       const uint4 q = reinterpret_cast<const uint4*>(p)[i];
@@ -201,7 +203,9 @@ template <typename T, int N>
 __device__ __forceinline__ void load_raw_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voffset,
                                              int soffset, RawRow<T, N>& out) {
   constexpr int kWords = RawRow<T, N>::kWords;
-  if constexpr (kWords % 4 == 0) {
+  if constexpr (kWords == 1) {
+    out.w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, voffset, soffset, 0);
+  } else if constexpr (kWords % 4 == 0) {
 #pragma unroll
     for (int i = 0; i < kWords / 4; ++i) {
       typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));

@@ -272,6 +272,46 @@ def test_config2_per_token_kernel_subset_of_batch():
     _check("state", _np(dev["state_pool"]), pool_ref, 1e-3)
 
 
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float32))
+def test_narrow_slabs_of_small_launches_match_wide_slabs_bitwise(dtype):
+    """Launches over at most 128 (sequence, head) states split each state into
+    8-column slabs, larger ones into 16-column slabs. Both sum every column's
+    keys in the same order, so the same sequences give the same bits either
+    way: two sequences alone (64 states) against the same two followed by
+    three more (160 states), per-token kernel, then against the oracle."""
+    from flashrwkv_amd import capi
+
+    heads, lengths = 32, [300, 77, 5, 120, 9]
+    print(f"case narrow vs wide slabs {dtype} H={heads} lengths {lengths}", flush=True)
+    case = _baseline_case(lengths, heads, dtype, seed=20260810, state_std=0.1)
+    n_small = sum(lengths[:2])
+
+    def run(n_seq):
+        n_tok = sum(lengths[:n_seq])
+        toks = [case[n][:n_tok].to(DEV) for n in ("r", "w", "k", "v", "a", "b")]
+        pool = case["state_pool"][:n_seq].clone().to(DEV)
+        cu = case["cu_seqlens"][: n_seq + 1].to(DEV)
+        slots = torch.arange(n_seq, dtype=torch.int32, device=DEV)
+        y = torch.empty_like(toks[3])
+        status = torch.zeros(1, dtype=torch.int32, device=DEV)
+        capi.recurrent_forward(*toks, state_pool=pool, cu_seqlens=cu, state_indices=slots,
+                               metadata_status=status, output=y, max_seqlen=-1)
+        torch.cuda.synchronize()
+        return y, pool
+
+    y_narrow, pool_narrow = run(2)
+    y_wide, pool_wide = run(len(lengths))
+    assert torch.equal(y_narrow, y_wide[:n_small])
+    assert torch.equal(pool_narrow, pool_wide[:2])
+    sub = {k: case[k] for k in ("r", "w", "k", "v", "a", "b")}
+    y_ref, pool_ref = oracle.forward_varlen(
+        *(_np(sub[n][:n_small]) for n in ("r", "w", "k", "v", "a", "b")),
+        _np(case["state_pool"][:2]), case["cu_seqlens"][:3].numpy(),
+        np.arange(2, dtype=np.int32), 1.0)
+    _check("y", _np(y_narrow), y_ref, TOL_Y[dtype])
+    _check("state", _np(pool_narrow), pool_ref, 1e-5 if dtype == torch.float32 else 1e-3)
+
+
 def test_config2_full_shape_sampled_heads():
     """Config 2 at its full shape (B=8, T=4096, H=32, bf16 tokens, S0 = 0)
     through the operator, which runs it on the split-precision chunk kernel:
