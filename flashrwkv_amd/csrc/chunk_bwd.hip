@@ -1123,7 +1123,10 @@ __device__ void run_backward_step(BwdSmem& sm, const ChunkBwdParams& p, const To
   __builtin_amdgcn_raw_buffer_store_b128(pack8<T>(dw), rsrc(args().ddecay), st_off, 0, 0);
 }
 
-template <typename T, DecayMode M>
+// kDense: the pretraining layout (dense_t > 0), a separate instantiation so
+// that the StateTune path's piece walk carries no dense-layout branches (18
+// fewer SGPRs spilled to VGPR lanes; 2% faster at config 4, same bits).
+template <typename T, DecayMode M, bool kDense>
 __global__ __launch_bounds__(kBwdThreads, 1) void chunk_bwd_kernel(ChunkBwdParams p) {
   __shared__ BwdSmem sm;
 
@@ -1138,7 +1141,7 @@ __global__ __launch_bounds__(kBwdThreads, 1) void chunk_bwd_kernel(ChunkBwdParam
   const int seq = blockIdx.x / heads;
   const int head = blockIdx.x % heads;
   const int f0 = 32 * hf + 8 * g;
-  const bool dense = p.dense_t > 0;
+  constexpr bool dense = kDense;
   const int seg_lo = dense ? 0 : uniform(max(p.seg_offsets[seq], 0));
   const int seg_hi = dense ? 1 : uniform(min(p.seg_offsets[seq + 1], p.num_segments));
 
@@ -1365,7 +1368,13 @@ int launch_bwd(const ChunkBwdParams& p, int units, hipStream_t stream) {
     return set_error(FRWKV_ERR_UNSUPPORTED, "chunked kernels take at most %d heads, got %d",
                      kMaxChunkHeads, p.num_heads);
   }
-  hipLaunchKernelGGL((chunk_bwd_kernel<T, M>), dim3(units), dim3(kBwdThreads), 0, stream, p);
+  if (p.dense_t > 0) {
+    hipLaunchKernelGGL((chunk_bwd_kernel<T, M, true>), dim3(units), dim3(kBwdThreads), 0,
+                       stream, p);
+  } else {
+    hipLaunchKernelGGL((chunk_bwd_kernel<T, M, false>), dim3(units), dim3(kBwdThreads), 0,
+                       stream, p);
+  }
   return check_launch("chunk_bwd_kernel");
 }
 
