@@ -1,0 +1,107 @@
+// Parameters and chunk walking shared by the head-size-128/256 training
+// kernels: the per-token kernels (train_recurrent.hip) and the head-size-128
+// MFMA backward over 16-token pieces (piece_bwd.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace frwkv {
+
+constexpr int kPiece = 16;  // tokens per piece; the interior checkpoint spacing
+
+struct TrainParams {
+  int32_t num_heads;
+  int32_t total_tokens;
+  int32_t num_sequences;
+  // Segmented chunks (StateTune): chunk c of sequence s, c in
+  // [seg_offsets[s], seg_offsets[s+1]), covers tokens seg_starts[c] ..
+  // seg_ends[c]-1; its start state is ckpt[c, h].
+  const int32_t* seg_offsets;
+  const int32_t* seg_starts;
+  const int32_t* seg_ends;
+  int32_t num_chunks;  // length of seg_starts / seg_ends
+  // Dense (pretraining): > 0 means sequence s holds tokens s*T .. s*T+T-1 in
+  // chunks of 16; chunk j's start state is ckpt[s, h, j] ([B,H,T/16,D,D]).
+  int32_t dense_t;
+  float* state;        // [B,H,D,D] S0 in, S_T out (forward); null: zero start, no S_T
+  float* ckpt;         // chunk start states
+  float* state_dot_a;  // [N,H,D] a^T S_{t-1} (forward output)
+  const void* r;
+  const void* decay;
+  const void* bias;    // [H*D] or null (logits mode only)
+  const void* k;
+  const void* v;
+  const void* a;
+  const void* b;
+  void* out;           // y (forward)
+  const void* dy;             // or null (zero)
+  const float* dstate_final;  // or null (zero)
+  void* dr;
+  void* ddecay;
+  void* dk;
+  void* dv;
+  void* da;
+  void* db;
+  float* dstate0;  // or null
+  float* accum;    // [groups, 5, N*H*D] fp32 slices (dr, dk, db, ddecay, da), groups > 1
+  float scale;
+  // [ceil(N/16), H, D, D] or null: the state at every 16-token piece start
+  // inside a chunk (not at the chunk start), at slot (piece start) / 16;
+  // interior starts of different chunks lie more than 16 tokens apart, so the
+  // slots are distinct. Written by the forward, read by the backward.
+  float* interior;
+  // Forward only: 1 = one chunk per unit (seg_offsets null; chunk c starts from
+  // state[c]), only the interior states are written; chunks of at most 16
+  // tokens are skipped and a chunk's last piece is not computed.
+  int32_t fill_only;
+};
+
+struct Chunk {
+  int32_t start, end;
+  int64_t ckpt_off;  // element offset of the chunk start state
+};
+
+__device__ __forceinline__ void chunk_range(const TrainParams& p, int seq, int& c_begin,
+                                            int& c_end) {
+  if (p.dense_t > 0) {
+    c_begin = 0;
+    c_end = p.dense_t / kPiece;
+  } else if (p.seg_offsets == nullptr) {
+    c_begin = seq;
+    c_end = min(seq + 1, p.num_chunks);
+  } else {
+    // Clamped to the chunk arrays, so malformed offsets cannot address
+    // outside them.
+    c_begin = __builtin_amdgcn_readfirstlane(max(p.seg_offsets[seq], 0));
+    c_end = __builtin_amdgcn_readfirstlane(min(p.seg_offsets[seq + 1], p.num_chunks));
+  }
+}
+
+template <int D>
+__device__ __forceinline__ Chunk chunk_at(const TrainParams& p, int seq, int head, int c) {
+  Chunk ch;
+  if (p.dense_t > 0) {
+    ch.start = seq * p.dense_t + kPiece * c;
+    ch.end = ch.start + kPiece;
+    ch.ckpt_off = ((static_cast<int64_t>(seq) * p.num_heads + head) * (p.dense_t / kPiece) + c) *
+                  static_cast<int64_t>(D) * D;
+  } else {
+    ch.start = __builtin_amdgcn_readfirstlane(p.seg_starts[c]);
+    ch.end = __builtin_amdgcn_readfirstlane(p.seg_ends[c]);
+    ch.ckpt_off = (static_cast<int64_t>(c) * p.num_heads + head) * static_cast<int64_t>(D) * D;
+  }
+  return ch;
+}
+
+__device__ __forceinline__ bool chunk_ok(const Chunk& ch, int32_t total_tokens) {
+  return ch.start >= 0 && ch.end >= ch.start && ch.end <= total_tokens;
+}
+
+// The head-size-128 backward on bf16 MFMA (piece_bwd.hip), for the
+// per-token forward's checkpoints. Same parameters and outputs as the
+// per-token backward at head size 128 (one workgroup per (sequence, head)).
+int launch_piece_backward(const TrainParams& p, int io_dtype, int decay_mode, int units,
+                          hipStream_t stream);
+
+}  // namespace frwkv

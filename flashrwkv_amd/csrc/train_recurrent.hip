@@ -42,6 +42,7 @@
 // the same lane layout per head size, the same fma forms and the same
 // reduction order.
 #include "capi_internal.h"
+#include "train_common.h"
 #include "wkv7_device.h"
 
 #include <algorithm>
@@ -49,13 +50,23 @@
 namespace frwkv {
 namespace {
 
-constexpr int kPiece = 16;  // tokens per LDS piece; the backward's chunk limit
-
 // Columns per wave and waves per workgroup for each head size. The two fp32
 // state slabs (state and adjoint) of a lane take 2 * D * CW / 64 registers.
 template <int D> struct TrainShape;
 template <> struct TrainShape<128> { static constexpr int kCW = 16, kNW = 8; };
 template <> struct TrainShape<256> { static constexpr int kCW = 8, kNW = 8; };
+
+// The retention of the training kernels: raw retention clamped to
+// [2^-20, 1], as the chunked MFMA kernels (head size 64 and the head-size-128
+// backward) take it, so every head size trains on the same function.
+template <DecayMode M>
+__device__ __forceinline__ float train_retention(float x) {
+  if constexpr (M == DecayMode::kLogits) {
+    return decay_retention<M>(x);
+  } else {
+    return __builtin_amdgcn_fmed3f(x, 0x1p-20f, 1.0f);
+  }
+}
 
 template <int D>
 struct Layout {
@@ -70,93 +81,6 @@ struct Layout {
   static_assert(kRpl % 4 == 0 && kGroups * kCols == D, "layout");
 };
 
-struct TrainParams {
-  int32_t num_heads;
-  int32_t total_tokens;
-  int32_t num_sequences;
-  // Segmented chunks (StateTune): chunk c of sequence s, c in
-  // [seg_offsets[s], seg_offsets[s+1]), covers tokens seg_starts[c] ..
-  // seg_ends[c]-1; its start state is ckpt[c, h].
-  const int32_t* seg_offsets;
-  const int32_t* seg_starts;
-  const int32_t* seg_ends;
-  int32_t num_chunks;  // length of seg_starts / seg_ends
-  // Dense (pretraining): > 0 means sequence s holds tokens s*T .. s*T+T-1 in
-  // chunks of 16; chunk j's start state is ckpt[s, h, j] ([B,H,T/16,D,D]).
-  int32_t dense_t;
-  float* state;        // [B,H,D,D] S0 in, S_T out (forward); null: zero start, no S_T
-  float* ckpt;         // chunk start states
-  float* state_dot_a;  // [N,H,D] a^T S_{t-1} (forward output)
-  const void* r;
-  const void* decay;
-  const void* bias;    // [H*D] or null (logits mode only)
-  const void* k;
-  const void* v;
-  const void* a;
-  const void* b;
-  void* out;           // y (forward)
-  const void* dy;             // or null (zero)
-  const float* dstate_final;  // or null (zero)
-  void* dr;
-  void* ddecay;
-  void* dk;
-  void* dv;
-  void* da;
-  void* db;
-  float* dstate0;  // or null
-  float* accum;    // [groups, 5, N*H*D] fp32 slices (dr, dk, db, ddecay, da), groups > 1
-  float scale;
-  // [ceil(N/16), H, D, D] or null: the state at every 16-token piece start
-  // inside a chunk (not at the chunk start), at slot (piece start) / 16;
-  // interior starts of different chunks lie more than 16 tokens apart, so the
-  // slots are distinct. Written by the forward, read by the backward.
-  float* interior;
-  // Forward only: 1 = one chunk per unit (seg_offsets null; chunk c starts from
-  // state[c]), only the interior states are written; chunks of at most 16
-  // tokens are skipped and a chunk's last piece is not computed.
-  int32_t fill_only;
-};
-
-struct Chunk {
-  int32_t start, end;
-  int64_t ckpt_off;  // element offset of the chunk start state
-};
-
-__device__ __forceinline__ void chunk_range(const TrainParams& p, int seq, int& c_begin,
-                                            int& c_end) {
-  if (p.dense_t > 0) {
-    c_begin = 0;
-    c_end = p.dense_t / kPiece;
-  } else if (p.seg_offsets == nullptr) {
-    c_begin = seq;
-    c_end = min(seq + 1, p.num_chunks);
-  } else {
-    // Clamped to the chunk arrays, so malformed offsets cannot address
-    // outside them.
-    c_begin = __builtin_amdgcn_readfirstlane(max(p.seg_offsets[seq], 0));
-    c_end = __builtin_amdgcn_readfirstlane(min(p.seg_offsets[seq + 1], p.num_chunks));
-  }
-}
-
-template <int D>
-__device__ __forceinline__ Chunk chunk_at(const TrainParams& p, int seq, int head, int c) {
-  Chunk ch;
-  if (p.dense_t > 0) {
-    ch.start = seq * p.dense_t + kPiece * c;
-    ch.end = ch.start + kPiece;
-    ch.ckpt_off = ((static_cast<int64_t>(seq) * p.num_heads + head) * (p.dense_t / kPiece) + c) *
-                  static_cast<int64_t>(D) * D;
-  } else {
-    ch.start = __builtin_amdgcn_readfirstlane(p.seg_starts[c]);
-    ch.end = __builtin_amdgcn_readfirstlane(p.seg_ends[c]);
-    ch.ckpt_off = (static_cast<int64_t>(c) * p.num_heads + head) * static_cast<int64_t>(D) * D;
-  }
-  return ch;
-}
-
-__device__ __forceinline__ bool chunk_ok(const Chunk& ch, int32_t total_tokens) {
-  return ch.start >= 0 && ch.end >= ch.start && ch.end <= total_tokens;
-}
 
 template <int kCtrl>
 __device__ __forceinline__ float dpp(float x) {
@@ -377,8 +301,8 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_fwd_kernel(TrainPar
         float x[4];
         decode4<T>(g.x[u], x);
         *reinterpret_cast<float4*>(&s.w[i][e]) = make_float4(
-            decay_retention<M>(x[0] + bias4[u][0]), decay_retention<M>(x[1] + bias4[u][1]),
-            decay_retention<M>(x[2] + bias4[u][2]), decay_retention<M>(x[3] + bias4[u][3]));
+            train_retention<M>(x[0] + bias4[u][0]), train_retention<M>(x[1] + bias4[u][1]),
+            train_retention<M>(x[2] + bias4[u][2]), train_retention<M>(x[3] + bias4[u][3]));
       }
     }
     const int i = Sg::col_tok(tid);
@@ -626,13 +550,15 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_bwd_kernel(TrainPar
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const float xb = x[j] + bias4[u][j];
-          w4[j] = decay_retention<M>(xb);
+          w4[j] = train_retention<M>(xb);
           if constexpr (M == DecayMode::kLogits) {
             // dw/dx = w * (-e^{-1/2}) sigmoid(x) (1 - sigmoid(x))
             const float sig = 1.0f / (1.0f + exp2f(-kLog2E * xb));
             f4[j] = w4[j] * (-kExpNegHalf) * sig * (1.0f - sig);
           } else {
-            f4[j] = 1.0f;
+            // Raw retention is clamped to [2^-20, 1], with zero derivative
+            // outside (as torch.clamp).
+            f4[j] = (xb >= 0x1p-20f && xb <= 1.0f) ? 1.0f : 0.0f;
           }
         }
         *reinterpret_cast<float4*>(&sm.w[i][e]) = make_float4(w4[0], w4[1], w4[2], w4[3]);
@@ -1020,6 +946,9 @@ int frwkv_train_recurrent_backward(int io_dtype, int decay_mode, int32_t num_seq
                        head_size);
     }
     p.accum = slices;
+  }
+  if (head_size == 128) {
+    return launch_piece_backward(p, io_dtype, decay_mode, num_sequences * num_heads, s);
   }
   const int rc = dispatch_train_io(p, io_dtype, decay_mode, head_size,
                                    num_sequences * num_heads, /*backward=*/true, s);

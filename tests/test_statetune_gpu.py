@@ -134,19 +134,23 @@ def _strong_decay(case, seed):
     case["w"] = w.to(case["r"].dtype)
 
 
+@pytest.mark.parametrize("head_size", (64, 128, 256))
 @pytest.mark.parametrize("recipe", ("cfg3", "w1e-3_1e-9"))
 @pytest.mark.parametrize("lengths,chunk", [((130, 64, 33), 64), ((200, 50), 100)])
-def test_strong_decay_backward_sub_pieces(recipe, lengths, chunk):
-    """Decay spans beyond the single-reference limit: the backward runs such
-    pieces as 16- and 4-token sub-pieces recomputed from the piece start.
-    Recipes: benchmark config 3's decay (w = exp(-exp(u)), u ~ U(-8, 0)) and
-    retention 1e-3 / 1e-9. Raw retention is clamped to [2^-20, 1] (log2 w
-    to [-20, 0]) with zero derivative outside, as torch.clamp: the expected
+def test_strong_decay_backward_sub_pieces(head_size, recipe, lengths, chunk):
+    """Decay spans beyond the single-reference limit: the head-size-64
+    backward runs such pieces as 16- and 4-token sub-pieces recomputed from
+    the piece start, the head-size-128 one (16-token pieces) as 4-token
+    sub-pieces; head size 256 runs per token. Recipes: benchmark config 3's
+    decay (w = exp(-exp(u)), u ~ U(-8, 0)) and retention 1e-3 / 1e-9. Raw
+    retention is clamped to [2^-20, 1] (log2 w to [-20, 0]) with zero
+    derivative outside, as torch.clamp, at every head size: the expected
     values are the oracle's at the clamped retention, with the decay gradient
     zero where the input lies below the floor."""
     meta = oracle.chunk_metadata(lengths, chunk)
-    case = workloads.make_case(lengths=lengths, heads=2, head_size=64, dtype=torch.bfloat16,
-                               seed=400 + chunk, state_std=0.1, u_low=-8.0)
+    case = workloads.make_case(lengths=lengths, heads=2, head_size=head_size,
+                               dtype=torch.bfloat16, seed=400 + chunk, state_std=0.1,
+                               u_low=-8.0)
     if recipe != "cfg3":
         _strong_decay(case, seed=chunk)
     out, grads, dy, ds = _run(case, meta, scale=0.5)
