@@ -961,8 +961,8 @@ def cpu_baseline_training(t_len, heads_total, seconds):
 
 
 def bench_training_large(args):
-    """StateTune at head sizes 128 and 256 (the per-token fp32 training
-    kernels): B=8, T=4096, C=H*D=4096, bf16 io, raw retention, S0 ~ N(0, 0.1),
+    """StateTune at head sizes 128 (bf16 MFMA over 16-token pieces) and 256
+    (the per-token fp32 training kernels): B=8, T=4096, C=H*D=4096, bf16 io, raw retention, S0 ~ N(0, 0.1),
     dY ~ N(0, 1), dS_T ~ N(0, 0.01), caller chunks of 64 tokens (split into
     16-token kernel chunks by the wrapper). One step = autograd forward +
     backward. No benchmark config uses these head sizes; this leg records their

@@ -145,7 +145,8 @@ __device__ __forceinline__ float rowsum16(float x) {
 // the derivative of the decay input's gradient with respect to dlg.
 struct PieceRows {
   float fg[4], fgp[4], fgn[4], dwf[4];
-  bool on;  // token n is inside the pass's range
+  bool on;     // token n is inside the pass's range
+  int lo, hi;  // the pass's range (wave-uniform)
 };
 
 // One (sub-)piece pass over tokens [lo, hi) of the piece at token t0 with
@@ -176,6 +177,8 @@ __device__ __forceinline__ void piece_prepare(PieceSmem& sm, PieceRows& rows,
   const uint2 vq = load(p.v);
   const uint2 yq = load(p.dy);
   rows.on = n >= lo && n < hi;
+  rows.lo = lo;
+  rows.hi = hi;
 
   float x[4];
   unpack4<T>(xq, x);
@@ -325,8 +328,16 @@ __device__ __forceinline__ i16x8 lo32(i16x4 x) {
 }
 
 // A forward pass of the prepared (sub-)piece on the wave's slab:
-// S <- diag(g) (S + Bh^T SA + Kh^T V). Ends with a barrier.
-__device__ __forceinline__ void piece_forward_state(PieceSmem& sm, Slab& S) {
+// S <- diag(g) (S + Bh^T SA + Kh^T V). kOut: also the outputs of its tokens
+// (those inside the pass's range; the others store to kDropOffset):
+// y = scale (Rt S0 + Arb SA + Ark V) and state_dot_a = SA, for the wave's
+// value columns, when p.out is set. Ends with a barrier.
+template <typename T, bool kOut>
+__device__ __forceinline__ void piece_forward_state(PieceSmem& sm, Slab& S,
+                                                    const PieceRows& rows,
+                                                    const TrainParams& p, int head, int32_t t0,
+                                                    int ntok) {
+  using St = typename IoTraits<T>::storage;
   const int tid = lane_tid();
   const int w = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, n = lane & 15;
@@ -343,7 +354,41 @@ __device__ __forceinline__ void piece_forward_state(PieceSmem& sm, Slab& S) {
   rhs = mfma32(lo32(lds_operand<kTriStride>(sm.tri[kTLak], n, 4 * g)), lo32(v_op), rhs);
   const f32x4 sa =
       mfma32(lo32(lds_operand<kTriStride>(sm.tri[kTT], n, 4 * g)), lo32(to_operand(rhs)), zero4());
-  const i16x8 sav = cat(to_operand(sa), v_op);
+  const i16x4 sa_op = to_operand(sa);
+  if (kOut && p.out != nullptr) {
+    // Y^T = S0^T Rt^T + [SA^T | V^T] [Arb^T ; Ark^T]: lane (g, n) holds
+    // y[t = n][16w + 4g + j].
+    f32x4 yt = zero4();
+#pragma unroll
+    for (int c = 0; c < kPD / 32; ++c) {
+      yt = mfma32(cat(s_op[2 * c], s_op[2 * c + 1]), lds_operand32<kPS>(sm.rt, n, 32 * c, g), yt);
+    }
+    yt = mfma32(cat(sa_op, v_op), cat(lds_operand<kTriStride>(sm.tri[kTArb], n, 4 * g),
+                                      lds_operand<kTriStride>(sm.tri[kTArk], n, 4 * g)),
+                yt);
+    const uint32_t row_bytes = static_cast<uint32_t>(p.num_heads) * kPD * 2;
+    const int64_t base = (static_cast<int64_t>(t0) * p.num_heads + head) * kPD;
+    const auto out_rs =
+        buffer_rsrc(static_cast<St*>(p.out) + base, static_cast<uint32_t>(ntok) * row_bytes);
+    const u32x2 q = {pack2<T>(p.scale * yt[0], p.scale * yt[1]),
+                     pack2<T>(p.scale * yt[2], p.scale * yt[3])};
+    __builtin_amdgcn_raw_buffer_store_b64(
+        q, out_rs,
+        rows.on ? static_cast<uint32_t>(n) * row_bytes + 2 * (16 * w + 4 * g) : kDropOffset, 0,
+        0);
+    // state_dot_a[t][16w + n] = SA[t][n]: lane (g, n) holds tokens 4g + j.
+    const auto sda_rs =
+        buffer_rsrc(p.state_dot_a + base, static_cast<uint32_t>(ntok) * row_bytes * 2);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = 4 * g + j;
+      const bool on = t >= rows.lo && t < rows.hi;
+      __builtin_amdgcn_raw_buffer_store_b32(
+          __float_as_uint(sa[j]), sda_rs,
+          on ? static_cast<uint32_t>(t) * row_bytes * 2 + 4 * (16 * w + n) : kDropOffset, 0, 0);
+    }
+  }
+  const i16x8 sav = cat(sa_op, v_op);
 #pragma unroll
   for (int kb = 0; kb < kPD / 16; ++kb) {
     const i16x8 a = cat(lds_operand_tr<kPS>(sm.bh, 0, 16 * kb, g, n),
@@ -644,7 +689,7 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_bwd_kernel(TrainParams p) 
         prepared = false;
         if (fwd) {
           piece_intra(sm);
-          piece_forward_state(sm, S);
+          piece_forward_state<T, false>(sm, S, rows, p, head, t0, ntok);
           ++q;
           continue;
         }
@@ -665,16 +710,117 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_bwd_kernel(TrainParams p) 
   }
 }
 
+// The head-size-128 training forward: the per-token forward's outputs and
+// checkpoints (train_recurrent.hip) from 16-token pieces. Per chunk of the
+// unit: the state at the chunk start (ckpt), at every further 16-token piece
+// start (interior, slot (piece start) / 16), y and state_dot_a per token, and
+// the final state. kFill: the interior replay (one chunk per unit, only the
+// interior states; chunks of at most 16 tokens are skipped and a chunk's last
+// piece is not computed).
+template <typename T, DecayMode M, bool kFill>
+__global__ __launch_bounds__(kPThreads, 1) void piece_fwd_kernel(TrainParams p) {
+  __shared__ PieceSmem sm;
+  using St = typename IoTraits<T>::storage;
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, lane = tid & 63;
+  const int g = lane >> 4;
+  const int unit = blockIdx.x;
+  const int seq = unit / p.num_heads;
+  const int head = unit % p.num_heads;
+  const int64_t unit_state =
+      (static_cast<int64_t>(seq) * p.num_heads + head) * static_cast<int64_t>(kPD) * kPD;
+
+  float bias[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (M == DecayMode::kLogits) {
+    if (p.bias != nullptr) {
+      const St* bp = static_cast<const St*>(p.bias) + head * kPD + 16 * w + 4 * g;
+      const uint2 q = *reinterpret_cast<const uint2*>(bp);
+      unpack4<T>(q, bias);
+    }
+  }
+  Slab S;
+  if (p.state != nullptr) {
+    load_slab16(S, p.state + unit_state);
+  } else {
+#pragma unroll
+    for (int kb = 0; kb < kPD / 16; ++kb) S.x[kb] = zero4();
+  }
+
+  int c_begin, c_end;
+  chunk_range(p, seq, c_begin, c_end);
+  bool range_ok = true;
+  PieceRows rows;
+  for (int c = c_begin; c < c_end; ++c) {
+    const Chunk ch = chunk_at<kPD>(p, seq, head, c);
+    if (!chunk_ok(ch, p.total_tokens)) {
+      range_ok = false;
+      break;
+    }
+    const int len = ch.end - ch.start;
+    if (kFill && len <= kPiece) continue;
+    const int pieces = len > kPiece ? (len + kPiece - 1) / kPiece : 1;
+    for (int pj = 0; pj < pieces; ++pj) {
+      const int32_t t0 = ch.start + kPiece * pj;
+      const int ntok = min(kPiece, ch.end - t0);
+      if (pj == 0 && !kFill && p.ckpt != nullptr) store_slab16(p.ckpt + ch.ckpt_off, S);
+      if (pj > 0 && p.interior != nullptr) {
+        store_slab16(p.interior + (static_cast<int64_t>(t0 / kPiece) * p.num_heads + head) *
+                                      static_cast<int64_t>(kPD) * kPD,
+                     S);
+      }
+      if (ntok <= 0 || (kFill && t0 + kPiece >= ch.end)) break;
+      piece_prepare<T, M>(sm, rows, p, bias, head, t0, ntok, 0, ntok);
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < kPWaves; ++i) ok = ok && sm.span_ok[i] != 0;
+      ok = __builtin_amdgcn_readfirstlane(ok ? 1 : 0) != 0;
+      // One pass over [0, ntok), or under strong decay 4-token sub-pieces in
+      // order, each continuing from the state the one before it left.
+      int sub = 0;
+      bool prepared = ok;
+      for (;;) {
+        const int lo = ok ? 0 : 4 * sub;
+        const int hi = ok ? ntok : min(lo + 4, ntok);
+        if (!prepared) piece_prepare<T, M>(sm, rows, p, bias, head, t0, ntok, lo, hi);
+        prepared = false;
+        piece_intra(sm);
+        piece_forward_state<T, !kFill>(sm, S, rows, p, head, t0, ntok);
+        if (hi >= ntok) break;
+        ++sub;
+      }
+    }
+  }
+
+  if (p.state != nullptr && !kFill) {
+    if (!range_ok) {
+      const float nan = __int_as_float(0x7fc00000);
+#pragma unroll
+      for (int kb = 0; kb < kPD / 16; ++kb) S.x[kb] = f32x4{nan, nan, nan, nan};
+    }
+    store_slab16(p.state + unit_state, S);
+  }
+}
+
 template <typename T, DecayMode M>
-int launch_piece(const TrainParams& p, int units, hipStream_t stream) {
-  hipLaunchKernelGGL((piece_bwd_kernel<T, M>), dim3(units), dim3(kPThreads), 0, stream, p);
-  return check_launch("piece_bwd_kernel");
+int launch_piece(const TrainParams& p, int units, bool backward, hipStream_t stream) {
+  if (backward) {
+    hipLaunchKernelGGL((piece_bwd_kernel<T, M>), dim3(units), dim3(kPThreads), 0, stream, p);
+    return check_launch("piece_bwd_kernel");
+  }
+  if (p.fill_only) {
+    hipLaunchKernelGGL((piece_fwd_kernel<T, M, true>), dim3(units), dim3(kPThreads), 0, stream,
+                       p);
+  } else {
+    hipLaunchKernelGGL((piece_fwd_kernel<T, M, false>), dim3(units), dim3(kPThreads), 0, stream,
+                       p);
+  }
+  return check_launch("piece_fwd_kernel");
 }
 
 }  // namespace
 
-int launch_piece_backward(const TrainParams& p, int io_dtype, int decay_mode, int units,
-                          hipStream_t stream) {
+int launch_piece_train(const TrainParams& p, int io_dtype, int decay_mode, int units,
+                       bool backward, hipStream_t stream) {
   const bool logits = decay_mode == FRWKV_DECAY_LOGITS;
   if (!logits && decay_mode != FRWKV_DECAY_RAW_W) {
     return set_error(FRWKV_ERR_INVALID_ARGUMENT, "unknown decay mode %d", decay_mode);
@@ -685,11 +831,11 @@ int launch_piece_backward(const TrainParams& p, int io_dtype, int decay_mode, in
   }
   switch (io_dtype) {
     case FRWKV_DTYPE_BF16:
-      return logits ? launch_piece<Bf16, DecayMode::kLogits>(p, units, stream)
-                    : launch_piece<Bf16, DecayMode::kRawW>(p, units, stream);
+      return logits ? launch_piece<Bf16, DecayMode::kLogits>(p, units, backward, stream)
+                    : launch_piece<Bf16, DecayMode::kRawW>(p, units, backward, stream);
     case FRWKV_DTYPE_F16:
-      return logits ? launch_piece<F16, DecayMode::kLogits>(p, units, stream)
-                    : launch_piece<F16, DecayMode::kRawW>(p, units, stream);
+      return logits ? launch_piece<F16, DecayMode::kLogits>(p, units, backward, stream)
+                    : launch_piece<F16, DecayMode::kRawW>(p, units, backward, stream);
     default:
       return set_error(FRWKV_ERR_UNSUPPORTED,
                        "training kernels take float16 or bfloat16 tokens (io dtype %d)",

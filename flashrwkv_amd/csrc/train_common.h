@@ -1,6 +1,6 @@
 // Parameters and chunk walking shared by the head-size-128/256 training
 // kernels: the per-token kernels (train_recurrent.hip) and the head-size-128
-// MFMA backward over 16-token pieces (piece_bwd.hip).
+// MFMA kernels over 16-token pieces (piece_train.hip).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -98,10 +98,10 @@ __device__ __forceinline__ bool chunk_ok(const Chunk& ch, int32_t total_tokens) 
   return ch.start >= 0 && ch.end >= ch.start && ch.end <= total_tokens;
 }
 
-// The head-size-128 backward on bf16 MFMA (piece_bwd.hip), for the
-// per-token forward's checkpoints. Same parameters and outputs as the
-// per-token backward at head size 128 (one workgroup per (sequence, head)).
-int launch_piece_backward(const TrainParams& p, int io_dtype, int decay_mode, int units,
-                          hipStream_t stream);
+// The head-size-128 training forward or backward on bf16 MFMA over 16-token
+// pieces (piece_train.hip). Same parameters, outputs and checkpoint layout as
+// the per-token kernels at head size 128 (one workgroup per unit).
+int launch_piece_train(const TrainParams& p, int io_dtype, int decay_mode, int units,
+                       bool backward, hipStream_t stream);
 
 }  // namespace frwkv

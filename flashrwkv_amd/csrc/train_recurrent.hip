@@ -893,6 +893,10 @@ int frwkv_train_recurrent_forward(int io_dtype, int decay_mode, int32_t num_sequ
   p.b = b;
   p.out = output;
   p.scale = scale;
+  if (head_size == 128) {
+    return launch_piece_train(p, io_dtype, decay_mode, num_sequences * num_heads,
+                              /*backward=*/false, static_cast<hipStream_t>(stream));
+  }
   return dispatch_train_io(p, io_dtype, decay_mode, head_size, num_sequences * num_heads,
                            /*backward=*/false, static_cast<hipStream_t>(stream));
 }
@@ -948,7 +952,8 @@ int frwkv_train_recurrent_backward(int io_dtype, int decay_mode, int32_t num_seq
     p.accum = slices;
   }
   if (head_size == 128) {
-    return launch_piece_backward(p, io_dtype, decay_mode, num_sequences * num_heads, s);
+    return launch_piece_train(p, io_dtype, decay_mode, num_sequences * num_heads,
+                              /*backward=*/true, s);
   }
   const int rc = dispatch_train_io(p, io_dtype, decay_mode, head_size,
                                    num_sequences * num_heads, /*backward=*/true, s);
