@@ -149,33 +149,50 @@ struct PieceRows {
   int lo, hi;  // the pass's range (wave-uniform)
 };
 
-// One (sub-)piece pass over tokens [lo, hi) of the piece at token t0 with
-// ntok tokens: loads the rows (zeros past ntok), masks the tokens outside
-// [lo, hi) (retention 1, zero operands), writes the scaled tiles, 2^g and the
-// wave's span verdict. Ends with a barrier.
-template <typename T, DecayMode M>
-__device__ __forceinline__ void piece_prepare(PieceSmem& sm, PieceRows& rows,
-                                              const TrainParams& p, const float (&bias)[4],
-                                              int head, int32_t t0, int ntok, int lo, int hi) {
+// The rows of token n, features 16w + 4g .. +3, of the piece at token t0
+// with ntok tokens (zeros past ntok; dy only for the backward).
+struct PieceLoad {
+  uint2 r, k, a, b, x, v, y;
+};
+
+template <typename T, bool kGrad>
+__device__ __forceinline__ void piece_load(PieceLoad& L, const TrainParams& p, int head,
+                                           int32_t t0, int ntok) {
   using S = typename IoTraits<T>::storage;
   const int tid = lane_tid();
   const int w = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, n = lane & 15;
-  const int f0 = 16 * w + 4 * g;
   const uint32_t row_bytes = static_cast<uint32_t>(p.num_heads) * kPD * 2;
   const int64_t base = (static_cast<int64_t>(t0) * p.num_heads + head) * kPD;
   const uint32_t range = static_cast<uint32_t>(ntok) * row_bytes;
-  const uint32_t off = static_cast<uint32_t>(n) * row_bytes + 2 * f0;
+  const uint32_t off = static_cast<uint32_t>(n) * row_bytes + 2 * (16 * w + 4 * g);
   auto load = [&](const void* src) {
     const auto rs = buffer_rsrc(src != nullptr ? static_cast<const S*>(src) + base : nullptr,
                                 src != nullptr ? range : 0u);
     const u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
     return make_uint2(q.x, q.y);
   };
-  const uint2 rq = load(p.r), kq = load(p.k), aq = load(p.a), bq = load(p.b);
-  const uint2 xq = load(p.decay);
-  const uint2 vq = load(p.v);
-  const uint2 yq = load(p.dy);
+  L.r = load(p.r);
+  L.k = load(p.k);
+  L.a = load(p.a);
+  L.b = load(p.b);
+  L.x = load(p.decay);
+  L.v = load(p.v);
+  L.y = kGrad ? load(p.dy) : make_uint2(0u, 0u);
+}
+
+// One (sub-)piece pass over tokens [lo, hi) of the loaded piece: masks the
+// tokens outside [lo, hi) (retention 1, zero operands), writes the scaled
+// tiles, 2^g and the wave's span verdict. Ends with a barrier.
+template <typename T, DecayMode M, bool kGrad>
+__device__ __forceinline__ void piece_stage(PieceSmem& sm, PieceRows& rows, const PieceLoad& L,
+                                            const TrainParams& p, const float (&bias)[4], int lo,
+                                            int hi) {
+  const int tid = lane_tid();
+  const int w = tid >> 6, lane = tid & 63;
+  const int g = lane >> 4, n = lane & 15;
+  const int f0 = 16 * w + 4 * g;
+  const uint2 rq = L.r, kq = L.k, aq = L.a, bq = L.b, xq = L.x, vq = L.v, yq = L.y;
   rows.on = n >= lo && n < hi;
   rows.lo = lo;
   rows.hi = hi;
@@ -193,14 +210,16 @@ __device__ __forceinline__ void piece_prepare(PieceSmem& sm, PieceRows& rows,
     rows.fgp[e] = shift16_one(incl, n);
     rows.fgn[e] = __builtin_amdgcn_rcpf(incl);
     mn = fminf(mn, incl);
-    float dwf;
-    if constexpr (M == DecayMode::kLogits) {
-      const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-kLog2E * xb));
-      dwf = -kExpNegHalf * sig * (1.0f - sig);
-    } else {
-      dwf = (xb >= 0x1p-20f && xb <= 1.0f) ? __builtin_amdgcn_rcpf(xb) : 0.0f;
+    if constexpr (kGrad) {
+      float dwf;
+      if constexpr (M == DecayMode::kLogits) {
+        const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-kLog2E * xb));
+        dwf = -kExpNegHalf * sig * (1.0f - sig);
+      } else {
+        dwf = (xb >= 0x1p-20f && xb <= 1.0f) ? __builtin_amdgcn_rcpf(xb) : 0.0f;
+      }
+      rows.dwf[e] = rows.on ? dwf : 0.0f;
     }
-    rows.dwf[e] = rows.on ? dwf : 0.0f;
   }
   float a4[4], r4[4], b4[4], k4[4], v4[4], y4[4];
   unpack4<T>(aq, a4);
@@ -223,8 +242,10 @@ __device__ __forceinline__ void piece_prepare(PieceSmem& sm, PieceRows& rows,
   put(sm.kh, on * k4[0] * rows.fgn[0], on * k4[1] * rows.fgn[1], on * k4[2] * rows.fgn[2],
       on * k4[3] * rows.fgn[3]);
   put(sm.vt, on * v4[0], on * v4[1], on * v4[2], on * v4[3]);
-  const float ys = on * p.scale;
-  put(sm.dy, ys * y4[0], ys * y4[1], ys * y4[2], ys * y4[3]);
+  if constexpr (kGrad) {
+    const float ys = on * p.scale;
+    put(sm.dy, ys * y4[0], ys * y4[1], ys * y4[2], ys * y4[3]);
+  }
   if (n == 15) {
     *reinterpret_cast<float4*>(&sm.gc[f0]) =
         make_float4(rows.fg[0], rows.fg[1], rows.fg[2], rows.fg[3]);
@@ -233,6 +254,16 @@ __device__ __forceinline__ void piece_prepare(PieceSmem& sm, PieceRows& rows,
   const bool ok = __builtin_amdgcn_ballot_w64(!(mn >= kSpanFloor)) == 0;
   if (lane == 0) sm.span_ok[w] = ok ? 1 : 0;
   __syncthreads();
+}
+
+// Load and stage in one (the backward's prepare).
+template <typename T, DecayMode M>
+__device__ __forceinline__ void piece_prepare(PieceSmem& sm, PieceRows& rows,
+                                              const TrainParams& p, const float (&bias)[4],
+                                              int head, int32_t t0, int ntok, int lo, int hi) {
+  PieceLoad L;
+  piece_load<T, true>(L, p, head, t0, ntok);
+  piece_stage<T, M, true>(sm, rows, L, p, bias, lo, hi);
 }
 
 // Lab, Lak, Arb, Ark (waves 0-3) and T = (I - Lab)^{-1} (wave 0). Ends with a
@@ -750,6 +781,10 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_fwd_kernel(TrainParams p) 
   chunk_range(p, seq, c_begin, c_end);
   bool range_ok = true;
   PieceRows rows;
+  // The rows of the next piece to compute are loaded while the current one
+  // is computed (have: L holds the piece at t0).
+  PieceLoad L;
+  bool have = false;
   for (int c = c_begin; c < c_end; ++c) {
     const Chunk ch = chunk_at<kPD>(p, seq, head, c);
     if (!chunk_ok(ch, p.total_tokens)) {
@@ -769,25 +804,46 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_fwd_kernel(TrainParams p) 
                      S);
       }
       if (ntok <= 0 || (kFill && t0 + kPiece >= ch.end)) break;
-      piece_prepare<T, M>(sm, rows, p, bias, head, t0, ntok, 0, ntok);
+      if (!have) piece_load<T, false>(L, p, head, t0, ntok);
+      piece_stage<T, M, false>(sm, rows, L, p, bias, 0, ntok);
       bool ok = true;
 #pragma unroll
       for (int i = 0; i < kPWaves; ++i) ok = ok && sm.span_ok[i] != 0;
       ok = __builtin_amdgcn_readfirstlane(ok ? 1 : 0) != 0;
+
+      // The next piece that computes: the chunk's next piece, else the next
+      // chunk's first (only once its range is checked).
+      int32_t t0n = 0;
+      int ntokn = 0;
+      if (pj + 1 < pieces) {
+        t0n = t0 + kPiece;
+        ntokn = (kFill && t0n + kPiece >= ch.end) ? 0 : min(kPiece, ch.end - t0n);
+      } else if (c + 1 < c_end) {
+        const Chunk chn = chunk_at<kPD>(p, seq, head, c + 1);
+        if (chunk_ok(chn, p.total_tokens) && !(kFill && chn.end - chn.start <= kPiece)) {
+          t0n = chn.start;
+          ntokn = min(kPiece, chn.end - chn.start);
+        }
+      }
+      PieceLoad Ln;
+      have = ntokn > 0;
+      if (have) piece_load<T, false>(Ln, p, head, t0n, ntokn);
+
       // One pass over [0, ntok), or under strong decay 4-token sub-pieces in
       // order, each continuing from the state the one before it left.
       int sub = 0;
-      bool prepared = ok;
+      bool staged = ok;
       for (;;) {
         const int lo = ok ? 0 : 4 * sub;
         const int hi = ok ? ntok : min(lo + 4, ntok);
-        if (!prepared) piece_prepare<T, M>(sm, rows, p, bias, head, t0, ntok, lo, hi);
-        prepared = false;
+        if (!staged) piece_stage<T, M, false>(sm, rows, L, p, bias, lo, hi);
+        staged = false;
         piece_intra(sm);
         piece_forward_state<T, !kFill>(sm, S, rows, p, head, t0, ntok);
         if (hi >= ntok) break;
         ++sub;
       }
+      if (have) L = Ln;
     }
   }
 

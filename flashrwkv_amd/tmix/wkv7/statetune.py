@@ -3,9 +3,9 @@
 ``statetune_recurrent_fp32io16`` keeps the reference's signature, error
 contract and outputs ``(y, S_T, boundary, state_dot_a)`` (reference
 ``flashrwkv2/tmix/wkv7/statetune.py:11-236``). Head size 64 runs the chunked
-bf16-MFMA kernels, 128 and 256 the per-token fp32 training kernels; either
-backward recomputes every chunk from stored states instead of dividing by the
-decay.
+bf16-MFMA kernels, 128 the bf16-MFMA kernels over 16-token pieces, 256 the
+per-token fp32 training kernels; every backward recomputes each chunk from
+stored states instead of dividing by the decay.
 
 Caller chunks may have any length. The kernels walk a chunk in pieces of P
 tokens (P = 64 at head size 64, 16 at 128 and 256); the forward keeps the
