@@ -1,8 +1,9 @@
-// Per-token WKV7 training kernels for head sizes 128 and 256.
+// Per-token WKV7 training kernels for head size 256.
 //
 // The chunked MFMA kernels (chunk_fwd.hip, chunk_bwd.hip) are built around
-// D = 64 tiles. These kernels serve the StateTune and pretraining entry points
-// at D = 128 and 256, which the reference accepts too
+// D = 64 tiles and the piece kernels (piece_train.hip) around D = 128. These
+// kernels serve the StateTune and pretraining entry points at D = 256, which
+// the reference accepts too
 // (flashrwkv2/tmix/wkv7/statetune.py:57-58, pretrain.py:16-17; kernels
 // csrc/sm90/tmix/wkv7/statetune_recurrent_fp32io16_{forward,backward}.cu and
 // pretrain_recurrent_bf16_forward.cu). They run the recurrence token by token
@@ -34,9 +35,8 @@
 // sums to its own fp32 slice and a second kernel adds the slices in group
 // order, so the gradients are deterministic. Chunks are walked in reverse and
 // must be at most 16 tokens; S_{t-1} is recomputed from the chunk's stored
-// start state (never by dividing by the decay), from a register copy of the
-// state 8 tokens into the chunk, or at D = 128 from an LDS copy of the state 4
-// tokens in.
+// start state (never by dividing by the decay) or from a register copy of the
+// state 8 tokens into the chunk.
 //
 // The recomputed states are bitwise equal to the forward's: both kernels use
 // the same lane layout per head size, the same fma forms and the same
@@ -53,12 +53,11 @@ namespace {
 // Columns per wave and waves per workgroup for each head size. The two fp32
 // state slabs (state and adjoint) of a lane take 2 * D * CW / 64 registers.
 template <int D> struct TrainShape;
-template <> struct TrainShape<128> { static constexpr int kCW = 16, kNW = 8; };
 template <> struct TrainShape<256> { static constexpr int kCW = 8, kNW = 8; };
 
 // The retention of the training kernels: raw retention clamped to
-// [2^-20, 1], as the chunked MFMA kernels (head size 64 and the head-size-128
-// backward) take it, so every head size trains on the same function.
+// [2^-20, 1], as the MFMA training kernels (head sizes 64 and 128) take it,
+// so every head size trains on the same function.
 template <DecayMode M>
 __device__ __forceinline__ float train_retention(float x) {
   if constexpr (M == DecayMode::kLogits) {
@@ -424,11 +423,6 @@ struct BwdSmem {
   // Per-wave partial sums over the wave's columns: [buffer][wave][gradient][key]
   // with gradients dr, dk, db, dw, da.
   float red[2][kNW][5][D];
-  // D = 128: the workgroup's state slab 4 tokens into the chunk ([key][column],
-  // each lane reading back only what it wrote), which the LDS budget allows
-  // there and not at D = 256.
-  static constexpr bool kMid4 = D == 128;
-  float mid4[kMid4 ? D : 1][kMid4 ? kCols : 4];
 };
 
 template <int D, typename T, DecayMode M>
@@ -580,27 +574,11 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_bwd_kernel(TrainPar
       const float4 vv = decode4f<T>(lds8(&sm.v[i][wcol]));
       step_state<D, T, true>(s, sm.a[i], sm.b[i], sm.k[i], sm.w[i], vv, row0);
     };
-    // S^8, the state 8 tokens into the chunk (when the chunk is longer), and
-    // at D = 128 also S^4 in LDS, passed on the way.
-    constexpr bool kMid4 = BwdSmem<D>::kMid4;
-    auto mid4_row = [&](int j) -> float4* {
-      return reinterpret_cast<float4*>(&sm.mid4[kMid4 ? row0 + j : 0][kMid4 ? wcol : 0]);
-    };
+    // S^8, the state 8 tokens into the chunk (when the chunk is longer).
     float4 cm[kRpl];
-    const int last = n > 8 ? 8 : (kMid4 && n > 4 ? 4 : 0);
-    if (last > 0) {
+    if (n > 8) {
       load_slab<D, kRpl>(cm, ck, row0, col);
-      for (int i = 0; i < last; ++i) {
-        if (kMid4 && i == 4) {
-#pragma unroll
-          for (int j = 0; j < kRpl; ++j) *mid4_row(j) = cm[j];
-        }
-        step(cm, i);
-      }
-      if (kMid4 && last == 4) {
-#pragma unroll
-        for (int j = 0; j < kRpl; ++j) *mid4_row(j) = cm[j];
-      }
+      for (int i = 0; i < 8; ++i) step(cm, i);
     }
 
     for (int jt = n - 1; jt >= 0; --jt) {
@@ -611,10 +589,6 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_bwd_kernel(TrainPar
 #pragma unroll
         for (int j = 0; j < kRpl; ++j) s[j] = cm[j];
         i0 = 8;
-      } else if (kMid4 && jt >= 4) {
-#pragma unroll
-        for (int j = 0; j < kRpl; ++j) s[j] = *mid4_row(j);
-        i0 = 4;
       } else {
         load_slab<D, kRpl>(s, ck, row0, col);
       }
@@ -801,8 +775,6 @@ int launch_train_backward(const TrainParams& p, int units, hipStream_t stream) {
 
 int slice_groups(int head_size) {
   switch (head_size) {
-    case 128:
-      return Layout<128>::kGroups;
     case 256:
       return Layout<256>::kGroups;
     default:
@@ -814,15 +786,12 @@ template <typename T, DecayMode M>
 int dispatch_train(const TrainParams& p, int head_size, int units, bool backward,
                    hipStream_t s) {
   switch (head_size) {
-    case 128:
-      return backward ? launch_train_backward<128, T, M>(p, units, s)
-                      : launch_train_forward<128, T, M>(p, units, s);
     case 256:
       return backward ? launch_train_backward<256, T, M>(p, units, s)
                       : launch_train_forward<256, T, M>(p, units, s);
     default:
       return set_error(FRWKV_ERR_UNSUPPORTED,
-                       "the per-token training kernels take head size 128 or 256, got %d",
+                       "the per-token training kernels take head size 256, got %d",
                        head_size);
   }
 }

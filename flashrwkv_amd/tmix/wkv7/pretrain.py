@@ -6,8 +6,8 @@ dense bf16 ``[B,T,C]`` tokens with decay logits ``w`` (retention
 ``exp(-e^{-1/2} sigmoid(w))``), zero initial state, output ``[B,T,C]``.
 
 Both directions run through ``torch.ops.rwkv7_clampw_v3``: head size 64 on
-the chunked bf16-MFMA kernels, 128 and 256 on the per-token fp32 training
-kernels. The forward saves the state every 16 tokens; the backward recomputes
+the chunked bf16-MFMA kernels, 128 on the bf16-MFMA kernels over 16-token
+pieces, 256 on the per-token fp32 training kernels. The forward saves the state every 16 tokens; the backward recomputes
 from those states and never divides by the decay.
 """
 

@@ -215,7 +215,8 @@ int frwkv_chunk_forward(int io_dtype, int decay_mode, int pool_dtype,
  * Replaces statetune_recurrent_fp32io16_forward_cuda
  * (csrc/sm90/tmix/wkv7/statetune_recurrent_fp32io16_forward.cu:32-224;
  * binding statetune_recurrent_fp32io16_forward.cpp:26-56). head_size 64
- * runs the chunked MFMA kernel; 128 and 256 run the per-token fp32 kernel.
+ * runs the chunked MFMA kernel, 128 the MFMA kernel over 16-token pieces,
+ * 256 the per-token fp32 kernel.
  */
 int frwkv_statetune_forward(int io_dtype, int decay_mode, int32_t num_sequences,
                             int32_t num_heads, int32_t head_size,
@@ -272,8 +273,9 @@ int frwkv_statetune_interior(int io_dtype, int decay_mode, int32_t num_heads,
  * Replaces statetune_recurrent_fp32io16_backward_cuda
  * (csrc/sm90/tmix/wkv7/statetune_recurrent_fp32io16_backward.cu:49-676;
  * binding statetune_recurrent_fp32io16_backward.cpp:34-82). head_size 64
- * runs the chunked MFMA kernel, 128 and 256 the per-token fp32 kernel (at 256
- * with fp32 gradient slices in the workspace, added in a fixed order).
+ * runs the chunked MFMA kernel, 128 the MFMA kernel over 16-token pieces, 256
+ * the per-token fp32 kernel (with fp32 gradient slices in the workspace, added
+ * in a fixed order).
  */
 int frwkv_statetune_backward(int io_dtype, int decay_mode, int32_t num_sequences,
                              int32_t num_heads, int32_t head_size,
@@ -337,7 +339,8 @@ int frwkv_statetune_backward_noalloc(int io_dtype, int decay_mode, int32_t num_s
  * [B,H,T/16,D,D] fp32 receives the state every 16 tokens (entry i: the state
  * before token 16 i); state_dot_a [B,T,H,D] fp32 receives a_t^T S_{t-1}.
  * T must be a multiple of 16; head_size 64, 128 or 256 (64 on the chunked
- * MFMA kernel, 128 and 256 on the per-token fp32 kernel).
+ * MFMA kernel, 128 on the MFMA piece kernel, 256 on the per-token fp32
+ * kernel).
  * Replaces rwkv7_clampw_v3::forward / cuda_forward_v3
  * (csrc/sm90/tmix/wkv7/pretrain_recurrent_bf16_forward.cpp:20-26, 50-53;
  * kernel pretrain_recurrent_bf16_forward.cu).

@@ -1,5 +1,6 @@
 """GPU parity of the StateTune training path (forward + backward; head size 64
-on the chunked MFMA kernels, 128 and 256 on the per-token fp32 kernels).
+on the chunked MFMA kernels, 128 on the MFMA piece kernels, 256 on the
+per-token fp32 kernels).
 
 Expected values: the fp64 oracle forward (boundary and state_dot_a
 definitions of /root/reference/tests/tmix/wkv7/statetune/test.py:39-88) and
@@ -344,7 +345,7 @@ def test_initial_state_not_mutated_and_boundary_not_differentiable():
 @pytest.mark.parametrize("head_size", (128, 256))
 @pytest.mark.parametrize("lengths,chunk", [((40, 7), 16), ((70,), 64), ((33, 16, 1), 5)])
 def test_large_heads_forward_and_gradients(head_size, lengths, chunk):
-    """Head sizes 128 and 256 (per-token kernels): caller chunks of 16 tokens
+    """Head sizes 128 (MFMA pieces) and 256 (per-token): caller chunks of 16 tokens
     or fewer run as one piece, longer ones as 16-token pieces whose start
     states the forward keeps in the interior buffer."""
     meta = oracle.chunk_metadata(lengths, chunk)
