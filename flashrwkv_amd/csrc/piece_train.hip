@@ -266,6 +266,81 @@ __device__ __forceinline__ void piece_prepare(PieceSmem& sm, PieceRows& rows,
   piece_stage<T, M, true>(sm, rows, L, p, bias, lo, hi);
 }
 
+// The rows of the backward's next piece, loaded straight into LDS (buffer ->
+// LDS loads, 16 bytes per lane) while the current piece computes: r, k, a, b,
+// decay, v and dy, 16 tokens x 256 bytes each. A 1 KiB block holds 4 tokens;
+// token n's 16-byte chunk c (features 8c .. 8c + 7) sits at position
+// (n % 4) * 16 + ((c + n) & 15) of its block, so that the stage's 8-byte reads
+// (16 tokens x 2 chunks per wave) fall on distinct bank pairs. Tokens past
+// the piece read as zeros (out of the buffer range).
+constexpr int kStageTensors = 7;
+// s_waitcnt vmcnt(0), expcnt and lgkmcnt left at their maxima.
+constexpr int kWaitVmcnt0 = 0x0f70;
+struct RowStage {
+  uint16_t x[kStageTensors][kPiece * kPD];
+};
+
+template <typename T>
+__device__ __forceinline__ void piece_rows_to_lds(RowStage& st, const TrainParams& p, int head,
+                                                  int32_t t0, int ntok) {
+  using S = typename IoTraits<T>::storage;
+  const int tid = lane_tid();
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const uint32_t row_bytes = static_cast<uint32_t>(p.num_heads) * kPD * 2;
+  const int64_t base = (static_cast<int64_t>(t0) * p.num_heads + head) * kPD;
+  const uint32_t range = static_cast<uint32_t>(ntok) * row_bytes;
+  // 28 wave loads of 1 KiB (tensor ti, block b): waves 0-3 take four, 4-7 three.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int slot = w + 8 * i;
+    if (slot < kStageTensors * 4) {
+      const int ti = slot >> 2, b = slot & 3;
+      const void* src = ti == 0   ? p.r
+                        : ti == 1 ? p.k
+                        : ti == 2 ? p.a
+                        : ti == 3 ? p.b
+                        : ti == 4 ? p.decay
+                        : ti == 5 ? p.v
+                                  : p.dy;
+      const uint64_t addr =
+          src != nullptr ? reinterpret_cast<uint64_t>(static_cast<const S*>(src) + base) : 0;
+      const u32x4 rs = {static_cast<uint32_t>(addr), static_cast<uint32_t>(addr >> 32),
+                        src != nullptr ? range : 0u, 0x00020000u};
+      const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+          (__attribute__((address_space(3))) void*)&st.x[ti][4 * b * kPD]));
+      const int n = 4 * b + (lane >> 4);
+      const int c = ((lane & 15) - n) & 15;
+      const uint32_t off = static_cast<uint32_t>(n) * row_bytes + 16 * c;
+      // Written as assembly so that the compiler does not order every later
+      // LDS access after these loads: the staging area is only read after
+      // the explicit vmcnt(0) wait and barrier at the next piece's start.
+      // M0 (the LDS base of the load) is not used by any other instruction
+      // of the kernel.
+      asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                   :
+                   : "v"(off), "s"(rs), "s"(lds)
+                   : "memory");
+    }
+  }
+}
+
+// The thread's rows (token n, features 16w + 4g .. +3) from the staged piece.
+__device__ __forceinline__ void piece_load_staged(PieceLoad& L, const RowStage& st) {
+  const int tid = lane_tid();
+  const int w = tid >> 6, lane = tid & 63;
+  const int g = lane >> 4, n = lane & 15;
+  const int c = 2 * w + (g >> 1);
+  const int off = (n >> 2) * 4 * kPD + 8 * ((n & 3) * 16 + ((c + n) & 15)) + 4 * (g & 1);
+  auto rd = [&](int ti) { return *reinterpret_cast<const uint2*>(&st.x[ti][off]); };
+  L.r = rd(0);
+  L.k = rd(1);
+  L.a = rd(2);
+  L.b = rd(3);
+  L.x = rd(4);
+  L.v = rd(5);
+  L.y = rd(6);
+}
+
 // Lab, Lak, Arb, Ark (waves 0-3) and T = (I - Lab)^{-1} (wave 0). Ends with a
 // barrier.
 __device__ __forceinline__ void piece_intra(PieceSmem& sm) {
@@ -460,6 +535,10 @@ __device__ __forceinline__ void piece_backward(PieceSmem& sm, const PieceRows& r
   };
 
   // ---- columns: value columns 16w .. 16w+15 ----
+  // Every vector memory load of this wave has landed: the start state read
+  // here, and the next piece's rows staged before it (read after the barrier
+  // that ends this phase).
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int kb = 0; kb < kPD / 16; ++kb) {
@@ -629,6 +708,7 @@ __device__ __forceinline__ void piece_backward(PieceSmem& sm, const PieceRows& r
 template <typename T, DecayMode M>
 __global__ __launch_bounds__(kPThreads, 1) void piece_bwd_kernel(TrainParams p) {
   __shared__ PieceSmem sm;
+  __shared__ __align__(16) RowStage stage;
   using St = typename IoTraits<T>::storage;
   const int tid = threadIdx.x;
   const int w = tid >> 6, lane = tid & 63;
@@ -675,6 +755,9 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_bwd_kernel(TrainParams p) 
   chunk_range(p, seq, c_begin, c_end);
   bool failed = false;
   PieceRows rows;
+  // have: the rows of the piece at t0 are staged in LDS (loaded while the
+  // piece after it computed).
+  bool have = false;
   for (int c = c_end - 1; c >= c_begin; --c) {
     const Chunk whole = chunk_at<kPD>(p, seq, head, c);
     const bool range_ok = chunk_ok(whole, p.total_tokens);
@@ -693,18 +776,52 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_bwd_kernel(TrainParams p) 
           pj == 0 ? p.ckpt + whole.ckpt_off
                   : p.interior + (static_cast<int64_t>(t0 / kPiece) * p.num_heads + head) *
                                      static_cast<int64_t>(kPD) * kPD;
+      // The next piece (walking backwards): this chunk's previous piece, else
+      // the last piece of the chunk before when that chunk will not fail.
+      // Found here, before the start state's loads are issued: reading the
+      // chunk metadata waits for every load in flight.
+      int32_t t0n = 0;
+      int ntokn = 0;
+      if (pj > 0) {
+        t0n = t0 - kPiece;
+        ntokn = kPiece;
+      } else if (c > c_begin) {
+        const Chunk wn = chunk_at<kPD>(p, seq, head, c - 1);
+        const int lenn = wn.end - wn.start;
+        const int piecesn = lenn > kPiece ? (lenn + kPiece - 1) / kPiece : 1;
+        if (chunk_ok(wn, p.total_tokens) && !(piecesn > 1 && p.interior == nullptr)) {
+          t0n = wn.start + kPiece * (piecesn - 1);
+          ntokn = min(kPiece, wn.end - t0n);
+        }
+      }
+      // The piece's rows: staged while the piece after it computed (its
+      // column phase waited for them, and barriers followed), or now. Once
+      // every wave has read them, the next piece's rows are staged, then the
+      // start state is loaded.
+      if (!have) {
+        piece_rows_to_lds<T>(stage, p, head, t0, ntok);
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();
+      }
+      PieceLoad L;
+      piece_load_staged(L, stage);
+      __syncthreads();
+      have = ntokn > 0;
+      if (have) piece_rows_to_lds<T>(stage, p, head, t0n, ntokn);
       Slab S;
       load_slab16(S, ck);
-      piece_prepare<T, M>(sm, rows, p, bias, head, t0, ntok, 0, ntok);
+      piece_stage<T, M, true>(sm, rows, L, p, bias, 0, ntok);
       bool ok = true;
 #pragma unroll
       for (int i = 0; i < kPWaves; ++i) ok = ok && sm.span_ok[i] != 0;
       ok = __builtin_amdgcn_readfirstlane(ok ? 1 : 0) != 0;
+
+
       // One pass sequence with a single copy of each phase. A piece within
       // the span limit is one backward pass over [0, ntok), on the rows just
-      // prepared. Strong decay: 4-token sub-pieces s = nsub - 1 .. 0, each
+      // staged. Strong decay: 4-token sub-pieces s = nsub - 1 .. 0, each
       // preceded by forward passes over sub-pieces 0 .. s - 1 from the piece
-      // start state.
+      // start state, every pass on rows loaded again from global memory.
       const int nsub = (ntok + 3) / 4;
       int sub = ok ? 0 : nsub - 1;
       int q = 0;
