@@ -62,6 +62,13 @@ struct Chunk {
   int64_t ckpt_off;  // element offset of the chunk start state
 };
 
+// Chunk metadata is read-only for a whole launch: read it through the
+// constant address space, so that its (uniform) reads are scalar loads,
+// which do not wait for the vector memory operations in flight.
+__device__ __forceinline__ int32_t meta_at(const int32_t* a, int i) {
+  return ((const __attribute__((address_space(4))) int32_t*)a)[i];
+}
+
 __device__ __forceinline__ void chunk_range(const TrainParams& p, int seq, int& c_begin,
                                             int& c_end) {
   if (p.dense_t > 0) {
@@ -73,8 +80,8 @@ __device__ __forceinline__ void chunk_range(const TrainParams& p, int seq, int& 
   } else {
     // Clamped to the chunk arrays, so malformed offsets cannot address
     // outside them.
-    c_begin = __builtin_amdgcn_readfirstlane(max(p.seg_offsets[seq], 0));
-    c_end = __builtin_amdgcn_readfirstlane(min(p.seg_offsets[seq + 1], p.num_chunks));
+    c_begin = __builtin_amdgcn_readfirstlane(max(meta_at(p.seg_offsets, seq), 0));
+    c_end = __builtin_amdgcn_readfirstlane(min(meta_at(p.seg_offsets, seq + 1), p.num_chunks));
   }
 }
 
@@ -87,8 +94,8 @@ __device__ __forceinline__ Chunk chunk_at(const TrainParams& p, int seq, int hea
     ch.ckpt_off = ((static_cast<int64_t>(seq) * p.num_heads + head) * (p.dense_t / kPiece) + c) *
                   static_cast<int64_t>(D) * D;
   } else {
-    ch.start = __builtin_amdgcn_readfirstlane(p.seg_starts[c]);
-    ch.end = __builtin_amdgcn_readfirstlane(p.seg_ends[c]);
+    ch.start = __builtin_amdgcn_readfirstlane(meta_at(p.seg_starts, c));
+    ch.end = __builtin_amdgcn_readfirstlane(meta_at(p.seg_ends, c));
     ch.ckpt_off = (static_cast<int64_t>(c) * p.num_heads + head) * static_cast<int64_t>(D) * D;
   }
   return ch;
