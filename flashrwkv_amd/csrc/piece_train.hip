@@ -433,16 +433,54 @@ __device__ __forceinline__ i16x8 lo32(i16x4 x) {
   return cat(x, z);
 }
 
+// The outputs of a forward pass, held until they are stored: lane (g, n)
+// has y[t = n][16w + 4g .. +3] (scaled, packed) and state_dot_a[t][16w + n]
+// for the pass's tokens t = 4g + j.
+struct PieceOut {
+  u32x2 y;
+  f32x4 sa;
+  int32_t t0;
+  int ntok, lo, hi;
+  bool on;  // token n is inside [lo, hi)
+};
+
+// Stores the held outputs; tokens outside the pass's range go to
+// kDropOffset (dropped), so every lane issues the same stores.
+template <typename T>
+__device__ __forceinline__ void store_piece_out(const PieceOut& o, const TrainParams& p,
+                                                int head) {
+  using St = typename IoTraits<T>::storage;
+  const int tid = lane_tid();
+  const int w = tid >> 6, lane = tid & 63;
+  const int g = lane >> 4, n = lane & 15;
+  const uint32_t row_bytes = static_cast<uint32_t>(p.num_heads) * kPD * 2;
+  const int64_t base = (static_cast<int64_t>(o.t0) * p.num_heads + head) * kPD;
+  const auto out_rs =
+      buffer_rsrc(static_cast<St*>(p.out) + base, static_cast<uint32_t>(o.ntok) * row_bytes);
+  __builtin_amdgcn_raw_buffer_store_b64(
+      o.y, out_rs, o.on ? static_cast<uint32_t>(n) * row_bytes + 2 * (16 * w + 4 * g) : kDropOffset,
+      0, 0);
+  const auto sda_rs =
+      buffer_rsrc(p.state_dot_a + base, static_cast<uint32_t>(o.ntok) * row_bytes * 2);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int t = 4 * g + j;
+    const bool on = t >= o.lo && t < o.hi;
+    __builtin_amdgcn_raw_buffer_store_b32(
+        __float_as_uint(o.sa[j]), sda_rs,
+        on ? static_cast<uint32_t>(t) * row_bytes * 2 + 4 * (16 * w + n) : kDropOffset, 0, 0);
+  }
+}
+
 // A forward pass of the prepared (sub-)piece on the wave's slab:
-// S <- diag(g) (S + Bh^T SA + Kh^T V). kOut: also the outputs of its tokens
-// (those inside the pass's range; the others store to kDropOffset):
-// y = scale (Rt S0 + Arb SA + Ark V) and state_dot_a = SA, for the wave's
-// value columns, when p.out is set. Ends with a barrier.
+// S <- diag(g) (S + Bh^T SA + Kh^T V). kOut: also the outputs of its tokens,
+// y = scale (Rt S0 + Arb SA + Ark V) and state_dot_a = SA for the wave's
+// value columns, into `out` (p.out set). Ends with a barrier.
 template <typename T, bool kOut>
 __device__ __forceinline__ void piece_forward_state(PieceSmem& sm, Slab& S,
                                                     const PieceRows& rows,
-                                                    const TrainParams& p, int head, int32_t t0,
-                                                    int ntok) {
+                                                    const TrainParams& p, int32_t t0, int ntok,
+                                                    PieceOut& out) {
   using St = typename IoTraits<T>::storage;
   const int tid = lane_tid();
   const int w = tid >> 6, lane = tid & 63;
@@ -472,27 +510,14 @@ __device__ __forceinline__ void piece_forward_state(PieceSmem& sm, Slab& S,
     yt = mfma32(cat(sa_op, v_op), cat(lds_operand<kTriStride>(sm.tri[kTArb], n, 4 * g),
                                       lds_operand<kTriStride>(sm.tri[kTArk], n, 4 * g)),
                 yt);
-    const uint32_t row_bytes = static_cast<uint32_t>(p.num_heads) * kPD * 2;
-    const int64_t base = (static_cast<int64_t>(t0) * p.num_heads + head) * kPD;
-    const auto out_rs =
-        buffer_rsrc(static_cast<St*>(p.out) + base, static_cast<uint32_t>(ntok) * row_bytes);
-    const u32x2 q = {pack2<T>(p.scale * yt[0], p.scale * yt[1]),
-                     pack2<T>(p.scale * yt[2], p.scale * yt[3])};
-    __builtin_amdgcn_raw_buffer_store_b64(
-        q, out_rs,
-        rows.on ? static_cast<uint32_t>(n) * row_bytes + 2 * (16 * w + 4 * g) : kDropOffset, 0,
-        0);
-    // state_dot_a[t][16w + n] = SA[t][n]: lane (g, n) holds tokens 4g + j.
-    const auto sda_rs =
-        buffer_rsrc(p.state_dot_a + base, static_cast<uint32_t>(ntok) * row_bytes * 2);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = 4 * g + j;
-      const bool on = t >= rows.lo && t < rows.hi;
-      __builtin_amdgcn_raw_buffer_store_b32(
-          __float_as_uint(sa[j]), sda_rs,
-          on ? static_cast<uint32_t>(t) * row_bytes * 2 + 4 * (16 * w + n) : kDropOffset, 0, 0);
-    }
+    out.y = u32x2{pack2<T>(p.scale * yt[0], p.scale * yt[1]),
+                  pack2<T>(p.scale * yt[2], p.scale * yt[3])};
+    out.sa = sa;
+    out.t0 = t0;
+    out.ntok = ntok;
+    out.lo = rows.lo;
+    out.hi = rows.hi;
+    out.on = rows.on;
   }
   const i16x8 sav = cat(sa_op, v_op);
 #pragma unroll
@@ -837,7 +862,8 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_bwd_kernel(TrainParams p) 
         prepared = false;
         if (fwd) {
           piece_intra(sm);
-          piece_forward_state<T, false>(sm, S, rows, p, head, t0, ntok);
+          PieceOut unused;
+          piece_forward_state<T, false>(sm, S, rows, p, t0, ntok, unused);
           ++q;
           continue;
         }
@@ -893,15 +919,24 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_fwd_kernel(TrainParams p) 
 #pragma unroll
     for (int kb = 0; kb < kPD / 16; ++kb) S.x[kb] = zero4();
   }
+  // The initial state has landed before the piece loop: otherwise the
+  // compiler keeps a wait for it (vmcnt(31), counting every store in flight
+  // too) in front of each of the loop's state stores.
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 
   int c_begin, c_end;
   chunk_range(p, seq, c_begin, c_end);
   bool range_ok = true;
   PieceRows rows;
   // The rows of the next piece to compute are loaded while the current one
-  // is computed (have: L holds the piece at t0).
+  // is computed (have: L holds the piece at t0). A pass's outputs are stored
+  // at the start of the next piece, after its wait for those rows: on gfx9
+  // that wait (vmcnt) also waits for every store issued before it, and these
+  // then have had a whole piece to complete.
   PieceLoad L;
   bool have = false;
+  PieceOut held;
+  bool pending = false;
   for (int c = c_begin; c < c_end; ++c) {
     const Chunk ch = chunk_at<kPD>(p, seq, head, c);
     if (!chunk_ok(ch, p.total_tokens)) {
@@ -914,14 +949,18 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_fwd_kernel(TrainParams p) 
     for (int pj = 0; pj < pieces; ++pj) {
       const int32_t t0 = ch.start + kPiece * pj;
       const int ntok = min(kPiece, ch.end - t0);
+      const bool stop = ntok <= 0 || (kFill && t0 + kPiece >= ch.end);
+      if (!stop && !have) piece_load<T, false>(L, p, head, t0, ntok);
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      if (pending) store_piece_out<T>(held, p, head);
+      pending = false;
       if (pj == 0 && !kFill && p.ckpt != nullptr) store_slab16(p.ckpt + ch.ckpt_off, S);
       if (pj > 0 && p.interior != nullptr) {
         store_slab16(p.interior + (static_cast<int64_t>(t0 / kPiece) * p.num_heads + head) *
                                       static_cast<int64_t>(kPD) * kPD,
                      S);
       }
-      if (ntok <= 0 || (kFill && t0 + kPiece >= ch.end)) break;
-      if (!have) piece_load<T, false>(L, p, head, t0, ntok);
+      if (stop) break;
       piece_stage<T, M, false>(sm, rows, L, p, bias, 0, ntok);
       bool ok = true;
 #pragma unroll
@@ -929,7 +968,8 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_fwd_kernel(TrainParams p) 
       ok = __builtin_amdgcn_readfirstlane(ok ? 1 : 0) != 0;
 
       // The next piece that computes: the chunk's next piece, else the next
-      // chunk's first (only once its range is checked).
+      // chunk's first (only once its range is checked). Its rows go to L,
+      // which the stage above consumed.
       int32_t t0n = 0;
       int ntokn = 0;
       if (pj + 1 < pieces) {
@@ -942,27 +982,32 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_fwd_kernel(TrainParams p) 
           ntokn = min(kPiece, chn.end - chn.start);
         }
       }
-      PieceLoad Ln;
       have = ntokn > 0;
-      if (have) piece_load<T, false>(Ln, p, head, t0n, ntokn);
+      if (have) piece_load<T, false>(L, p, head, t0n, ntokn);
 
-      // One pass over [0, ntok), or under strong decay 4-token sub-pieces in
-      // order, each continuing from the state the one before it left.
-      int sub = 0;
-      bool staged = ok;
-      for (;;) {
-        const int lo = ok ? 0 : 4 * sub;
-        const int hi = ok ? ntok : min(lo + 4, ntok);
-        if (!staged) piece_stage<T, M, false>(sm, rows, L, p, bias, lo, hi);
-        staged = false;
+      if (ok) {
+        // One pass over [0, ntok); its outputs are stored with the next piece.
         piece_intra(sm);
-        piece_forward_state<T, !kFill>(sm, S, rows, p, head, t0, ntok);
-        if (hi >= ntok) break;
-        ++sub;
+        piece_forward_state<T, !kFill>(sm, S, rows, p, t0, ntok, held);
+        pending = !kFill && p.out != nullptr;
+      } else {
+        // Strong decay: 4-token sub-pieces in order, each continuing from the
+        // state the one before it left, on rows loaded again (L holds the
+        // next piece); outputs stored right away.
+        for (int sub = 0; 4 * sub < ntok; ++sub) {
+          const int lo = 4 * sub, hi = min(lo + 4, ntok);
+          PieceLoad Ls;
+          piece_load<T, false>(Ls, p, head, t0, ntok);
+          piece_stage<T, M, false>(sm, rows, Ls, p, bias, lo, hi);
+          piece_intra(sm);
+          PieceOut o;
+          piece_forward_state<T, !kFill>(sm, S, rows, p, t0, ntok, o);
+          if (!kFill && p.out != nullptr) store_piece_out<T>(o, p, head);
+        }
       }
-      if (have) L = Ln;
     }
   }
+  if (pending) store_piece_out<T>(held, p, head);
 
   if (p.state != nullptr && !kFill) {
     if (!range_ok) {
