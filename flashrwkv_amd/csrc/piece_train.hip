@@ -274,8 +274,6 @@ __device__ __forceinline__ void piece_prepare(PieceSmem& sm, PieceRows& rows,
 // (16 tokens x 2 chunks per wave) fall on distinct bank pairs. Tokens past
 // the piece read as zeros (out of the buffer range).
 constexpr int kStageTensors = 7;
-// s_waitcnt vmcnt(0), expcnt and lgkmcnt left at their maxima.
-constexpr int kWaitVmcnt0 = 0x0f70;
 struct RowStage {
   uint16_t x[kStageTensors][kPiece * kPD];
 };
@@ -758,6 +756,7 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_bwd_kernel(TrainParams p) 
   Slab dS;
   if (p.dstate_final != nullptr) {
     load_slab16(dS, p.dstate_final + unit_state);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   } else {
 #pragma unroll
     for (int kb = 0; kb < kPD / 16; ++kb) dS.x[kb] = zero4();
@@ -919,9 +918,7 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_fwd_kernel(TrainParams p) 
 #pragma unroll
     for (int kb = 0; kb < kPD / 16; ++kb) S.x[kb] = zero4();
   }
-  // The initial state has landed before the piece loop: otherwise the
-  // compiler keeps a wait for it (vmcnt(31), counting every store in flight
-  // too) in front of each of the loop's state stores.
+  // The initial state lands before the piece loop (kWaitVmcnt0).
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 
   int c_begin, c_end;

@@ -8,7 +8,13 @@
 
 namespace frwkv {
 
-constexpr int kPiece = 16;  // tokens per piece; the interior checkpoint spacing
+constexpr int kPiece = 16;
+
+// s_waitcnt vmcnt(0), expcnt and lgkmcnt left at their maxima. A state
+// loaded before a kernel's piece loop is waited for with it before the loop:
+// otherwise the compiler keeps a wait for that load (counting every store in
+// flight too) in front of each state store inside the loop.
+constexpr int kWaitVmcnt0 = 0x0f70;  // tokens per piece; the interior checkpoint spacing
 
 struct TrainParams {
   int32_t num_heads;

@@ -315,6 +315,7 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_fwd_kernel(TrainPar
   float4 s[kRpl];
   if (p.state != nullptr) {
     load_slab<D, kRpl>(s, p.state + unit_state, row0, col);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   } else {
 #pragma unroll
     for (int j = 0; j < kRpl; ++j) s[j] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -467,6 +468,7 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_bwd_kernel(TrainPar
   float4 A[kRpl];
   if (p.dstate_final != nullptr) {
     load_slab<D, kRpl>(A, p.dstate_final + unit_state, row0, col);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   } else {
 #pragma unroll
     for (int j = 0; j < kRpl; ++j) A[j] = make_float4(0.f, 0.f, 0.f, 0.f);
