@@ -762,8 +762,9 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_bwd_kernel(TrainParams p) 
     for (int kb = 0; kb < kPD / 16; ++kb) dS.x[kb] = zero4();
   }
 
-  // Fail closed, as the per-token backward: from an unsupported chunk on
-  // (walking backwards) the unit's gradients are NaN where addressable.
+  // Fail closed, as the per-token backward: from a chunk longer than one
+  // piece without interior states on (walking backwards), the unit's
+  // gradients are NaN.
   auto nan_fill = [&](const Chunk& ch) {
     const int64_t nt = static_cast<int64_t>(ch.end - ch.start);
     void* const outs[6] = {p.dr, p.dk, p.db, p.ddecay, p.da, p.dv};
@@ -784,12 +785,11 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_bwd_kernel(TrainParams p) 
   bool have = false;
   for (int c = c_end - 1; c >= c_begin; --c) {
     const Chunk whole = chunk_at<kPD>(p, seq, head, c);
-    const bool range_ok = chunk_ok(whole, p.total_tokens);
     const int len = whole.end - whole.start;
     const int pieces = len > kPiece ? (len + kPiece - 1) / kPiece : 1;
-    if (!range_ok || (pieces > 1 && p.interior == nullptr)) failed = true;
+    if (pieces > 1 && p.interior == nullptr) failed = true;
     if (failed) {
-      if (range_ok) nan_fill(whole);
+      nan_fill(whole);
       continue;
     }
     for (int pj = pieces - 1; pj >= 0; --pj) {
@@ -813,7 +813,7 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_bwd_kernel(TrainParams p) 
         const Chunk wn = chunk_at<kPD>(p, seq, head, c - 1);
         const int lenn = wn.end - wn.start;
         const int piecesn = lenn > kPiece ? (lenn + kPiece - 1) / kPiece : 1;
-        if (chunk_ok(wn, p.total_tokens) && !(piecesn > 1 && p.interior == nullptr)) {
+        if (!(piecesn > 1 && p.interior == nullptr)) {
           t0n = wn.start + kPiece * (piecesn - 1);
           ntokn = min(kPiece, wn.end - t0n);
         }
@@ -923,7 +923,6 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_fwd_kernel(TrainParams p) 
 
   int c_begin, c_end;
   chunk_range(p, seq, c_begin, c_end);
-  bool range_ok = true;
   PieceRows rows;
   // The rows of the next piece to compute are loaded while the current one
   // is computed (have: L holds the piece at t0). A pass's outputs are stored
@@ -936,10 +935,6 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_fwd_kernel(TrainParams p) 
   bool pending = false;
   for (int c = c_begin; c < c_end; ++c) {
     const Chunk ch = chunk_at<kPD>(p, seq, head, c);
-    if (!chunk_ok(ch, p.total_tokens)) {
-      range_ok = false;
-      break;
-    }
     const int len = ch.end - ch.start;
     if (kFill && len <= kPiece) continue;
     const int pieces = len > kPiece ? (len + kPiece - 1) / kPiece : 1;
@@ -974,7 +969,7 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_fwd_kernel(TrainParams p) 
         ntokn = (kFill && t0n + kPiece >= ch.end) ? 0 : min(kPiece, ch.end - t0n);
       } else if (c + 1 < c_end) {
         const Chunk chn = chunk_at<kPD>(p, seq, head, c + 1);
-        if (chunk_ok(chn, p.total_tokens) && !(kFill && chn.end - chn.start <= kPiece)) {
+        if (!(kFill && chn.end - chn.start <= kPiece)) {
           t0n = chn.start;
           ntokn = min(kPiece, chn.end - chn.start);
         }
@@ -1006,14 +1001,7 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_fwd_kernel(TrainParams p) 
   }
   if (pending) store_piece_out<T>(held, p, head);
 
-  if (p.state != nullptr && !kFill) {
-    if (!range_ok) {
-      const float nan = __int_as_float(0x7fc00000);
-#pragma unroll
-      for (int kb = 0; kb < kPD / 16; ++kb) S.x[kb] = f32x4{nan, nan, nan, nan};
-    }
-    store_slab16(p.state + unit_state, S);
-  }
+  if (p.state != nullptr && !kFill) store_slab16(p.state + unit_state, S);
 }
 
 template <typename T, DecayMode M>

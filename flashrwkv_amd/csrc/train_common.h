@@ -100,15 +100,15 @@ __device__ __forceinline__ Chunk chunk_at(const TrainParams& p, int seq, int hea
     ch.ckpt_off = ((static_cast<int64_t>(seq) * p.num_heads + head) * (p.dense_t / kPiece) + c) *
                   static_cast<int64_t>(D) * D;
   } else {
-    ch.start = __builtin_amdgcn_readfirstlane(meta_at(p.seg_starts, c));
-    ch.end = __builtin_amdgcn_readfirstlane(meta_at(p.seg_ends, c));
+    // Clamped to the token range (an end before the start makes the chunk
+    // empty), as the head-size-64 kernels clamp their segments.
+    const int32_t start = __builtin_amdgcn_readfirstlane(meta_at(p.seg_starts, c));
+    const int32_t end = __builtin_amdgcn_readfirstlane(meta_at(p.seg_ends, c));
+    ch.start = min(max(start, 0), p.total_tokens);
+    ch.end = max(min(end, p.total_tokens), ch.start);
     ch.ckpt_off = (static_cast<int64_t>(c) * p.num_heads + head) * static_cast<int64_t>(D) * D;
   }
   return ch;
-}
-
-__device__ __forceinline__ bool chunk_ok(const Chunk& ch, int32_t total_tokens) {
-  return ch.start >= 0 && ch.end >= ch.start && ch.end <= total_tokens;
 }
 
 // The head-size-128 training forward or backward on bf16 MFMA over 16-token

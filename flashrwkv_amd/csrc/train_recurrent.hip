@@ -328,11 +328,10 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_fwd_kernel(TrainPar
   int c = c_begin;
   Chunk ch{};
   if (c < c_end) ch = chunk_at<D>(p, seq, head, c);
-  bool ok = c >= c_end || chunk_ok(ch, p.total_tokens);
   int32_t t0 = ch.start;
   Regs g{};
   int buf = 0;
-  if (c < c_end && ok) {
+  if (c < c_end) {
     const int n0 = min(kPiece, ch.end - t0);
     load_piece(g, t0, n0);
     store_piece(st[0], g, n0);
@@ -340,7 +339,7 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_fwd_kernel(TrainPar
   __syncthreads();
 
   if (p.fill_only && (c >= c_end || ch.end - ch.start <= kPiece)) return;
-  while (c < c_end && ok) {
+  while (c < c_end) {
     const int n = min(kPiece, ch.end - t0);
     const bool first = t0 == ch.start;
     if (!first && p.interior != nullptr) {
@@ -360,8 +359,7 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_fwd_kernel(TrainPar
       }
     }
     const bool has_next = c_n < c_end;
-    const bool ok_n = !has_next || chunk_ok(ch_n, p.total_tokens);
-    const int n_n = has_next && ok_n ? min(kPiece, ch_n.end - t0_n) : 0;
+    const int n_n = has_next ? min(kPiece, ch_n.end - t0_n) : 0;
     if (n_n > 0) load_piece(g, t0_n, n_n);
 
     if (first && p.ckpt != nullptr) store_slab<D, kRpl>(p.ckpt + ch.ckpt_off, s, row0, col);
@@ -397,16 +395,10 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_fwd_kernel(TrainPar
     c = c_n;
     ch = ch_n;
     t0 = t0_n;
-    ok = ok_n;
     buf ^= 1;
   }
 
   if (p.state != nullptr && !p.fill_only) {
-    if (!ok) {
-      const float nan = __int_as_float(0x7fc00000);
-#pragma unroll
-      for (int j = 0; j < kRpl; ++j) s[j] = make_float4(nan, nan, nan, nan);
-    }
     store_slab<D, kRpl>(p.state + unit_state, s, row0, col);
   }
 }
@@ -484,8 +476,8 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_bwd_kernel(TrainPar
     }
   };
 
-  // Fail closed: from an unsupported chunk on (walking backwards), the unit's
-  // gradients are NaN wherever the chunk ranges are addressable.
+  // Fail closed: from a chunk longer than one piece without interior states
+  // on (walking backwards), the unit's gradients are NaN.
   auto nan_fill = [&](const Chunk& ch) {
     const int64_t n = static_cast<int64_t>(ch.end - ch.start);
     const float4 nan4 = make_float4(nan, nan, nan, nan);
@@ -509,14 +501,13 @@ __global__ __launch_bounds__(Layout<D>::kThreads) void train_bwd_kernel(TrainPar
 
   for (int c = c_end - 1; c >= c_begin; --c) {
     const Chunk whole = chunk_at<D>(p, seq, head, c);
-    const bool range_ok = chunk_ok(whole, p.total_tokens);
     const int len = whole.end - whole.start;
     // Pieces of kPiece tokens from the chunk start; piece j > 0 starts from
     // the interior state at slot (its first token) / kPiece.
     const int pieces = len > kPiece ? (len + kPiece - 1) / kPiece : 1;
-    if (!range_ok || (pieces > 1 && p.interior == nullptr)) failed = true;
+    if (pieces > 1 && p.interior == nullptr) failed = true;
     if (failed) {
-      if (range_ok) nan_fill(whole);
+      nan_fill(whole);
       continue;
     }
    for (int pj = pieces - 1; pj >= 0; --pj) {

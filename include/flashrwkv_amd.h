@@ -202,7 +202,10 @@ int frwkv_chunk_forward(int io_dtype, int decay_mode, int pool_dtype,
 /*
  * Training (StateTune) forward with caller chunk metadata: sequence s owns
  * chunks sequence_chunk_offsets[s] .. sequence_chunk_offsets[s+1]-1, chunk c
- * covers tokens chunk_token_starts[c] .. chunk_token_ends[c]-1 (any length).
+ * covers tokens chunk_token_starts[c] .. chunk_token_ends[c]-1 (any length;
+ * a range reaching outside [0, total_tokens) is clamped to it, and an end
+ * before the start makes the chunk empty; the backward reads the metadata
+ * the same way).
  * state [B,H,D,D] fp32 holds S0 on entry and the final state on return (the
  * caller passes a copy). boundary [num_chunks,H,D,D] fp32 receives the state
  * at each chunk start; state_dot_a [total_tokens,H,D] fp32 receives

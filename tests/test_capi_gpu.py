@@ -172,6 +172,52 @@ def test_statetune_forward_and_backward():
         assert torch.equal(x, y2), name
 
 
+@pytest.mark.parametrize("head_size", (64, 128, 256))
+def test_statetune_chunk_ranges_are_clamped_to_the_tokens(head_size):
+    """Chunk metadata reaching outside [0, total_tokens) runs as its clamp to
+    that range (an end before the start: an empty chunk) at every head size:
+    outputs, boundary states, final state and gradients equal, bit for bit,
+    those of the clamped metadata."""
+    lengths = (40, 24)
+    n_tok, heads, batch, d = sum(lengths), 1, 2, head_size
+    case = workloads.make_case(lengths=lengths, heads=heads, head_size=d,
+                               dtype=torch.bfloat16, seed=71, state_std=0.1)
+    toks = [case[n].to(DEV) for n in NAMES]
+    offsets = torch.tensor([0, 4, 7], dtype=torch.int32, device=DEV)
+    # seq 0: [-7,16) [16,32) [32,40) and an empty chunk [38,30); seq 1:
+    # [40,56) [56,90) and one past the end [70,75).
+    bad = ([-7, 16, 32, 38, 40, 56, 70], [16, 32, 40, 30, 56, 90, 75])
+    good = ([0, 16, 32, 38, 40, 56, 64], [16, 32, 40, 38, 56, 64, 64])
+    gen = torch.Generator().manual_seed(72)
+    dy = torch.randn((n_tok, heads, d), generator=gen).to(torch.bfloat16).to(DEV)
+    ds = (torch.randn((batch, heads, d, d), generator=gen) * 0.01).to(DEV)
+    s0 = case["state_pool"][:batch].to(DEV)
+    results = []
+    for st, en in (bad, good):
+        starts = torch.tensor(st, dtype=torch.int32, device=DEV)
+        ends = torch.tensor(en, dtype=torch.int32, device=DEV)
+        state = s0.clone()
+        out = torch.zeros_like(toks[3])
+        boundary = torch.zeros((starts.numel(), heads, d, d), device=DEV)
+        sda = torch.zeros((n_tok, heads, d), device=DEV)
+        interior = torch.zeros(capi.statetune_interior_bytes(d, heads, n_tok) // 4, device=DEV)
+        capi.statetune_forward(*toks, sequence_chunk_offsets=offsets, chunk_token_starts=starts,
+                               chunk_token_ends=ends, state=state, output=out,
+                               boundary=boundary, state_dot_a=sda, interior=interior)
+        grads = [torch.zeros_like(t) for t in toks]
+        ds0 = torch.zeros((batch, heads, d, d), device=DEV)
+        capi.statetune_backward(*toks, sequence_chunk_offsets=offsets, chunk_token_starts=starts,
+                                chunk_token_ends=ends, boundary=boundary, grad_output=dy,
+                                grad_final_state=ds, grads=grads, grad_initial_state=ds0,
+                                interior=interior)
+        torch.cuda.synchronize()
+        results.append([out, state, boundary, sda, *grads, ds0])
+    names = ("y", "state", "boundary", "state_dot_a", *(f"d{n}" for n in NAMES), "dS0")
+    for name, x, y in zip(names, *results):
+        assert torch.isfinite(x.float()).all(), name
+        assert torch.equal(x, y), name
+
+
 def test_statetune_backward_rejects_short_workspace():
     """Without interior states and with a workspace below the stated size
     the backward returns an argument error before launching anything."""
