@@ -172,6 +172,56 @@ def test_statetune_forward_and_backward():
         assert torch.equal(x, y2), name
 
 
+@pytest.mark.parametrize("head_size", (128, 256))
+def test_large_heads_backward_without_interior_recomputes_it(head_size):
+    """Head sizes 128 and 256 with caller chunks longer than one 16-token
+    piece: a backward without the forward's interior states recomputes them
+    into its workspace (the fill-only forward) and gives the same gradients,
+    bit for bit, as the backward that reads them; both match the fp64
+    oracle."""
+    lengths = (45, 20)
+    meta = oracle.chunk_metadata(lengths, 40)
+    n_tok, heads, batch, d = sum(lengths), 1, len(lengths), head_size
+    case = workloads.make_case(lengths=lengths, heads=heads, head_size=d,
+                               dtype=torch.bfloat16, seed=81, state_std=0.1)
+    offsets, starts, ends = (torch.from_numpy(x).to(DEV) for x in meta[:3])
+    toks = [case[n].to(DEV) for n in NAMES]
+    s0 = case["state_pool"][:batch].clone()
+    state = s0.to(DEV)
+    out = torch.empty_like(toks[3])
+    boundary = torch.empty((starts.numel(), heads, d, d), device=DEV)
+    sda = torch.empty((n_tok, heads, d), device=DEV)
+    interior = torch.empty(capi.statetune_interior_bytes(d, heads, n_tok) // 4, device=DEV)
+    capi.statetune_forward(*toks, sequence_chunk_offsets=offsets, chunk_token_starts=starts,
+                           chunk_token_ends=ends, state=state, output=out, boundary=boundary,
+                           state_dot_a=sda, interior=interior)
+    gen = torch.Generator().manual_seed(82)
+    dy = torch.randn((n_tok, heads, d), generator=gen).to(torch.bfloat16)
+    ds = torch.randn((batch, heads, d, d), generator=gen) * 0.01
+    runs = []
+    for inner in (interior, None):
+        grads = [torch.empty_like(t) for t in toks]
+        ds0 = torch.empty((batch, heads, d, d), device=DEV)
+        capi.statetune_backward(*toks, sequence_chunk_offsets=offsets,
+                                chunk_token_starts=starts, chunk_token_ends=ends,
+                                boundary=boundary, grad_output=dy.to(DEV),
+                                grad_final_state=ds.to(DEV), grads=grads,
+                                grad_initial_state=ds0, interior=inner)
+        runs.append((grads, ds0))
+    torch.cuda.synchronize()
+    args = [_np(case[n]) for n in NAMES]
+    kw = dict(seg_offsets=meta[0], seg_starts=meta[1], seg_ends=meta[2],
+              state_slots=np.arange(batch, dtype=np.int32), scale=1.0)
+    ref = oracle.backward(*args, _np(s0), dy=_np(dy), dstate_final=_np(ds), **kw)
+    grads, ds0 = runs[0]
+    for name, g in zip(NAMES, grads):
+        _check(f"d{name}", g, ref["d" + name], 2e-2)
+    _check("dS0", ds0, ref["dstate0"], 2e-2)
+    for name, x, y2 in zip((*NAMES, "s0"), (*runs[0][0], runs[0][1]),
+                           (*runs[1][0], runs[1][1])):
+        assert torch.equal(x, y2), name
+
+
 @pytest.mark.parametrize("head_size", (64, 128, 256))
 def test_statetune_chunk_ranges_are_clamped_to_the_tokens(head_size):
     """Chunk metadata reaching outside [0, total_tokens) runs as its clamp to

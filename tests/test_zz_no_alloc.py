@@ -69,6 +69,7 @@ def _backward(entry, toks, meta, boundary, dy, ds, **extra):
 
 @pytest.mark.parametrize("head_size,first,second", [
     (64, ((300, 90), 160, 2), ((150,), 100, 1)),
+    (128, ((40, 9), 32, 2), ((20,), 18, 1)),
     (256, ((40, 9), 16, 2), ((20,), 8, 1)),
 ])
 def test_noalloc_backward_matches_workspace_entry_twice(head_size, first, second):
