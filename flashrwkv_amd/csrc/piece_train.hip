@@ -1,13 +1,15 @@
-// Training backward for head size 128 on bf16 MFMA, over 16-token pieces.
+// Training forward and backward for head size 128 on bf16 MFMA, over
+// 16-token pieces.
 //
-// Replaces the reference's StateTune / pretraining backward at head size 128
-// (csrc/sm90/tmix/wkv7/statetune_recurrent_fp32io16_backward.cu:317-502 and
-// pretrain_recurrent_bf16_backward.cu), which rebuilds S_{t-1} by dividing
-// by the decay token by token. Like chunk_bwd.hip it recomputes every piece
-// from a stored state instead: the head-size-128 forward (train_recurrent.hip)
-// stores the state at every chunk start and at every further 16-token piece
-// start, and this kernel walks each sequence's pieces in reverse, carrying the
-// state adjoint dS (dL/dS at the current piece end) in registers.
+// Replaces the reference's StateTune / pretraining kernels at head size 128
+// (csrc/sm90/tmix/wkv7/statetune_recurrent_fp32io16_{forward,backward}.cu,
+// backward :317-502; pretrain_recurrent_bf16_{forward,backward}.cu). The
+// reference's backward rebuilds S_{t-1} by dividing by the decay token by
+// token. Here, as in chunk_bwd.hip, every piece is recomputed from a stored
+// state: the forward stores the state at every chunk start and at every
+// further 16-token piece start (the interior slots), and the backward walks
+// each sequence's pieces in reverse, carrying the state adjoint dS (dL/dS at
+// the current piece end) in registers.
 //
 // A 16-token piece is one 16 x 16 block of the chunk algebra of chunk_fwd.hip
 // (tokens t, i in 0..15, keys k and values v in 0..127, G the cumulative log2
@@ -30,25 +32,33 @@
 // e3 = g 2^-G (dBt b + dKt k), the gradient of the log2 retention of token j
 // is dlg_j = sum_{t>=j} (e1_t + e2_t) - e2_j + sum_t e3_t + g dg; the decay
 // input's gradient is dlg / w for raw retention (clamped to [2^-20, 1], zero
-// outside) and dlg (-e^{-1/2}) sigmoid(x) (1 - sigmoid(x)) for logits.
+// outside) and dlg (-e^{-1/2}) sigmoid(x) (1 - sigmoid(x)) for logits. The
+// products with r, a, b, k use the bf16 tile values the MFMA products used,
+// so their cancellations match.
 //
 // Work decomposition: one 512-thread workgroup (8 waves, lane (g, n) with
-// g = lane / 16, n = lane % 16) per (sequence, head); per piece five phases
-// separated by barriers:
-//   prepare  thread (wave w, lane (g, n)) decodes token n, features
+// g = lane / 16, n = lane % 16) per (sequence, head), its fp32 state slab in
+// MFMA accumulators (wave w: value columns 16w .. 16w+15, all 128 keys). Per
+// piece, phases separated by barriers:
+//   stage    thread (wave w, lane (g, n)) decodes token n, features
 //            16w + 4g .. +3: the retention, a product scan over the 16
-//            tokens of its DPP row, the scaled tiles At, Rt, Bh, Kh, V, dYs
-//            ([t][k], bf16); it keeps its raw rows and decay factors in
-//            registers for the tokens phase, whose lane layout is the same;
+//            tokens of its DPP row, the scaled tiles At, Rt, Bh, Kh, V (and
+//            dYs in the backward; [t][k], bf16); it keeps the decay factors
+//            in registers for the tokens phase, whose lane layout is the same;
 //   intra    waves 0-3: Lab, Lak, Arb, Ark ([t][i] blocks), wave 0 also T;
-//   columns  wave w, value columns 16w .. 16w+15: S0 and dS tiles ([v][k]),
-//            SA, dSA, dZ (tiles SA and dZ, [t][v]), dV (stored), dS0;
-//   matrices waves 0-3: dArb, dArk, dLab, dLak; every wave meanwhile forms
-//            the products over values of the tokens phase;
-//   tokens   wave w, keys 16w .. 16w+15, lane (g, n) = keys 16w + 4g + j of
-//            token n: dRt, dAt, dBh, dKh, dBt, dKt and dg (transposed
-//            products), the chain rules, the decay gradient's suffix sums
-//            over the row's 16 tokens, and 8-byte gradient stores.
+//   forward  (forward kernel) every wave, its columns: SA, y, state_dot_a and
+//            the state update;
+//   columns  (backward) wave w, its columns: S0 and dS tiles ([v][k]), SA,
+//            dSA, dZ (tiles SA and dZ, [t][v]), dV (stored), dS0;
+//   matrices (backward) waves 0-3: dArb, dArk, dLab, dLak; every wave
+//            meanwhile forms the products over values of the tokens phase;
+//   tokens   (backward) wave w, keys 16w .. 16w+15, lane (g, n) = keys
+//            16w + 4g + j of token n: dRt, dAt, dBh, dKh, dBt, dKt and dg
+//            (transposed products), the chain rules, the decay gradient's
+//            suffix sums over the row's 16 tokens, and 8-byte gradient stores.
+// The next piece's rows are loaded while a piece computes: into registers in
+// the forward, into an LDS staging area (direct buffer-to-LDS loads) in the
+// backward, whose registers are full.
 // Strong decay: the factorisation needs the piece's decay span (-log2 of its
 // retention product) within 80; a piece above it runs as 4-token sub-pieces
 // (a 4-token span is at most 80 under the [2^-20, 1] clamp), sub-piece s
@@ -140,7 +150,7 @@ __device__ __forceinline__ float rowsum16(float x) {
   return rowsum16_step<1>(x);
 }
 
-// The thread's share of a piece, kept from the prepare to the tokens phase:
+// The thread's share of a piece, kept from the stage to the tokens phase:
 // the decay factors 2^G, 2^Gp, 2^-G of token n, features 16w + 4g .. +3, and
 // the derivative of the decay input's gradient with respect to dlg.
 struct PieceRows {
@@ -883,9 +893,8 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_bwd_kernel(TrainParams p) 
   }
 }
 
-// The head-size-128 training forward: the per-token forward's outputs and
-// checkpoints (train_recurrent.hip) from 16-token pieces. Per chunk of the
-// unit: the state at the chunk start (ckpt), at every further 16-token piece
+// The head-size-128 training forward, with the outputs and checkpoint layout
+// of the per-token kernels (train_recurrent.hip). Per chunk of the unit: the state at the chunk start (ckpt), at every further 16-token piece
 // start (interior, slot (piece start) / 16), y and state_dot_a per token, and
 // the final state. kFill: the interior replay (one chunk per unit, only the
 // interior states; chunks of at most 16 tokens are skipped and a chunk's last
