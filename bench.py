@@ -11,9 +11,9 @@ cache. The timed loop therefore rotates over 4 pool replicas (671 MB) and 8
 token sets; step i uses replica i % 4, which keeps every step's state traffic
 on HBM. The in-place single-pool rate is reported beside it.
 
-Steps are replayed from HIP graphs (the 8-step rotation captured as one
-graph, single-step graphs for a remainder), so host launch overhead is not
-on the timed path. HIP events on
+Steps are replayed from HIP graphs (64 consecutive steps, eight times the
+8-step rotation, captured as one graph, and one graph for a remainder), so
+host launch overhead is not on the timed path. HIP events on
 the launch stream bracket the timed region; the average launch duration is
 elapsed / steps.
 
@@ -365,40 +365,50 @@ def bench_decode(args, fp16_state=False):
         for i in range(8):
             step(i)
         stream.synchronize()
-        cycle = 8  # lcm(n_pools, n_tokens)
+        rotation = 8  # lcm(n_pools, n_tokens)
+        # Steps are replayed as HIP graphs of 64 consecutive steps (8 rotations)
+        # plus one graph for the remainder: graph launches then cost about
+        # 0.01 us per step instead of 0.5-0.7 us with 8-step graphs.
+        cycle = 8 * rotation
 
-        def capture(positions, pool=None):
+        def capture(count, pool=None):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream):
-                for i in positions:
+                for i in range(count):
                     step(i, pool)
             return g
 
-        def run_steps(cycle_graph, single_graphs, count):
-            for _ in range(count // cycle):
-                cycle_graph.replay()
-            for i in range(count % cycle):
-                single_graphs[i].replay()
+        def graphs(pool=None):
+            # Every graph a run replays, captured before any timing.
+            sizes = {cycle} | {n % cycle for n in (args.warmup, args.steps)} - {0}
+            return {n: capture(n, pool) for n in sorted(sizes)}
 
-        def timed(cycle_graph, single_graphs):
-            run_steps(cycle_graph, single_graphs, args.warmup)
+        def run_steps(g, count):
+            # Graph positions restart at 0 and cycle is a multiple of the
+            # rotation, so step i still uses pool i % n_pools, tokens i % 8.
+            for _ in range(count // cycle):
+                g[cycle].replay()
+            if count % cycle:
+                g[count % cycle].replay()
+
+        def timed(g):
+            run_steps(g, args.warmup)
             stream.synchronize()
             start = torch.cuda.Event(enable_timing=True)
             end = torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
             wall0 = time.perf_counter()
             start.record(stream)
-            run_steps(cycle_graph, single_graphs, args.steps)
+            run_steps(g, args.steps)
             end.record(stream)
             end.synchronize()
             torch.cuda.synchronize()
             return start.elapsed_time(end) / args.steps, time.perf_counter() - wall0
 
         # Cache-cold: step i uses pool replica i % n_pools and token set i % 8.
-        cold_ms, wall = timed(capture(range(cycle)), [capture([i]) for i in range(cycle)])
+        cold_ms, wall = timed(graphs())
         # In-place: one pool, the literal "consecutive steps" of the config.
-        inplace_ms, _ = timed(capture(range(cycle), pools[0]),
-                              [capture([i], pools[0]) for i in range(cycle)])
+        inplace_ms, _ = timed(graphs(pools[0]))
 
     nbytes = decode_bytes_per_step(batch, heads, d, state_bytes=2 if fp16_state else 4)
     achieved = nbytes / (cold_ms * 1e-3) / 1e9
@@ -408,7 +418,7 @@ def bench_decode(args, fp16_state=False):
         return {
             "workload": f"wkv7_decode_fp16_state: B=256, H=40, D=64, T=1 per step, fp16 io, "
                         f"fp16 state pool in place, decay logits, {n_pools} rotating pool "
-                        "replicas (cache-cold)",
+                        "replicas (cache-cold), HIP graphs of 64 steps",
             "ms_per_step": round(cold_ms, 6),
             "tokens_per_s": round(tok_s, 1),
             "roofline": {
@@ -439,7 +449,7 @@ def bench_decode(args, fp16_state=False):
         "config": {
             "workload": "wkv7_decode_cfg1: B=256, H=40, D=64, T=1 per step, bf16 io, "
                         "fp32 state pool in place, raw retention, 4 rotating pool "
-                        "replicas (cache-cold)",
+                        "replicas (cache-cold), HIP graphs of 64 steps",
             "batch": batch, "heads": heads, "head_size": d, "io_dtype": "bf16",
             "state_dtype": "fp32", "parallelism": "single GPU",
         },
