@@ -321,13 +321,18 @@ __device__ __forceinline__ void piece_rows_to_lds(RowStage& st, const TrainParam
       const uint32_t off = static_cast<uint32_t>(n) * row_bytes + 16 * c;
       // Written as assembly so that the compiler does not order every later
       // LDS access after these loads: the staging area is only read after
-      // the explicit vmcnt(0) wait and barrier at the next piece's start.
-      // M0 (the LDS base of the load) is not used by any other instruction
-      // of the kernel.
-      asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-                   :
-                   : "v"(off), "s"(rs), "s"(lds)
-                   : "memory");
+      // the column phase's explicit vmcnt(0) wait and the barriers after it.
+      // M0 holds the load's LDS base; the block saves and restores it, so a
+      // value the compiler keeps in M0 survives.
+      uint32_t m0_saved;
+      asm volatile(
+          "s_mov_b32 %0, m0\n\t"
+          "s_mov_b32 m0, %3\n\t"
+          "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+          "s_mov_b32 m0, %0"
+          : "=&s"(m0_saved)
+          : "v"(off), "s"(rs), "s"(lds)
+          : "memory");
     }
   }
 }
