@@ -19,7 +19,9 @@ elapsed / steps.
 
 The default run (--workload all) adds a "chunked_prefill" object measuring
 benchmark config 3 (chunked prefill, B=16, T=4096, H=32) against the bf16 MFMA
-roofline; --workload prefill makes that the headline line instead.
+roofline (--workload prefill makes that the headline line instead), and the
+other legs: fp16-state and fused decode, config 4 training, config 2, config 0,
+clampw-v3 pretraining and StateTune at head sizes 128 and 256.
 """
 
 from __future__ import annotations
@@ -1555,7 +1557,8 @@ def main():
                     ("training", lambda: bench_training(args)),
                     ("recurrent_long", lambda: bench_recurrent_long(args)),
                     ("recurrent_cfg0", lambda: bench_config0(args)),
-                    ("pretrain_clampw", lambda: bench_pretrain(args)))
+                    ("pretrain_clampw", lambda: bench_pretrain(args)),
+                    ("training_large_heads", lambda: bench_training_large(args)))
             for name, leg in legs:
                 if name == "varlen":
                     line["chunked_prefill"]["varlen"] = leg()
