@@ -404,6 +404,39 @@ def test_large_heads_long_sequence(head_size):
     _compare(out, grads, ref_out, ref_grads)
 
 
+def test_head128_full_shape_sampled_heads():
+    """The head-size-128 leg's shape (B=8, T=4096, H=32, D=128, 64-token caller
+    chunks walked as four 16-token pieces, S0 ~ N(0, 0.1)) on the MFMA piece
+    kernels; heads are independent, so the fp64 oracle checks a sample of
+    (sequence, head) pairs at the full length."""
+    batch, t_len, heads, d = 8, 4096, 32, 128
+    lengths = [t_len] * batch
+    meta = oracle.chunk_metadata(lengths, 64)
+    case = workloads.make_case(lengths=lengths, heads=heads, head_size=d,
+                               dtype=torch.bfloat16, seed=20260812, state_std=0.1)
+    out, grads, dy, ds = _run(case, meta, scale=1.0)
+    for seq, head in ((0, 0), (6, 27)):
+        print(f"case head128 full shape: seq {seq} head {head}", flush=True)
+        sl = slice(seq * t_len, (seq + 1) * t_len)
+        sub = {nm: case[nm][sl, head:head + 1] for nm in NAMES}
+        sub["state_pool"] = case["state_pool"][seq:seq + 1, head:head + 1]
+        sub_meta = oracle.chunk_metadata([t_len], 64)
+        ref_out, ref_grads = _oracle(sub, sub_meta, _np(sub["w"]), scale=1.0,
+                                     dy=dy[sl, head:head + 1],
+                                     ds=ds[seq:seq + 1, head:head + 1], batch=1)
+        y, st, bnd, sda = out
+        chunk_sl = slice(seq * (t_len // 64), (seq + 1) * (t_len // 64))
+        mine = (y[sl, head:head + 1], st[seq:seq + 1, head:head + 1],
+                bnd[chunk_sl, head:head + 1], sda[sl, head:head + 1])
+        for name, a, e in zip(("y", "final state", "boundary", "state_dot_a"), mine, ref_out):
+            _check(f"{name} seq{seq} head{head}", a, e)
+        for nm, key in (("r", "dr"), ("k", "dk"), ("v", "dv"), ("a", "da"), ("b", "db"),
+                        ("w", "dw")):
+            _check(f"d{nm} seq{seq} head{head}", grads[nm][sl, head:head + 1], ref_grads[key])
+        _check(f"dS0 seq{seq} head{head}", grads["s0"][seq:seq + 1, head:head + 1],
+               ref_grads["dstate0"])
+
+
 @pytest.mark.parametrize("lengths,chunk,hint", [((130, 64, 33), 64, 64), ((200, 50), 100, 64)])
 def test_max_chunk_len_hint_keeps_no_interior_and_changes_no_result(lengths, chunk, hint):
     """statetune_recurrent_internal(max_chunk_len=...) at or below the piece
