@@ -375,16 +375,20 @@ def test_large_heads_public_logits_fp16(head_size):
     _compare(out, grads, ref_out, ref_grads, dw_factor=w * oracle.retention_log_derivative(x))
 
 
-def test_large_heads_backward_deterministic():
-    """Head size 256 splits each (sequence, head) over four workgroups whose
-    per-key sums are added in a fixed order: repeated backward passes are
-    bitwise equal."""
-    lengths = (35,)
-    meta = oracle.chunk_metadata(lengths, 16)
-    case = workloads.make_case(lengths=lengths, heads=1, head_size=256, dtype=torch.bfloat16,
-                               seed=7, state_std=0.1)
-    _, g1, _, _ = _run(case, meta, scale=1.0)
-    _, g2, _, _ = _run(case, meta, scale=1.0)
+@pytest.mark.parametrize("head_size", (128, 256))
+def test_large_heads_backward_deterministic(head_size):
+    """Repeated forward and backward passes are bitwise equal: head size 256
+    splits each (sequence, head) over four workgroups whose per-key sums are
+    added in a fixed order; head size 128 runs one workgroup per unit, its
+    next rows staged through LDS while a piece computes."""
+    lengths = (35, 70)
+    meta = oracle.chunk_metadata(lengths, 32)
+    case = workloads.make_case(lengths=lengths, heads=2, head_size=head_size,
+                               dtype=torch.bfloat16, seed=7, state_std=0.1)
+    o1, g1, _, _ = _run(case, meta, scale=1.0)
+    o2, g2, _, _ = _run(case, meta, scale=1.0)
+    for name, a, b in zip(("y", "final state", "boundary", "state_dot_a"), o1, o2):
+        assert torch.equal(a, b), name
     for nm in (*NAMES, "s0"):
         assert torch.equal(g1[nm], g2[nm]), nm
 
