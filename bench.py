@@ -186,6 +186,83 @@ def cpu_baseline_decode(batch, heads, seconds):
     }
 
 
+def cpu_baseline_decode_fp16(batch, heads, seconds, sample=32):
+    """Times the fp16-state oracle (oracle.forward_fp16_state: fp64 arithmetic
+    with the contract's fp16 rounding points, one numpy loop per sequence, one
+    thread) on decode steps of ``sample`` sequences; sequences are independent,
+    so tokens/s does not depend on how many a step holds."""
+    import numpy as np
+    import torch
+
+    from flashrwkv_amd import workloads
+    from oracle import oracle
+
+    case = workloads.make_case(lengths=[1] * sample, heads=heads, head_size=64,
+                               dtype=torch.float16, seed=99, state_std=0.1)
+    args = [case[n].double().numpy() for n in ("r", "w", "k", "v", "a", "b")]
+    args[1] = np.random.default_rng(1).standard_normal(args[1].shape) * 3.5  # decay logits
+    pool = case["state_pool"].numpy().astype(np.float16)
+    elapsed_pool = np.arange(pool.shape[0], dtype=np.int32) * 11
+    cu = case["cu_seqlens"].numpy()
+    slots = case["state_indices"].numpy()
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        _, pool = oracle.forward_fp16_state(*args, pool, elapsed_pool, cu, slots)
+        steps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            break
+    return {
+        "value": steps * sample / elapsed,
+        "unit": "tokens/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{steps} decode steps of {sample} sequences (of B={batch}), H={heads}, D=64 "
+                  f"through the fp16-state oracle (numpy, one thread), {elapsed:.1f} s",
+    }
+
+
+def cpu_baseline_tmix_chain(batch, heads, seconds, sample=64):
+    """Times the fp64 chain oracle (oracle.tmix_fused: kk_a_gate in numpy, the
+    recurrence in the C oracle over every core, lnx_rkvres_xg in numpy) on
+    decode steps of ``sample`` sequences."""
+    import numpy as np
+
+    from oracle import oracle
+
+    cores = len(os.sched_getaffinity(0))
+    rng = np.random.default_rng(3)
+    d = 64
+    shape = (sample, heads, d)
+    r, k, v, a12 = (rng.standard_normal(shape) for _ in range(4))
+    w = np.exp(-np.exp(rng.uniform(-5.0, 0.0, shape)))
+    g = 1.0 / (1.0 + np.exp(-rng.standard_normal(shape)))
+    vec = lambda: rng.standard_normal(heads * d) * 0.1
+    k_k, a0, k_a, r_k, ln_w, ln_b = vec(), vec(), vec(), vec(), 1.0 + vec(), vec()
+    pool = rng.standard_normal((sample, heads, d, d)) * 0.1
+    cu = np.arange(sample + 1, dtype=np.int32)
+    slots = np.arange(sample, dtype=np.int32)
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        _, pool = oracle.tmix_fused(r, w, k, v, a12, g, k_k, a0, k_a, r_k, ln_w, ln_b, pool,
+                                    cu, slots)
+        steps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            break
+    return {
+        "value": steps * sample / elapsed,
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{steps} decode steps of {sample} sequences (of B={batch}), H={heads}, D=64 "
+                  f"through the fp64 chain oracle (gates in numpy, the recurrence in the C "
+                  f"oracle with OpenMP over (sequence, head)), {elapsed:.1f} s",
+    }
+
+
 def cpu_baseline_torch(lengths, heads, seconds, *, seed=97, u_low=-5.0, heads_total=None,
                        backward=False, dtype=None):
     """The torch fp32 restatement of the naive recurrence (oracle.forward_torch)
@@ -434,6 +511,8 @@ def bench_decode(args, fp16_state=False):
                 "tokens_per_s": round(batch / (inplace_ms * 1e-3), 1),
                 "achieved_GBps": round(nbytes / (inplace_ms * 1e-3) / 1e9, 1),
             },
+            **({"cpu_baseline": cpu_baseline_decode_fp16(batch, heads, args.cpu_seconds / 2)}
+               if args.cpu_seconds > 0 else {}),
         }
     line = {
         "metric": METRIC,
@@ -636,6 +715,8 @@ def bench_decode_fused(args):
                                "tokens_per_s": round(batch / (chain_ms * 1e-3), 1),
                                "algorithmic_bytes_per_step": chain_bytes},
         "speedup": round(chain_ms / fused_ms, 3),
+        **({"cpu_baseline": cpu_baseline_tmix_chain(batch, heads, args.cpu_seconds / 2)}
+           if args.cpu_seconds > 0 else {}),
     }
 
 
@@ -932,9 +1013,11 @@ def bench_training(args):
     return out
 
 
-def cpu_baseline_training(t_len, heads_total, seconds):
+def cpu_baseline_training(t_len, heads_total, seconds, head_size=64):
     """fp64 C oracle forward + adjoint on a bounded sample of whole (sequence,
-    head) recurrences (heads are independent, so the rate scales exactly)."""
+    head) recurrences (heads are independent, so the rate scales exactly; the
+    per-token work does not depend on the sequence length, so a shorter
+    sample sequence measures the same rate)."""
     import numpy as np
     import torch
 
@@ -943,7 +1026,7 @@ def cpu_baseline_training(t_len, heads_total, seconds):
 
     cores = len(os.sched_getaffinity(0))
     sample_heads = max(1, cores)
-    case = workloads.make_case(lengths=[t_len], heads=sample_heads, head_size=64,
+    case = workloads.make_case(lengths=[t_len], heads=sample_heads, head_size=head_size,
                                dtype=torch.bfloat16, seed=97, state_std=0.1)
     args = [case[n].double().numpy() for n in ("r", "w", "k", "v", "a", "b")]
     s0 = case["state_pool"].double().numpy()
@@ -966,9 +1049,9 @@ def cpu_baseline_training(t_len, heads_total, seconds):
         "unit": "train tokens/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"{reps} x (1 sequence x {sample_heads} heads x T={t_len}) forward + adjoint "
-                  f"through the fp64 C oracle, OpenMP over heads, {elapsed:.1f} s; "
-                  f"token-heads/s divided by H={heads_total}",
+        "sample": f"{reps} x (1 sequence x {sample_heads} heads x T={t_len}, D={head_size}) "
+                  f"forward + adjoint through the fp64 C oracle, OpenMP over heads, "
+                  f"{elapsed:.1f} s; token-heads/s divided by H={heads_total}",
     }
 
 
@@ -1025,6 +1108,9 @@ def bench_training_large(args):
                                     f"retention, 64-token caller chunks",
                         "steps": steps, "ms_per_step": round(ms, 3),
                         "train_tokens_per_s": round(n_tok / (ms * 1e-3), 1)}
+        if args.cpu_seconds > 0:
+            out[f"d{d}"]["cpu_baseline"] = cpu_baseline_training(
+                512, heads, args.cpu_seconds / 4, head_size=d)
         del tok, leaves, s0, dy, ds
         torch.cuda.empty_cache()
     return out
