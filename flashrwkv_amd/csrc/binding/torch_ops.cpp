@@ -524,8 +524,10 @@ Tensor chunk_forward_internal(Tensor r, Tensor decay, Tensor k, Tensor v, Tensor
 
 // ------------------------------------------------------------ statetune ---
 
-// The interior-state buffer of the training ops: [ceil(N/P), H, D, D] fp32
-// (P = 64 at head size 64, else 16), or none.
+// The interior-state buffer of the training ops, or none: a float32 tensor of
+// at least frwkv_statetune_interior_bytes bytes, opaque storage
+// ([ceil(N/P), H, D, D] fp32 with P = 64 at head size 64, else 16; bf16 states
+// at head size 128).
 float* checked_interior(const std::optional<Tensor>& interior, const Tensor& r, int64_t d) {
   if (!interior.has_value() || !interior->defined()) return nullptr;
   check_device_contiguous(*interior, "interior");

@@ -1262,7 +1262,9 @@ extern "C" size_t frwkv_statetune_interior_bytes(int32_t head_size, int32_t num_
   if (num_heads <= 0 || total_tokens <= 0) return 0;
   const int64_t piece = head_size == 64 ? 64 : 16;
   const int64_t slots = (total_tokens + piece - 1) / piece;
-  return static_cast<size_t>(slots * num_heads * head_size * head_size * 4);
+  // Head size 128 keeps the states in bf16 (the piece kernels' own order).
+  const int64_t bytes = head_size == 128 ? 2 : 4;
+  return static_cast<size_t>(slots * num_heads * head_size * head_size * bytes);
 }
 
 extern "C" int frwkv_statetune_interior(int io_dtype, int decay_mode, int32_t num_heads,

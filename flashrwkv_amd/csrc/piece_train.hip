@@ -6,8 +6,8 @@
 // backward :317-502; pretrain_recurrent_bf16_{forward,backward}.cu). The
 // reference's backward rebuilds S_{t-1} by dividing by the decay token by
 // token. Here, as in chunk_bwd.hip, every piece is recomputed from a stored
-// state: the forward stores the state at every chunk start and at every
-// further 16-token piece start (the interior slots), and the backward walks
+// state: the forward stores the state at every chunk start (fp32) and at
+// every further 16-token piece start (the interior slots, bf16), and the backward walks
 // each sequence's pieces in reverse, carrying the state adjoint dS (dL/dS at
 // the current piece end) in registers.
 //
@@ -441,6 +441,47 @@ __device__ __forceinline__ void store_slab16(float* base, const Slab& s) {
   }
 }
 
+// Interior piece-start states (slot = piece start / 16) are kept in bf16 in
+// the slab's lane order: thread i = 64w + lane holds S[kb][j] for kb < 8,
+// j < 4; kb pair (2q, 2q + 1) goes to the 16 bytes at (q * 512 + i) * 16 of
+// the (slot, head) block as the bf16 pairs (j0 j1)(j2 j3) of 2q, then of
+// 2q + 1. Every wave store and load is one contiguous KiB. The backward uses
+// a piece's start state only as bf16 MFMA operands (rounded to nearest even,
+// as here), so the rounding changes none of its results; a strong-decay
+// piece, whose sub-piece states are recomputed in fp32, starts from the
+// rounded state.
+constexpr int64_t kInteriorBlock = static_cast<int64_t>(kPD) * kPD;  // bf16 per (slot, head)
+
+__device__ __forceinline__ uint16_t* interior_block(const TrainParams& p, int head, int32_t t0) {
+  return reinterpret_cast<uint16_t*>(p.interior) +
+         (static_cast<int64_t>(t0 / kPiece) * p.num_heads + head) * kInteriorBlock;
+}
+
+__device__ __forceinline__ void store_slab_bf16(uint16_t* base, const Slab& s) {
+  const uint32_t off = static_cast<uint32_t>(lane_tid()) * 16;
+  const auto rs = buffer_rsrc(base, kPD * kPD * 2);
+#pragma unroll
+  for (int q = 0; q < kPD / 32; ++q) {
+    const f32x4 a = s.x[2 * q], b = s.x[2 * q + 1];
+    const u32x4 v = {pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]),
+                     pack_bf16x2(b[2], b[3])};
+    __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, q * kPThreads * 16, 0);
+  }
+}
+
+__device__ __forceinline__ void load_slab_bf16(Slab& s, const uint16_t* base) {
+  const uint32_t off = static_cast<uint32_t>(lane_tid()) * 16;
+  const auto rs = buffer_rsrc(base, kPD * kPD * 2);
+#pragma unroll
+  for (int q = 0; q < kPD / 32; ++q) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, q * kPThreads * 16, 0);
+    s.x[2 * q] = f32x4{__uint_as_float(v[0] << 16), __uint_as_float(v[0] & 0xffff0000u),
+                       __uint_as_float(v[1] << 16), __uint_as_float(v[1] & 0xffff0000u)};
+    s.x[2 * q + 1] = f32x4{__uint_as_float(v[2] << 16), __uint_as_float(v[2] & 0xffff0000u),
+                           __uint_as_float(v[3] << 16), __uint_as_float(v[3] & 0xffff0000u)};
+  }
+}
+
 __device__ __forceinline__ i16x8 lo32(i16x4 x) {
   const i16x4 z = {0, 0, 0, 0};
   return cat(x, z);
@@ -811,10 +852,14 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_bwd_kernel(TrainParams p) 
       const int32_t t0 = whole.start + kPiece * pj;
       const int ntok = min(kPiece, whole.end - t0);
       if (ntok <= 0) continue;
-      const float* ck =
-          pj == 0 ? p.ckpt + whole.ckpt_off
-                  : p.interior + (static_cast<int64_t>(t0 / kPiece) * p.num_heads + head) *
-                                     static_cast<int64_t>(kPD) * kPD;
+      // The piece's start state: the chunk's (fp32) or an interior one (bf16).
+      auto load_start = [&](Slab& S) {
+        if (pj == 0) {
+          load_slab16(S, p.ckpt + whole.ckpt_off);
+        } else {
+          load_slab_bf16(S, interior_block(p, head, t0));
+        }
+      };
       // The next piece (walking backwards): this chunk's previous piece, else
       // the last piece of the chunk before when that chunk will not fail.
       // Found here, before the start state's loads are issued: reading the
@@ -848,7 +893,7 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_bwd_kernel(TrainParams p) 
       have = ntokn > 0;
       if (have) piece_rows_to_lds<T>(stage, p, head, t0n, ntokn);
       Slab S;
-      load_slab16(S, ck);
+      load_start(S);
       piece_stage<T, M, true>(sm, rows, L, p, bias, 0, ntok);
       bool ok = true;
 #pragma unroll
@@ -870,7 +915,7 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_bwd_kernel(TrainParams p) 
         const int lo = ok ? 0 : 4 * (fwd ? q : sub);
         const int hi = ok ? ntok : min(lo + 4, ntok);
         if (!prepared) {
-          if (!ok && q == 0 && sub != nsub - 1) load_slab16(S, ck);
+          if (!ok && q == 0 && sub != nsub - 1) load_start(S);
           piece_prepare<T, M>(sm, rows, p, bias, head, t0, ntok, lo, hi);
         }
         prepared = false;
@@ -961,11 +1006,7 @@ __global__ __launch_bounds__(kPThreads, 1) void piece_fwd_kernel(TrainParams p) 
       if (pending) store_piece_out<T>(held, p, head);
       pending = false;
       if (pj == 0 && !kFill && p.ckpt != nullptr) store_slab16(p.ckpt + ch.ckpt_off, S);
-      if (pj > 0 && p.interior != nullptr) {
-        store_slab16(p.interior + (static_cast<int64_t>(t0 / kPiece) * p.num_heads + head) *
-                                      static_cast<int64_t>(kPD) * kPD,
-                     S);
-      }
+      if (pj > 0 && p.interior != nullptr) store_slab_bf16(interior_block(p, head, t0), S);
       if (stop) break;
       piece_stage<T, M, false>(sm, rows, L, p, bias, 0, ntok);
       bool ok = true;

@@ -8,13 +8,13 @@
 
 namespace frwkv {
 
-constexpr int kPiece = 16;
+constexpr int kPiece = 16;  // tokens per piece; the interior checkpoint spacing
 
 // s_waitcnt vmcnt(0), expcnt and lgkmcnt left at their maxima. A state
 // loaded before a kernel's piece loop is waited for with it before the loop:
 // otherwise the compiler keeps a wait for that load (counting every store in
 // flight too) in front of each state store inside the loop.
-constexpr int kWaitVmcnt0 = 0x0f70;  // tokens per piece; the interior checkpoint spacing
+constexpr int kWaitVmcnt0 = 0x0f70;
 
 struct TrainParams {
   int32_t num_heads;
@@ -55,7 +55,8 @@ struct TrainParams {
   // [ceil(N/16), H, D, D] or null: the state at every 16-token piece start
   // inside a chunk (not at the chunk start), at slot (piece start) / 16;
   // interior starts of different chunks lie more than 16 tokens apart, so the
-  // slots are distinct. Written by the forward, read by the backward.
+  // slots are distinct. Written by the forward, read by the backward. fp32 at
+  // head size 256; bf16 in the piece kernels' lane order at 128.
   float* interior;
   // Forward only: 1 = one chunk per unit (seg_offsets null; chunk c starts from
   // state[c]), only the interior states are written; chunks of at most 16
@@ -112,8 +113,8 @@ __device__ __forceinline__ Chunk chunk_at(const TrainParams& p, int seq, int hea
 }
 
 // The head-size-128 training forward or backward on bf16 MFMA over 16-token
-// pieces (piece_train.hip). Same parameters, outputs and checkpoint layout as
-// the per-token kernels at head size 128 (one workgroup per unit).
+// pieces (piece_train.hip). Same parameters, outputs and chunk-start states as
+// the per-token kernels (one workgroup per unit); interior states in bf16.
 int launch_piece_train(const TrainParams& p, int io_dtype, int decay_mode, int units,
                        bool backward, hipStream_t stream);
 

@@ -89,13 +89,18 @@ def _piece_len(head_size: int) -> int:
 
 def _interior(r: torch.Tensor, heads: int, d: int,
               max_chunk_len: int | None) -> torch.Tensor | None:
-    """Buffer for the interior piece-start states: ceil(N / P) slots, or None
-    when the caller states that no chunk is longer than one piece."""
+    """Buffer for the interior piece-start states: ceil(N / P) slots of
+    [D, D] fp32 (bf16 at head size 128, in the kernels' own order), as a flat
+    float32 tensor, or None when the caller states that no chunk is longer than
+    one piece."""
     p = _piece_len(d)
     if max_chunk_len is not None and max_chunk_len <= p:
         return None
     slots = (r.shape[0] + p - 1) // p
-    return torch.empty((slots, heads, d, d), device=r.device, dtype=torch.float32)
+    elems = slots * heads * d * d
+    if d == 128:
+        elems //= 2
+    return torch.empty((elems,), device=r.device, dtype=torch.float32)
 
 
 class _StateTune(torch.autograd.Function):

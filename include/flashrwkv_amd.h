@@ -214,7 +214,10 @@ int frwkv_chunk_forward(int io_dtype, int decay_mode, int pool_dtype,
  * length P is 64 tokens for head size 64 and 16 for 128 and 256; it holds
  * frwkv_statetune_interior_bytes, and only the slots of chunks longer than P
  * are written. Interior piece starts of different chunks lie more than P
- * tokens apart, so the slots never collide.
+ * tokens apart, so the slots never collide. The buffer is opaque to the
+ * caller: [D,D] fp32 per (slot, head) at head sizes 64 and 256; at 128 the
+ * states rounded to bf16 in the kernels' own element order (the backward
+ * uses a piece's start state only as bf16 MFMA operands).
  * Replaces statetune_recurrent_fp32io16_forward_cuda
  * (csrc/sm90/tmix/wkv7/statetune_recurrent_fp32io16_forward.cu:32-224;
  * binding statetune_recurrent_fp32io16_forward.cpp:26-56). head_size 64
@@ -234,7 +237,8 @@ int frwkv_statetune_forward(int io_dtype, int decay_mode, int32_t num_sequences,
                             float* interior, float scale, void* stream);
 
 /* Bytes of the interior-state buffer of frwkv_statetune_forward /
- * frwkv_statetune_backward: ceil(total_tokens / P) x H x D x D fp32. */
+ * frwkv_statetune_backward: ceil(total_tokens / P) x H x D x D elements of
+ * 4 bytes (fp32; 2 bytes, bf16, at head size 128). */
 size_t frwkv_statetune_interior_bytes(int32_t head_size, int32_t num_heads,
                                       int32_t total_tokens);
 

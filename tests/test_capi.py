@@ -178,6 +178,21 @@ def test_library_imports_no_allocating_or_synchronizing_hip_call():
     assert "hipLaunchKernel" in imported
 
 
+@pytest.mark.parametrize("head_size,piece,elem", [(64, 64, 4), (128, 16, 2), (256, 16, 4)])
+def test_interior_bytes_per_head_size(head_size, piece, elem):
+    """The interior-state buffer holds ceil(N / P) slots of H x D x D states:
+    fp32 at head sizes 64 and 256, bf16 at 128 (the piece kernels' layout);
+    a backward without it needs that much workspace beside its slices."""
+    from flashrwkv_amd import capi
+
+    for heads, n_tok in ((1, 1), (3, 130), (32, 4096)):
+        want = -(-n_tok // piece) * heads * head_size * head_size * elem
+        assert capi.statetune_interior_bytes(head_size, heads, n_tok) == want
+        assert (capi.statetune_backward_workspace_bytes(head_size, heads, n_tok, False)
+                - capi.statetune_backward_workspace_bytes(head_size, heads, n_tok, True)) == want
+    assert capi.statetune_interior_bytes(head_size, 0, 16) == 0
+
+
 def test_noalloc_backward_rejects_oversized_need_without_a_gpu():
     """frwkv_statetune_backward_noalloc compares the workspace it needs with
     its static scratch before anything else: head size 256 with 4096 tokens
